@@ -1,0 +1,737 @@
+// MI355X (gfx950 / CDNA4) int4 GEMV library: kernels and the C-ABI.
+//
+// What is computed is the reference kernel/q4gemv.c on x86, bit for bit:
+//   prologue (kernel/q4gemv.c:242-272): xsum[g] sequential fp32 sum of each
+//     group, xscale = amax/32767 (1 if amax == 0), inv = 1/xscale,
+//     xq[i] = (int16)(x*inv +- 0.5) truncated;
+//   per row o (kernel/q4gemv.c:158-183):
+//     acc = 0; for g ascending:
+//       idot = sum_{i in g} q[o][i]*xq[i]            (exact int32)
+//       acc  = acc + fma(scale, xscale*(float)idot, bias*xsum[g])
+// The integer part is order-free, so it is computed wide across lanes; only
+// the per-row chain over groups keeps the reference order, and it is run with
+// one lane per row after a transpose through LDS.
+//
+// Kernel layout (decode is an HBM stream of packed weights):
+//   * a chunk is 256 consecutive words (2048 values) of one row; lane l of a
+//     wave loads words [4l, 4l+4) of the chunk as one 128-bit load, so one
+//     wave-load instruction moves 1 KiB of one row, fully coalesced;
+//   * x is pre-split once per call into int8 high and uint8 low planes laid
+//     out to match the nibble split of a weight word (w & 0x0F0F0F0F gives
+//     the even values, (w >> 4) & 0x0F0F0F0F the odd ones), so a word costs
+//     two bit ops and four v_dot4 (sdot4 on the high plane, udot4 on the low);
+//     each wave keeps its chunk's x planes in registers and reuses them
+//     across every row of the workgroup's row tile;
+//   * the lanes of one group combine their partial integer dots with DPP,
+//     the group's leader lane forms the fp32 term and writes it to an LDS
+//     table T[m][row][group]; after a barrier one lane per (m, row) adds the
+//     row's terms in ascending group order.
+//
+// Everything is compiled with -ffp-contract=off: the only fused multiply-adds
+// are the explicit fmaf calls that mirror the reference's own contractions.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "q4gemv.h"
+
+namespace {
+
+constexpr int kChunkWords = 256;   // words per wave chunk: 64 lanes x 4 words
+constexpr int kMaxM = 8;           // activation rows per main-kernel launch
+constexpr int kLdsBudget = 64 * 1024;
+
+// ---------------------------------------------------------------- helpers --
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// x86 cvttss2si followed by a 16-bit truncation: values outside the int32
+// range (and NaN) give 0x80000000, whose low half is 0.
+__device__ __forceinline__ int32_t to_i16_like_x86(float r) {
+    int32_t v = (r > -2147483648.0f && r < 2147483648.0f) ? static_cast<int32_t>(r)
+                                                           : static_cast<int32_t>(0x80000000u);
+    return static_cast<int16_t>(v);
+}
+
+// Sum of an int over the `lpg` consecutive lanes of a group (lpg a power of
+// two, 1..64).  Every lane of the wave must execute it.
+__device__ __forceinline__ int group_sum(int v, int lpg) {
+    if (lpg >= 2) v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    if (lpg >= 4) v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+    if (lpg >= 8) v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    if (lpg >= 16) v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false); // row_mirror
+    if (lpg >= 32) v += __shfl_xor(v, 16);
+    if (lpg >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+// --------------------------------------------------------------- prologue --
+//
+// One workgroup per activation row.  Writes, for row m:
+//   planes[m][j] = {xl even, xl odd, xh even, xh odd} bytes of word j
+//   xsum[m][g], xscale[m]
+__global__ __launch_bounds__(1024) void xprep_kernel(
+    const float* __restrict__ x, int n_in, int gs, uint4* __restrict__ planes,
+    float* __restrict__ xsum, float* __restrict__ xscale_out) {
+    const int m = blockIdx.x;
+    const float* xr = x + static_cast<size_t>(m) * n_in;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    __shared__ float red[16];
+    __shared__ float s_inv;
+
+    float amax = 0.0f;                                  // kernel/q4gemv.c:258-259
+    for (int i = tid; i < n_in; i += nt) {
+        float v = xr[i];
+        v = v < 0 ? -v : v;
+        amax = v > amax ? v : amax;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        float o = __shfl_xor(amax, off);
+        amax = o > amax ? o : amax;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+
+    const int n_groups = n_in / gs;                     // kernel/q4gemv.c:244-248
+    for (int g = tid; g < n_groups; g += nt) {
+        const float* p = xr + static_cast<size_t>(g) * gs;
+        float s = 0.0f;
+        for (int i = 0; i < gs; i++) s = __fadd_rn(s, p[i]);
+        xsum[static_cast<size_t>(m) * n_groups + g] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float a = 0.0f;
+        for (int i = 0; i < (nt >> 6); i++) a = red[i] > a ? red[i] : a;
+        const float sc = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;   // :260
+        xscale_out[m] = sc;
+        s_inv = __fdiv_rn(1.0f, sc);                                  // :261
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    const int wpr = n_in >> 3;
+    for (int j = tid; j < wpr; j += nt) {
+        uint32_t le = 0, lo = 0, he = 0, ho = 0;
+#pragma unroll
+        for (int n = 0; n < 8; n++) {
+            const float a = __fmul_rn(xr[8 * j + n], inv);             // :266
+            const float r = a < 0 ? __fsub_rn(a, 0.5f) : __fadd_rn(a, 0.5f);  // :267-268
+            const int32_t q = to_i16_like_x86(r);
+            const uint32_t xl = static_cast<uint32_t>(q) & 0xFFu;
+            const uint32_t xh = static_cast<uint32_t>(q >> 8) & 0xFFu;
+            const int sh = 8 * (n >> 1);
+            if (n & 1) { lo |= xl << sh; ho |= xh << sh; }
+            else       { le |= xl << sh; he |= xh << sh; }
+        }
+        planes[static_cast<size_t>(m) * wpr + j] = make_uint4(le, lo, he, ho);
+    }
+}
+
+// ------------------------------------------------------------ main GEMV ----
+//
+// grid.x = ceil(n_out / R); block = 64 * nwaves.  Wave w handles chunks
+// w, w + nwaves, ...; for each it loads the chunk's x planes once and runs
+// every row of the tile.  Requires gs a power of two in [64, 2048] (groups
+// never straddle a chunk) and w 16-byte aligned.
+template <int MR>
+constexpr int main_threads() { return MR <= 2 ? 1024 : (MR <= 4 ? 512 : 256); }
+
+template <int MR>
+__global__ __launch_bounds__(main_threads<MR>()) void gemv_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
+    const uint16_t* __restrict__ bi, const uint4* __restrict__ planes,
+    const float* __restrict__ xsum, const float* __restrict__ xscale,
+    float* __restrict__ out, int n_out, int n_in, int gs, int R, int Gp) {
+    extern __shared__ float T[];                 // [MR][R][Gp]
+    const int wpr = n_in >> 3, n_groups = n_in / gs;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+    const int row0 = blockIdx.x * R;
+    const int n_chunks = (wpr + kChunkWords - 1) / kChunkWords;
+    const int wpg = gs >> 3;                     // words per group
+    const int lpg = gs >> 5;                     // lanes per group
+
+    for (int c = wave; c < n_chunks; c += nwaves) {
+        const int word0 = c * kChunkWords + lane * 4;
+        const bool active = word0 < wpr;
+        const int g = word0 / wpg;
+        const bool leader = active && (lane & (lpg - 1)) == 0;
+
+        uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
+        float xs[MR], xsc[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                uint4 p = active ? planes[static_cast<size_t>(m) * wpr + word0 + t]
+                                 : make_uint4(0, 0, 0, 0);
+                xle[m][t] = p.x; xlo[m][t] = p.y; xhe[m][t] = p.z; xho[m][t] = p.w;
+            }
+            xs[m] = leader ? xsum[static_cast<size_t>(m) * n_groups + g] : 0.0f;
+            xsc[m] = xscale[m];
+        }
+
+        for (int r = 0; r < R; r += 4) {
+            uint4 wv[4];
+            uint16_t s16[4], b16[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int o = row0 + r + u;
+                const bool valid = active && (r + u < R) && o < n_out;
+                wv[u] = valid ? *reinterpret_cast<const uint4*>(w + static_cast<size_t>(o) * wpr + word0)
+                              : make_uint4(0, 0, 0, 0);
+                const size_t si = static_cast<size_t>(valid ? o : 0) * n_groups + g;
+                s16[u] = (valid && leader) ? sc[si] : uint16_t(0);
+                b16[u] = (valid && leader) ? bi[si] : uint16_t(0);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t wd[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+                uint32_t lo4[4], hi4[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    lo4[t] = wd[t] & 0x0F0F0F0Fu;          // values 8j+0,2,4,6
+                    hi4[t] = (wd[t] >> 4) & 0x0F0F0F0Fu;   // values 8j+1,3,5,7
+                }
+                int part[MR];
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    int ah = 0;
+                    uint32_t al = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        ah = __builtin_amdgcn_sdot4(static_cast<int>(lo4[t]), static_cast<int>(xhe[m][t]), ah, false);
+                        ah = __builtin_amdgcn_sdot4(static_cast<int>(hi4[t]), static_cast<int>(xho[m][t]), ah, false);
+                        al = __builtin_amdgcn_udot4(lo4[t], xle[m][t], al, false);
+                        al = __builtin_amdgcn_udot4(hi4[t], xlo[m][t], al, false);
+                    }
+                    part[m] = static_cast<int>(static_cast<uint32_t>(ah) * 256u + al);
+                    part[m] = group_sum(part[m], lpg);
+                }
+                const int rr = r + u;
+                if (leader && rr < R && row0 + rr < n_out) {
+                    const float sf = h2f(s16[u]), bf = h2f(b16[u]);
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        const float dot = __fmul_rn(xsc[m], static_cast<float>(part[m]));
+                        const float bx = __fmul_rn(bf, xs[m]);
+                        T[(m * R + rr) * Gp + g] = __builtin_fmaf(sf, dot, bx);
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < MR * R; t += blockDim.x) {
+        const int m = t / R, r = t - m * R, o = row0 + r;
+        if (o < n_out) {
+            const float* p = T + static_cast<size_t>(m * R + r) * Gp;
+            float acc = 0.0f;
+            for (int g = 0; g < n_groups; g++) acc = __fadd_rn(acc, p[g]);
+            out[static_cast<size_t>(m) * n_out + o] = acc;
+        }
+    }
+}
+
+// Any gs with gs % 64 == 0 (the reference's x86 condition): one thread per
+// (m, row), scalar.  Used only for group sizes the tiled kernel does not take.
+__global__ void gemv_generic_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
+    const uint16_t* __restrict__ bi, const uint4* __restrict__ planes,
+    const float* __restrict__ xsum, const float* __restrict__ xscale,
+    float* __restrict__ out, int m_rows, int n_out, int n_in, int gs) {
+    const long t = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= static_cast<long>(m_rows) * n_out) return;
+    const int m = static_cast<int>(t / n_out), o = static_cast<int>(t % n_out);
+    const int wpr = n_in >> 3, n_groups = n_in / gs;
+    const uint32_t* row = w + static_cast<size_t>(o) * wpr;
+    const uint4* xp = planes + static_cast<size_t>(m) * wpr;
+    float acc = 0.0f;
+    for (int g = 0; g < n_groups; g++) {
+        uint32_t idot = 0;
+        for (int i = 0; i < gs; i++) {
+            const int k = g * gs + i, j = k >> 3, n = k & 7;
+            const uint32_t q = (row[j] >> (4 * n)) & 0xFu;
+            const uint4 p = xp[j];
+            const int sh = 8 * (n >> 1);
+            const uint32_t xl = ((n & 1) ? p.y : p.x) >> sh & 0xFFu;
+            const int32_t xh = static_cast<int8_t>(((n & 1) ? p.w : p.z) >> sh & 0xFFu);
+            idot += q * static_cast<uint32_t>(xh * 256 + static_cast<int32_t>(xl));
+        }
+        const size_t si = static_cast<size_t>(o) * n_groups + g;
+        const float dot = __fmul_rn(xscale[m], static_cast<float>(static_cast<int32_t>(idot)));
+        const float bx = __fmul_rn(h2f(bi[si]), xsum[static_cast<size_t>(m) * n_groups + g]);
+        acc = __fadd_rn(acc, __builtin_fmaf(h2f(sc[si]), dot, bx));
+    }
+    out[static_cast<size_t>(m) * n_out + o] = acc;
+}
+
+__global__ void fill_zero_kernel(float* __restrict__ p, long n) {
+    const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+// ---------------------------------------------------------------- dequant --
+//
+// One thread per packed word: 8 values of one row, written as two 16-byte
+// stores.  out[(o-row0)][i] = fma(q, scale, bias) (kernel/q4gemv.c:331-334).
+template <bool kBf16>
+__global__ __launch_bounds__(256) void dequant_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
+    const uint16_t* __restrict__ bi, void* __restrict__ out, int row0, int rows,
+    int n_in, int gs) {
+    const int wpr = n_in >> 3, n_groups = n_in / gs;
+    const long idx = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= static_cast<long>(rows) * wpr) return;
+    const int rr = static_cast<int>(idx / wpr), j = static_cast<int>(idx % wpr);
+    const int o = row0 + rr, g = (8 * j) / gs;
+    const uint32_t word = w[static_cast<size_t>(o) * wpr + j];
+    const size_t si = static_cast<size_t>(o) * n_groups + g;
+    const float s = h2f(sc[si]), b = h2f(bi[si]);
+    float v[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++)
+        v[n] = __builtin_fmaf(static_cast<float>((word >> (4 * n)) & 0xFu), s, b);
+    const size_t base = static_cast<size_t>(rr) * n_in + 8 * static_cast<size_t>(j);
+    if constexpr (kBf16) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            uint32_t h[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t bits = __builtin_bit_cast(uint32_t, v[2 * n + e]);
+                const bool nan = (bits & 0x7FFFFFFFu) > 0x7F800000u;
+                h[e] = nan ? ((bits >> 16) | 0x40u) : ((bits + 0x7FFFu + ((bits >> 16) & 1u)) >> 16);
+            }
+            pk[n] = h[0] | (h[1] << 16);
+        }
+        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + base) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    } else {
+        float* o4 = static_cast<float*>(out) + base;
+        *reinterpret_cast<float4*>(o4) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(o4 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// ============================================================ host side ===
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+#define HIP_TRY(expr)                                                              \
+    do {                                                                           \
+        hipError_t e_ = (expr);                                                    \
+        if (e_ != hipSuccess) {                                                    \
+            return fail(e_ == hipErrorOutOfMemory ? Q4_ENOMEM : Q4_EHIP, "%s: %s", \
+                        #expr, hipGetErrorString(e_));                             \
+        }                                                                          \
+    } while (0)
+
+bool pow2_gs(int gs) { return gs >= 64 && gs <= 2048 && (gs & (gs - 1)) == 0; }
+
+// Per-stream x workspace (prologue outputs).  Grows only; before freeing an
+// old buffer the stream is drained, since earlier launches may still read it.
+struct Workspace {
+    uint4* planes = nullptr;
+    float* xsum = nullptr;
+    float* xscale = nullptr;
+    size_t cap_words = 0, cap_groups = 0;
+};
+
+struct DevState {
+    hipStream_t stream = nullptr;               // stream of the host-pointer calls
+    std::map<hipStream_t, Workspace> ws;
+    float* pin_x = nullptr;                     // pinned staging
+    float* pin_out = nullptr;
+    size_t pin_x_cap = 0, pin_out_cap = 0;
+    float* dev_x = nullptr;
+    float* dev_out = nullptr;
+    size_t dev_x_cap = 0, dev_out_cap = 0;
+};
+
+struct Resident {
+    uint32_t* w = nullptr;
+    uint16_t* s = nullptr;
+    uint16_t* b = nullptr;
+    uint64_t fp = 0;
+};
+
+// (device, w, scales, biases, n_out, n_in, gs)
+using ResKey = std::tuple<int, const void*, const void*, const void*, int, int, int>;
+
+std::mutex g_mu;                       // serialises every host-pointer call
+std::map<int, DevState> g_dev;
+std::map<ResKey, Resident> g_res;
+
+int ensure_ws(Workspace& ws, hipStream_t st, size_t words, size_t groups) {
+    if (words <= ws.cap_words && groups <= ws.cap_groups && ws.planes) return 0;
+    HIP_TRY(hipStreamSynchronize(st));
+    hipFree(ws.planes);
+    hipFree(ws.xsum);
+    hipFree(ws.xscale);
+    ws = Workspace{};
+    size_t cw = words < 4096 ? 4096 : words, cg = groups < 1024 ? 1024 : groups;
+    HIP_TRY(hipMalloc(&ws.planes, cw * sizeof(uint4)));
+    HIP_TRY(hipMalloc(&ws.xsum, cg * sizeof(float)));
+    HIP_TRY(hipMalloc(&ws.xscale, kMaxM * sizeof(float)));
+    ws.cap_words = cw;
+    ws.cap_groups = cg;
+    return 0;
+}
+
+template <int MR>
+hipError_t launch_main(const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                       const Workspace& ws, float* out, int n_out, int n_in, int gs,
+                       hipStream_t st) {
+    const int wpr = n_in / 8, n_groups = n_in / gs;
+    const int n_chunks = (wpr + kChunkWords - 1) / kChunkWords;
+    const int max_waves = main_threads<MR>() / 64;
+    const int nwaves = n_chunks < max_waves ? n_chunks : max_waves;
+    const int Gp = n_groups | 1;                        // odd stride: no LDS bank conflicts
+    int R = n_out >= 32768 ? 16 : 4;
+    while (R > 1 && static_cast<size_t>(MR) * R * Gp * sizeof(float) > kLdsBudget) R >>= 1;
+    if (static_cast<size_t>(MR) * R * Gp * sizeof(float) > kLdsBudget) return hipErrorInvalidValue;
+    const int grid = (n_out + R - 1) / R;
+    const size_t lds = static_cast<size_t>(MR) * R * Gp * sizeof(float);
+    hipLaunchKernelGGL(gemv_kernel<MR>, dim3(grid), dim3(64 * nwaves), lds, st, w, s, b,
+                       ws.planes, ws.xsum, ws.xscale, out, n_out, n_in, gs, R, Gp);
+    return hipGetLastError();
+}
+
+// Prologue + main kernels for m (<= kMaxM) rows already on the device.
+int gemv_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
+              float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws) {
+    const int wpr = n_in / 8, n_groups = n_in / gs;
+    int rc = ensure_ws(ws, st, static_cast<size_t>(m) * wpr, static_cast<size_t>(m) * n_groups);
+    if (rc) return rc;
+    hipLaunchKernelGGL(xprep_kernel, dim3(m), dim3(1024), 0, st, x, n_in, gs, ws.planes, ws.xsum,
+                       ws.xscale);
+    HIP_TRY(hipGetLastError());
+    if (n_in == 0) {
+        // n_in == 0: every row is an empty sum (no memset: callers may capture)
+        const long n = static_cast<long>(m) * n_out;
+        hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st, out, n);
+        HIP_TRY(hipGetLastError());
+        return 0;
+    }
+    hipError_t e = hipSuccess;
+    if (!pow2_gs(gs)) {
+        const long total = static_cast<long>(m) * n_out;
+        hipLaunchKernelGGL(gemv_generic_kernel, dim3((total + 255) / 256), dim3(256), 0, st, w, s, b,
+                           ws.planes, ws.xsum, ws.xscale, out, m, n_out, n_in, gs);
+        e = hipGetLastError();
+    } else {
+        switch (m) {
+            case 1: e = launch_main<1>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            case 2: e = launch_main<2>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            case 3:
+            case 4: e = m == 4 ? launch_main<4>(w, s, b, ws, out, n_out, n_in, gs, st)
+                               : launch_main<3>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            case 5: e = launch_main<5>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            case 6: e = launch_main<6>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            case 7: e = launch_main<7>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            default: e = launch_main<8>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+        }
+    }
+    if (e != hipSuccess) return fail(Q4_EHIP, "gemv launch: %s", hipGetErrorString(e));
+    return 0;
+}
+
+int check_gemv_shape(int n_out, int n_in, int gs) {
+    if (gs <= 0 || n_in % gs || gs % 64) return fail(-1, "invalid shape n_in=%d gs=%d", n_in, gs);
+    if (n_out < 0 || n_in < 0) return fail(-1, "negative size");
+    return 0;
+}
+
+int current_device(int* dev) {
+    HIP_TRY(hipGetDevice(dev));
+    return 0;
+}
+
+int dev_state(DevState** out) {
+    int dev;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    DevState& d = g_dev[dev];
+    if (!d.stream) HIP_TRY(hipStreamCreateWithFlags(&d.stream, hipStreamNonBlocking));
+    *out = &d;
+    return 0;
+}
+
+template <typename T>
+int grow_pinned(T** p, size_t* cap, size_t n) {
+    if (n <= *cap && *p) return 0;
+    if (*p) hipHostFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    size_t c = n < 65536 ? 65536 : n;
+    HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(p), c * sizeof(T), hipHostMallocDefault));
+    *cap = c;
+    return 0;
+}
+
+template <typename T>
+int grow_dev(T** p, size_t* cap, size_t n) {
+    if (n <= *cap && *p) return 0;
+    if (*p) hipFree(*p);
+    *p = nullptr;
+    *cap = 0;
+    size_t c = n < 65536 ? 65536 : n;
+    HIP_TRY(hipMalloc(reinterpret_cast<void**>(p), c * sizeof(T)));
+    *cap = c;
+    return 0;
+}
+
+// Sampled fingerprint of the host weights: catches a matrix replaced at the
+// same address without reading all of it on every call.
+uint64_t fingerprint(const void* p, size_t bytes) {
+    const uint8_t* c = static_cast<const uint8_t*>(p);
+    uint64_t h = 1469598103934665603ull ^ bytes;
+    auto mix = [&](size_t off) {
+        uint64_t v = 0;
+        size_t n = bytes - off < 8 ? bytes - off : 8;
+        memcpy(&v, c + off, n);
+        h = (h ^ v) * 1099511628211ull;
+        h ^= h >> 29;
+    };
+    if (bytes == 0) return h;
+    const int samples = 16;
+    for (int i = 0; i < samples; i++) mix((bytes - 1) * static_cast<size_t>(i) / (samples - 1));
+    return h;
+}
+
+int resident(const uint32_t* w, const uint16_t* s, const uint16_t* b, int n_out, int n_in,
+             int gs, int dev, Resident** out) {
+    const size_t wb = static_cast<size_t>(n_out) * (n_in / 8) * 4;
+    const size_t gb = static_cast<size_t>(n_out) * (n_in / gs) * 2;
+    const uint64_t fp = fingerprint(w, wb) * 31 + fingerprint(s, gb) * 7 + fingerprint(b, gb);
+    Resident& r = g_res[ResKey{dev, w, s, b, n_out, n_in, gs}];
+    if (r.w && r.fp == fp) {
+        *out = &r;
+        return 0;
+    }
+    if (!r.w) {
+        HIP_TRY(hipMalloc(&r.w, wb ? wb : 16));
+        HIP_TRY(hipMalloc(&r.s, gb ? gb : 16));
+        HIP_TRY(hipMalloc(&r.b, gb ? gb : 16));
+    }
+    if (wb) HIP_TRY(hipMemcpy(r.w, w, wb, hipMemcpyHostToDevice));
+    if (gb) HIP_TRY(hipMemcpy(r.s, s, gb, hipMemcpyHostToDevice));
+    if (gb) HIP_TRY(hipMemcpy(r.b, b, gb, hipMemcpyHostToDevice));
+    r.fp = fp;
+    *out = &r;
+    return 0;
+}
+
+void free_resident(Resident& r) {
+    hipFree(r.w);
+    hipFree(r.s);
+    hipFree(r.b);
+}
+
+int gemv_host(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
+              float* out, int m, int n_out, int n_in, int gs) {
+    int rc = check_gemv_shape(n_out, n_in, gs);
+    if (rc) return rc;
+    if (m < 0) return fail(Q4_EARG, "m=%d", m);
+    if (n_out == 0 || m == 0) return 0;
+    if (!w || !s || !b || !x || !out) return fail(Q4_EARG, "null pointer");
+    std::lock_guard<std::mutex> lock(g_mu);
+    DevState* d;
+    if ((rc = dev_state(&d))) return rc;
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    Resident* r;
+    if ((rc = resident(w, s, b, n_out, n_in, gs, dev, &r))) return rc;
+    const size_t nx = static_cast<size_t>(m) * n_in, ny = static_cast<size_t>(m) * n_out;
+    if ((rc = grow_pinned(&d->pin_x, &d->pin_x_cap, nx))) return rc;
+    if ((rc = grow_pinned(&d->pin_out, &d->pin_out_cap, ny))) return rc;
+    if ((rc = grow_dev(&d->dev_x, &d->dev_x_cap, nx))) return rc;
+    if ((rc = grow_dev(&d->dev_out, &d->dev_out_cap, ny))) return rc;
+    memcpy(d->pin_x, x, nx * sizeof(float));
+    HIP_TRY(hipMemcpyAsync(d->dev_x, d->pin_x, nx * sizeof(float), hipMemcpyHostToDevice, d->stream));
+    Workspace& ws = d->ws[d->stream];
+    for (int m0 = 0; m0 < m; m0 += kMaxM) {
+        const int mm = m - m0 < kMaxM ? m - m0 : kMaxM;
+        rc = gemv_rows(r->w, r->s, r->b, d->dev_x + static_cast<size_t>(m0) * n_in,
+                       d->dev_out + static_cast<size_t>(m0) * n_out, mm, n_out, n_in, gs,
+                       d->stream, ws);
+        if (rc) return rc;
+    }
+    HIP_TRY(hipMemcpyAsync(d->pin_out, d->dev_out, ny * sizeof(float), hipMemcpyDeviceToHost, d->stream));
+    HIP_TRY(hipStreamSynchronize(d->stream));
+    memcpy(out, d->pin_out, ny * sizeof(float));
+    return 0;
+}
+
+int check_dequant_shape(int n_in, int gs) {
+    if (gs <= 0 || n_in % gs || gs % 8) return fail(-1, "invalid shape n_in=%d gs=%d", n_in, gs);
+    if (n_in < 0) return fail(-1, "negative size");
+    return 0;
+}
+
+template <bool kBf16>
+int dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, void* out,
+                   int row0, int rows, int n_in, int gs, hipStream_t st) {
+    const long words = static_cast<long>(rows) * (n_in / 8);
+    if (words == 0) return 0;
+    hipLaunchKernelGGL(dequant_kernel<kBf16>, dim3((words + 255) / 256), dim3(256), 0, st, w, s, b,
+                       out, row0, rows, n_in, gs);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+}  // namespace
+
+// ================================================================ C-ABI ====
+
+extern "C" {
+
+int q4_gemv(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const float* x,
+            float* out, int n_out, int n_in, int gs, int nthreads) {
+    (void)nthreads;
+    return gemv_host(w, scales, biases, x, out, 1, n_out, n_in, gs);
+}
+
+int q4_gemv_batched(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                    const float* x, float* out, int m, int n_out, int n_in, int gs, int nthreads) {
+    (void)nthreads;
+    return gemv_host(w, scales, biases, x, out, m, n_out, n_in, gs);
+}
+
+int q4_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,
+               int row0, int row1, int n_in, int gs, int nthreads) {
+    (void)nthreads;
+    int rc = check_dequant_shape(n_in, gs);
+    if (rc) return rc;
+    const int rows = row1 - row0;
+    if (rows <= 0) return 0;
+    if (row0 < 0) return fail(Q4_EARG, "row0=%d", row0);
+    if (!w || !scales || !biases || !out) return fail(Q4_EARG, "null pointer");
+    std::lock_guard<std::mutex> lock(g_mu);
+    DevState* d;
+    if ((rc = dev_state(&d))) return rc;
+    int dev;
+    if ((rc = current_device(&dev))) return rc;
+    // The reference indexes whole-matrix bases with rows [row0,row1)
+    // (kernel/q4gemv.c:372).  The caller walks a matrix block by block
+    // (hetero/cpu_model.py:129-135), so each row block is registered as its
+    // own resident matrix, keyed by the block's first-row addresses; a block
+    // that is the whole matrix shares q4_gemv's entry.
+    const size_t wpr = static_cast<size_t>(n_in / 8), ng = static_cast<size_t>(n_in / gs);
+    Resident* r;
+    if ((rc = resident(w + row0 * wpr, scales + row0 * ng, biases + row0 * ng, rows, n_in, gs, dev, &r)))
+        return rc;
+    const size_t ny = static_cast<size_t>(rows) * n_in;
+    if ((rc = grow_pinned(&d->pin_out, &d->pin_out_cap, ny))) return rc;
+    if ((rc = grow_dev(&d->dev_out, &d->dev_out_cap, ny))) return rc;
+    if ((rc = dequant_launch<false>(r->w, r->s, r->b, d->dev_out, 0, rows, n_in, gs, d->stream)))
+        return rc;
+    HIP_TRY(hipMemcpyAsync(d->pin_out, d->dev_out, ny * sizeof(float), hipMemcpyDeviceToHost, d->stream));
+    HIP_TRY(hipStreamSynchronize(d->stream));
+    memcpy(out, d->pin_out, ny * sizeof(float));
+    return 0;
+}
+
+int q4_release(const void* w) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    int n = 0;
+    for (auto it = g_res.begin(); it != g_res.end();) {
+        if (std::get<1>(it->first) == w) {
+            int cur = 0;
+            hipGetDevice(&cur);
+            hipSetDevice(std::get<0>(it->first));
+            free_resident(it->second);
+            hipSetDevice(cur);
+            it = g_res.erase(it);
+            n++;
+        } else {
+            ++it;
+        }
+    }
+    return n;
+}
+
+int q4_release_all(void) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    int n = 0, cur = 0;
+    hipGetDevice(&cur);
+    for (auto& kv : g_res) {
+        hipSetDevice(std::get<0>(kv.first));
+        free_resident(kv.second);
+        n++;
+    }
+    hipSetDevice(cur);
+    g_res.clear();
+    return n;
+}
+
+const char* q4_last_error(void) { return g_err; }
+
+int q4_gemv_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const float* x,
+                float* out, int m, int n_out, int n_in, int gs, void* stream) {
+    int rc = check_gemv_shape(n_out, n_in, gs);
+    if (rc) return rc;
+    if (m < 0) return fail(Q4_EARG, "m=%d", m);
+    if (n_out == 0 || m == 0) return 0;
+    if (!w || !scales || !biases || !x || !out) return fail(Q4_EARG, "null pointer");
+    if (reinterpret_cast<uintptr_t>(w) & 15) return fail(Q4_EARG, "w must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Workspace* ws;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        int dev;
+        if ((rc = current_device(&dev))) return rc;
+        ws = &g_dev[dev].ws[st];
+    }
+    for (int m0 = 0; m0 < m; m0 += kMaxM) {
+        const int mm = m - m0 < kMaxM ? m - m0 : kMaxM;
+        rc = gemv_rows(w, scales, biases, x + static_cast<size_t>(m0) * n_in,
+                       out + static_cast<size_t>(m0) * n_out, mm, n_out, n_in, gs, st, *ws);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+int q4_dequant_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,
+                   int row0, int row1, int n_in, int gs, void* stream) {
+    int rc = check_dequant_shape(n_in, gs);
+    if (rc) return rc;
+    if (row1 - row0 <= 0) return 0;
+    if (row0 < 0) return fail(Q4_EARG, "row0=%d", row0);
+    if (!w || !scales || !biases || !out) return fail(Q4_EARG, "null pointer");
+    if (reinterpret_cast<uintptr_t>(out) & 15) return fail(Q4_EARG, "out must be 16-byte aligned");
+    return dequant_launch<false>(w, scales, biases, out, row0, row1 - row0, n_in, gs,
+                                 static_cast<hipStream_t>(stream));
+}
+
+int q4_dequant_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                        uint16_t* out, int row0, int row1, int n_in, int gs, void* stream) {
+    int rc = check_dequant_shape(n_in, gs);
+    if (rc) return rc;
+    if (row1 - row0 <= 0) return 0;
+    if (row0 < 0) return fail(Q4_EARG, "row0=%d", row0);
+    if (!w || !scales || !biases || !out) return fail(Q4_EARG, "null pointer");
+    if (reinterpret_cast<uintptr_t>(out) & 15) return fail(Q4_EARG, "out must be 16-byte aligned");
+    return dequant_launch<true>(w, scales, biases, out, row0, row1 - row0, n_in, gs,
+                                static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

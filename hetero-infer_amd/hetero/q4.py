@@ -1,0 +1,142 @@
+"""ctypes binding of libq4gemv.so, the gfx950 int4 GEMV library.
+
+The drop-in entry points keep the reference's argument types exactly
+(hetero/cpu_model.py:41-44): q4_gemv takes [c_void_p]*5 + [c_int]*4 and
+q4_dequant [c_void_p]*4 + [c_int]*5, both returning c_int.  The additional
+entry points (batched, device-pointer, release) are declared the same way;
+their C declarations are in include/q4gemv.h.
+
+There is no fallback: if the library is missing, load() raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import numpy as np
+
+PKG_PARENT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
+
+EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
+           "q4_last_error", "q4_gemv_dev", "q4_dequant_dev", "q4_dequant_bf16_dev")
+
+Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
+
+_VP, _I = ctypes.c_void_p, ctypes.c_int
+
+
+def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
+    """Attach argtypes/restype for every symbol the library exports."""
+    lib.q4_gemv.argtypes = [_VP] * 5 + [_I] * 4
+    lib.q4_gemv.restype = _I
+    lib.q4_dequant.argtypes = [_VP] * 4 + [_I] * 5
+    lib.q4_dequant.restype = _I
+    if hasattr(lib, "q4_gemv_batched"):
+        lib.q4_gemv_batched.argtypes = [_VP] * 5 + [_I] * 5
+        lib.q4_gemv_batched.restype = _I
+        lib.q4_release.argtypes = [_VP]
+        lib.q4_release.restype = _I
+        lib.q4_release_all.argtypes = []
+        lib.q4_release_all.restype = _I
+        lib.q4_last_error.argtypes = []
+        lib.q4_last_error.restype = ctypes.c_char_p
+        lib.q4_gemv_dev.argtypes = [_VP] * 5 + [_I] * 4 + [_VP]
+        lib.q4_gemv_dev.restype = _I
+        lib.q4_dequant_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
+        lib.q4_dequant_dev.restype = _I
+        lib.q4_dequant_bf16_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
+        lib.q4_dequant_bf16_dev.restype = _I
+    return lib
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise if it is not built."""
+    global _LIB
+    if _LIB is not None and path == LIB_PATH:
+        return _LIB
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run `python hetero-infer_amd/build.py`")
+    # One HIP runtime per process.  PyTorch-ROCm ships its own libamdhip64
+    # (same SONAME, libamdhip64.so.7); if it is imported after this library
+    # has pulled in /opt/rocm's copy, torch finds no GPU.  Importing torch
+    # first makes the dynamic linker bind this library to torch's runtime.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    lib = declare(ctypes.CDLL(path))
+    if path == LIB_PATH:
+        _LIB = lib
+    return lib
+
+
+def last_error(lib: ctypes.CDLL) -> str:
+    return lib.q4_last_error().decode(errors="replace")
+
+
+def check(lib: ctypes.CDLL, rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with {rc}: {last_error(lib)}")
+
+
+# ---- device-pointer helpers over torch tensors (torch is only plumbing) ----
+
+def _ptr(t) -> int:
+    return t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+def gemv_dev(w, scales, biases, x, out=None, stream=None, lib=None):
+    """out[m, n_out] = x[m, n_in] @ W^T on the GPU (torch tensors on one device)."""
+    import torch
+    lib = lib or load()
+    n_out, n_in = w.shape[0], w.shape[1] * 8
+    gs = n_in // scales.shape[1]
+    x2 = x.reshape(-1, n_in)
+    assert x2.dtype == torch.float32 and x2.is_contiguous()
+    if out is None:
+        out = torch.empty((x2.shape[0], n_out), dtype=torch.float32, device=x.device)
+    rc = lib.q4_gemv_dev(_ptr(w), _ptr(scales), _ptr(biases), _ptr(x2), _ptr(out),
+                         x2.shape[0], n_out, n_in, gs, _stream(stream))
+    check(lib, rc, "q4_gemv_dev")
+    return out
+
+
+def dequant_dev(w, scales, biases, row0=0, row1=None, out=None, bf16=False, stream=None, lib=None):
+    import torch
+    lib = lib or load()
+    n_in = w.shape[1] * 8
+    gs = n_in // scales.shape[1]
+    row1 = w.shape[0] if row1 is None else row1
+    rows = max(row1 - row0, 0)
+    if out is None:
+        out = torch.empty((rows, n_in), dtype=torch.bfloat16 if bf16 else torch.float32,
+                          device=w.device)
+    fn = lib.q4_dequant_bf16_dev if bf16 else lib.q4_dequant_dev
+    rc = fn(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out), row0, row1, n_in, gs, _stream(stream))
+    check(lib, rc, "q4_dequant_dev")
+    return out
+
+
+# ---- host-pointer calls (the reference's ABI) over NumPy arrays ----
+
+def gemv_host(lib, w: np.ndarray, scales: np.ndarray, biases: np.ndarray, x: np.ndarray,
+              gs: int, nthreads: int = 0) -> np.ndarray:
+    n_out, n_in = w.shape[0], w.shape[1] * 8
+    xc = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(n_out, dtype=np.float32)
+    rc = lib.q4_gemv(w.ctypes.data, scales.ctypes.data, biases.ctypes.data, xc.ctypes.data,
+                     out.ctypes.data, n_out, n_in, gs, nthreads)
+    if rc != 0:
+        raise RuntimeError(f"q4_gemv failed with {rc}")
+    return out

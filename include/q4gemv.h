@@ -1,0 +1,100 @@
+/* C-ABI of the MI355X (gfx950) int4 GEMV library, libq4gemv.so.
+ *
+ * Weight layout (MLX 4-bit, the reference's kernel/q4gemv.c:7-11):
+ *   w       [n_out][n_in/8]   uint32, eight 4-bit values each, low nibble first
+ *   scales  [n_out][n_in/gs]  fp16 bit patterns
+ *   biases  [n_out][n_in/gs]  fp16 bit patterns
+ *   value = q * scale + bias
+ *
+ * Return codes: 0 success; -1 invalid shape, for exactly the conditions the
+ * reference rejects (kernel/q4gemv.c:237, :361), plus gs <= 0; Q4_EHIP a HIP
+ * runtime error (no device, launch failure); Q4_ENOMEM device or pinned
+ * memory exhausted; Q4_EARG a null pointer, a misaligned device pointer or
+ * a size the library does not take.  q4_last_error() describes the last
+ * failure of the calling thread.
+ *
+ * Results: q4_gemv reproduces the reference's x86 arithmetic bit for bit
+ * (x quantised to int16 once per call, exact integer dot per group, groups
+ * accumulated in ascending order as acc + fma(scale, xscale*dot, bias*xsum)),
+ * i.e. the reference built with ROWS=1 -- and with any ROWS when
+ * n_out % ROWS == 0.
+ */
+#ifndef HETERO_AMD_Q4GEMV_H
+#define HETERO_AMD_Q4GEMV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q4_EHIP   (-2)
+#define Q4_ENOMEM (-3)
+#define Q4_EARG   (-4)
+
+/* ---- drop-in entry points: host pointers, synchronous ------------------- */
+
+/* y = W x for one activation row.  Replaces q4_gemv of the reference,
+ * kernel/q4gemv.c:232-233, bound by hetero/cpu_model.py:41-42 as
+ * [c_void_p]*5 + [c_int]*4 -> c_int.  All pointers are host addresses.
+ * w/scales/biases are uploaded to HBM on first use and kept resident, keyed
+ * by their host addresses and shape and checked against a sampled
+ * fingerprint on every call (they must not be modified while registered;
+ * q4_release drops them).  nthreads is accepted and ignored.  Returns after
+ * out[0..n_out) is written. */
+int q4_gemv(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+            const float *x, float *out, int n_out, int n_in, int gs, int nthreads);
+
+/* Rows [row0,row1) of W expanded to fp32, out[(o-row0)*n_in + i] =
+ * fma(q, scale, bias).  Replaces q4_dequant, kernel/q4gemv.c:359-360, bound
+ * by hetero/cpu_model.py:43-44 as [c_void_p]*4 + [c_int]*5 -> c_int.
+ * w/scales/biases are whole-matrix host bases (resident as for q4_gemv);
+ * out is a host buffer of (row1-row0)*n_in floats.  Returns 0 without
+ * touching out when row1 <= row0. */
+int q4_dequant(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+               float *out, int row0, int row1, int n_in, int gs, int nthreads);
+
+/* m activation rows x[m][n_in] -> out[m][n_out], each row bit-identical to
+ * q4_gemv on that row; the weights are read once for all rows.  No
+ * counterpart in the reference: it replaces the row-by-row loop of
+ * hetero/cpu_model.py:149-153 (QLinear.__call__ for 1 < rows <= 16).  Host
+ * pointers, synchronous, same residency rules as q4_gemv. */
+int q4_gemv_batched(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                    const float *x, float *out, int m, int n_out, int n_in, int gs,
+                    int nthreads);
+
+/* Drop the HBM copies registered for host weights at address w (every
+ * shape); q4_release_all drops every registered matrix on every device.
+ * Return the number of entries released. */
+int q4_release(const void *w);
+int q4_release_all(void);
+
+/* Text of the calling thread's last failure ("" if none). */
+const char *q4_last_error(void);
+
+/* ---- device-pointer entry points: asynchronous on `stream` --------------
+ * All pointers are device addresses on the current HIP device; `stream` is a
+ * hipStream_t (NULL = the null stream).  w must be 16-byte aligned.  Calls
+ * that share a device and overlap in time must be issued on one stream: the
+ * per-stream x workspace is reused by the next call on that stream. */
+
+/* Batched GEMV over m rows (any m >= 1; rows are processed eight at a time).
+ * Same arithmetic as q4_gemv.  x is [m][n_in], out is [m][n_out]. */
+int q4_gemv_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                const float *x, float *out, int m, int n_out, int n_in, int gs,
+                void *stream);
+
+/* Device q4_dequant: rows [row0,row1) to fp32 [row1-row0][n_in]. */
+int q4_dequant_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                   float *out, int row0, int row1, int n_in, int gs, void *stream);
+
+/* Rows [row0,row1) to bf16 bit patterns [row1-row0][n_in]: the fp32 value
+ * of q4_dequant rounded to nearest even. */
+int q4_dequant_bf16_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                        uint16_t *out, int row0, int row1, int n_in, int gs, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HETERO_AMD_Q4GEMV_H */

@@ -1,0 +1,194 @@
+"""GPU parity of the HIP int4 GEMV path, called through the C-ABI.
+
+Bar: bit-exact against the golden vectors written from the reference
+kernel/q4gemv.c compiled from source (tests/golden/make_golden.py), and
+against the oracle on seeded inputs; dequantised weights bit-exact.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from hetero import q4, synth
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def assert_bit_exact(got, want, what):
+    got, want = bits(got), bits(want)
+    bad = np.nonzero(got != want)[0] if got.ndim == 1 else np.argwhere(got != want)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    assert bad.size == 0, f"{what}: {len(bad)} of {got.size} differ, first at {bad[:5].tolist()}"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return q4.load()
+
+
+@pytest.fixture(scope="module")
+def manifest():
+    with open(os.path.join(GOLDEN, "manifest.json")) as f:
+        return json.load(f)
+
+
+@pytest.fixture(scope="module")
+def small():
+    return np.load(os.path.join(GOLDEN, "golden_small.npz"))
+
+
+def gemv_cases(man):
+    return [k for k in man["cases"] if k.startswith("g_")]
+
+
+def test_small_golden_host_abi(lib, manifest, small):
+    """q4_gemv (host pointers) vs the reference on every small golden case."""
+    for name in gemv_cases(manifest):
+        p = manifest["cases"][name]["params"]
+        w, s, b, x = (small[f"{name}.{k}"] for k in ("w", "scales", "biases", "x"))
+        print(f"case {name} {p}", flush=True)
+        out = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, p["gs"])
+        ref = small[f"{name}.out_rows1"]
+        assert_bit_exact(out, ref, name)
+        if p["n_out"] % 8 == 0:
+            assert_bit_exact(out, small[f"{name}.out_rows8"], name + " rows8")
+
+
+def test_small_golden_dev_abi(lib, manifest, small):
+    """q4_gemv_dev (device pointers, torch tensors) vs the reference."""
+    import torch
+    for name in gemv_cases(manifest):
+        p = manifest["cases"][name]["params"]
+        print(f"case {name} {p}", flush=True)
+        w, s, b, x = (torch.from_numpy(np.ascontiguousarray(small[f"{name}.{k}"])).cuda()
+                      for k in ("w", "scales", "biases", "x"))
+        out = q4.gemv_dev(w, s.view(torch.int16), b.view(torch.int16), x.reshape(1, -1))
+        torch.cuda.synchronize()
+        assert_bit_exact(out.cpu().numpy()[0], small[f"{name}.out_rows1"], name)
+
+
+def test_return_codes(lib, manifest):
+    """Invalid shapes give the reference's return codes."""
+    rcs = manifest["return_codes"]
+    w, s, b = synth.qlinear(120, 4, 256, 64)
+    x = synth.activations(120, 1, 256)[0]
+    out = np.empty(4, np.float32)
+    args = (w.ctypes.data, s.ctypes.data, b.ctypes.data, x.ctypes.data, out.ctypes.data)
+    assert lib.q4_gemv(*args, 4, 256, 32, 1) == rcs["gemv_gs32"]
+    assert lib.q4_gemv(*args, 4, 200, 64, 1) == rcs["gemv_nin_not_multiple"]
+    assert lib.q4_gemv(*args, 4, 192, 96, 1) == rcs["gemv_gs96"]
+    buf = np.empty((2, 256), np.float32)
+    dargs = (w.ctypes.data, s.ctypes.data, b.ctypes.data, buf.ctypes.data)
+    assert lib.q4_dequant(*dargs, 0, 2, 256, 12, 1) == rcs["dequant_gs12"]
+    assert lib.q4_dequant(*dargs, 3, 3, 256, 64, 1) == rcs["dequant_empty"]
+    assert lib.q4_dequant(*dargs, 3, 1, 256, 64, 1) == rcs["dequant_reversed"]
+
+
+def test_dequant_golden(lib, manifest, small):
+    """q4_dequant (host ABI) bit-exact vs the reference, incl. row sub-ranges and gs=32."""
+    for name, c in manifest["cases"].items():
+        if not name.startswith("d_"):
+            continue
+        p = c["params"]
+        w, s, b = (small[f"{name}.{k}"] for k in ("w", "scales", "biases"))
+        out = np.empty((p["row1"] - p["row0"], p["n_in"]), np.float32)
+        rc = lib.q4_dequant(w.ctypes.data, s.ctypes.data, b.ctypes.data, out.ctypes.data,
+                            p["row0"], p["row1"], p["n_in"], p["gs"], 4)
+        assert rc == 0, q4.last_error(lib)
+        assert_bit_exact(out, small[f"{name}.out"], name)
+
+
+def test_dequant_dev_vs_closed_form(lib):
+    """fp32 and bf16 device dequant vs q*s+b (NumPy) on a seeded matrix."""
+    import torch
+    w, s, b = synth.qlinear(7, 96, 1024, 64)
+    ref = oracle.dequant_np(w, s, b, 64)
+    tw, ts, tb = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16)))
+    got = q4.dequant_dev(tw, ts, tb).cpu().numpy()
+    assert_bit_exact(got, ref, "dequant fp32")
+    got16 = q4.dequant_dev(tw, ts, tb, 10, 90, bf16=True).cpu()
+    want16 = torch.from_numpy(ref[10:90]).to(torch.bfloat16)
+    assert torch.equal(got16.view(torch.int16), want16.view(torch.int16))
+
+
+def test_unpack_nibbles(lib):
+    """Integer nibbles: with scale 1 and bias 0 the dequantised value is q itself."""
+    import torch
+    w, s, b = synth.qlinear(8, 16, 512, 64)
+    s[:] = np.float16(1.0)
+    b[:] = np.float16(0.0)
+    tw, ts, tb = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16)))
+    got = q4.dequant_dev(tw, ts, tb).cpu().numpy()
+    assert np.array_equal(got.astype(np.uint8), oracle.unpack_np(w))
+    assert np.array_equal(got, got.astype(np.uint8).astype(np.float32))
+
+
+@pytest.mark.parametrize("name", [n for n, _, _ in synth.QWEN7B_SHAPES] + ["config0_q_proj"])
+def test_qwen7b_shapes(lib, manifest, name):
+    """Every Qwen2.5-7B projection at M=1 (and M=8 where stored) vs the reference."""
+    import torch
+    c = manifest["qwen7b"][name]
+    print(f"shape {name} K={c['n_in']} N={c['n_out']} m={c['m']}", flush=True)
+    w, s, b = synth.qlinear(c["seed"], c["n_out"], c["n_in"], 64)
+    x = synth.activations(c["seed"], c["m"], c["n_in"])
+    assert synth.sha256(w, s, b) == c["sha256_w_s_b"], "generator drift: inputs differ"
+    assert synth.sha256(x) == c["sha256_x"]
+    want = np.load(os.path.join(GOLDEN, "golden_qwen7b.npz"))[name]
+    got = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x[0], 64)
+    assert_bit_exact(got, want[0], name + " host")
+    if c["m"] > 1:
+        out = np.empty((c["m"], c["n_out"]), np.float32)
+        rc = lib.q4_gemv_batched(w.ctypes.data, s.ctypes.data, b.ctypes.data, x.ctypes.data,
+                                 out.ctypes.data, c["m"], c["n_out"], c["n_in"], 64, 0)
+        assert rc == 0, q4.last_error(lib)
+        assert_bit_exact(out, want, name + " batched")
+        tw, ts, tb, tx = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16), x))
+        for m in (1, 2, 3, 4, 5, 8):
+            o = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
+            torch.cuda.synchronize()
+            assert_bit_exact(o.cpu().numpy(), want[:m], f"{name} dev m={m}")
+    lib.q4_release(w.ctypes.data)
+
+
+def test_zero_sizes(lib):
+    """n_out = 0 is a no-op; n_in = 0 gives zeros (empty sums)."""
+    w = np.zeros((4, 0), np.uint32)
+    s = np.zeros((4, 0), np.uint16)
+    out = np.full(4, np.nan, np.float32)
+    x = np.zeros(0, np.float32)
+    rc = lib.q4_gemv(w.ctypes.data, s.ctypes.data, s.ctypes.data, x.ctypes.data, out.ctypes.data,
+                     4, 0, 64, 1)
+    assert rc == 0, q4.last_error(lib)
+    assert np.array_equal(out, np.zeros(4, np.float32))
+    assert lib.q4_gemv(w.ctypes.data, s.ctypes.data, s.ctypes.data, x.ctypes.data,
+                       out.ctypes.data, 0, 64, 64, 1) == 0
+
+
+def test_generic_group_size(lib):
+    """gs = 192 (a multiple of 64, not a power of two) vs the oracle, bit-exact."""
+    o = oracle.Oracle()
+    w, s, b = synth.qlinear(9, 33, 192 * 5, 192)
+    x = synth.activations(9, 1, 192 * 5)[0]
+    got = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, 192)
+    assert_bit_exact(got, o.gemv(w, s, b, x, 192), "gs192")
+
+
+def test_residency_detects_replaced_weights(lib):
+    """A matrix overwritten in place at the same address is re-uploaded."""
+    o = oracle.Oracle()
+    w, s, b = synth.qlinear(10, 64, 1024, 64)
+    x = synth.activations(10, 1, 1024)[0]
+    first = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, 64)
+    assert_bit_exact(first, o.gemv(w, s, b, x, 64), "first")
+    w2, s2, b2 = synth.qlinear(11, 64, 1024, 64)
+    w[:], s[:], b[:] = w2, s2, b2
+    second = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, 64)
+    assert_bit_exact(second, o.gemv(w, s, b, x, 64), "second")
+    assert lib.q4_release(w.ctypes.data) >= 1
