@@ -75,6 +75,55 @@ __device__ __forceinline__ int group_sum(int v, int lpg) {
     return v;
 }
 
+
+// Max over the wave (NaN-skipping, like the reference's `v > amax` scan):
+// DPP within rows of 16 lanes, then the four row results through SGPRs.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float a) {
+    const int o = __builtin_amdgcn_update_dpp(__float_as_int(a), __float_as_int(a), CTRL, 0xF, 0xF, false);
+    return fmaxf(a, __int_as_float(o));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max<0xB1>(v);    // quad_perm 1,0,3,2
+    v = dpp_max<0x4E>(v);    // quad_perm 2,3,0,1
+    v = dpp_max<0x141>(v);   // row_half_mirror
+    v = dpp_max<0x140>(v);   // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// One packed word of x (8 values, MLX order) -> {xl even, xl odd, xh even,
+// xh odd} byte planes of xq = (int16)(x*inv +- 0.5) (kernel/q4gemv.c:266-268).
+// a + copysign(0.5, a) is the reference's `a < 0 ? a - 0.5 : a + 0.5` for
+// every a whose truncation is defined (the two differ only for -0.0, which
+// truncates to 0 either way).  When inv is finite |x*inv| <= 32767.5, so
+// v_cvt_i32_f32 is the x86 truncation (NaN -> 0 on both after the 16-bit
+// cut); `exact_clamp` selects the out-of-range rule for an infinite inv.
+__device__ __forceinline__ uint4 quant_word(const float (&v)[8], float inv, bool exact_clamp) {
+    int32_t q[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const float a = __fmul_rn(v[n], inv);
+        const float r = __fadd_rn(a, __builtin_copysignf(0.5f, a));
+        q[n] = exact_clamp ? to_i16_like_x86(r) : static_cast<int32_t>(r);
+    }
+    // pack (q0,q2), (q4,q6), (q1,q3), (q5,q7) as int16 pairs, then gather bytes
+    const uint32_t e0 = (static_cast<uint32_t>(q[0]) & 0xFFFFu) | (static_cast<uint32_t>(q[2]) << 16);
+    const uint32_t e1 = (static_cast<uint32_t>(q[4]) & 0xFFFFu) | (static_cast<uint32_t>(q[6]) << 16);
+    const uint32_t o0 = (static_cast<uint32_t>(q[1]) & 0xFFFFu) | (static_cast<uint32_t>(q[3]) << 16);
+    const uint32_t o1 = (static_cast<uint32_t>(q[5]) & 0xFFFFu) | (static_cast<uint32_t>(q[7]) << 16);
+    // v_perm_b32(hi, lo, sel): byte k of the result = byte sel[k] of {hi:lo}
+    const uint32_t le = __builtin_amdgcn_perm(e1, e0, 0x06040200u);   // low bytes of q0,q2,q4,q6
+    const uint32_t he = __builtin_amdgcn_perm(e1, e0, 0x07050301u);   // high bytes
+    const uint32_t lo = __builtin_amdgcn_perm(o1, o0, 0x06040200u);
+    const uint32_t ho = __builtin_amdgcn_perm(o1, o0, 0x07050301u);
+    return make_uint4(le, lo, he, ho);
+}
+
 // --------------------------------------------------------------- prologue --
 //
 // One workgroup per activation row.  Writes, for row m:
@@ -105,7 +154,13 @@ __global__ __launch_bounds__(1024) void xprep_kernel(
     for (int g = tid; g < n_groups; g += nt) {
         const float* p = xr + static_cast<size_t>(g) * gs;
         float s = 0.0f;
-        for (int i = 0; i < gs; i++) s = __fadd_rn(s, p[i]);
+        for (int base = 0; base < gs; base += 32) {   // gs % 64 == 0; 32 loads in flight
+            float v[32];
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = p[base + i];
+#pragma unroll
+            for (int i = 0; i < 32; i++) s = __fadd_rn(s, v[i]);
+        }
         xsum[static_cast<size_t>(m) * n_groups + g] = s;
     }
     __syncthreads();
@@ -274,6 +329,259 @@ __global__ void gemv_generic_kernel(
     out[static_cast<size_t>(m) * n_out + o] = acc;
 }
 
+// ---------------------------------------------- streaming single-launch GEMV --
+//
+// One launch per call; weights are streamed row-contiguously (a wave-load
+// moves 1 KiB of one row: 64 lanes x 16 bytes):
+//   * the x prologue runs once per workgroup: 4 threads per group load x
+//     (before any weight load, so they are not queued behind HBM traffic),
+//     chain the group sum in ascending order and find amax; after one
+//     barrier they quantise their own values into int8/uint8 planes in LDS;
+//   * after that every wave works alone on units of UB consecutive rows.  A
+//     unit is a list of (chunk, row) items of 1 KiB each, streamed in
+//     batches of kBatch with the next batch (or the next unit's first batch)
+//     in flight while the current one is computed;
+//   * each group's fp32 term goes to a wave-private LDS table; when a unit
+//     is done one lane per (m, row) adds its row's terms in ascending group
+//     order -- no workgroup barrier in the main loop.
+// The row a wave works on is wave-uniform (kept in SGPRs), so choosing the
+// matrix of a grouped launch (q/k/v, gate/up: up to kMaxMats sharing x) is
+// scalar work.
+constexpr int kMaxMats = 4;
+constexpr int kBatch = 4;
+
+struct MatList {
+    const uint32_t* w[kMaxMats];
+    const uint16_t* s[kMaxMats];
+    const uint16_t* b[kMaxMats];
+    float* out[kMaxMats];
+    int n_out[kMaxMats];
+    int row_begin[kMaxMats + 1];   // prefix sums of n_out
+    int count;
+};
+
+// Row stride of the per-wave term table: a multiple of 4 floats (16-byte
+// reads) that is 4 mod 8 words, so lanes reading different rows spread over
+// the banks.
+__host__ __device__ inline int term_stride(int G) { return ((G + 3) & ~3) | 4; }
+
+size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int UB) {
+    return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
+         + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
+         + static_cast<size_t>(mr) * 16 * 4                              // amax per wave
+         + static_cast<size_t>(nwaves) * mr * UB * term_stride(G) * 4;  // term tables
+}
+
+__device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxMats; k++) p += (k < ml.count && gr >= ml.row_begin[k]) ? 1 : 0;
+    return p;
+}
+
+struct Batch {
+    uint4 w[kBatch];
+    uint16_t s[kBatch], b[kBatch];
+};
+
+// Issue the loads of items [i0, i0 + kBatch) of unit `unit` (item = c*UB + u:
+// chunk-major, so consecutive items share x planes).  Everything here is
+// wave-uniform except the lane's word offset.  Loads are unconditional from
+// clamped, always-valid addresses: lanes past the row end (whole groups) and
+// rows past the end load data that no leader ever turns into a term.
+__device__ __forceinline__ void load_batch(Batch& bt, const MatList& ml, int unit, int i0, int UB,
+                                           int C, int n_total, int wpr, int G, int lane, int wpg) {
+#pragma unroll
+    for (int k = 0; k < kBatch; k++) {
+        int item = i0 + k;
+        item = item < UB * C ? item : UB * C - 1;
+        const int c = item / UB, u = item - c * UB;
+        int gr = unit * UB + u;
+        gr = gr < n_total ? gr : n_total - 1;
+        // p is wave-uniform; readfirstlane makes that explicit, so the
+        // kernel-argument reads below are scalar loads
+        const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, gr));
+        const int o = gr - ml.row_begin[p];
+        const int word0 = c * kChunkWords + lane * 4;
+        const int wc = word0 < wpr ? word0 : wpr - 4;              // wpr >= 8
+        const int g = wc / wpg;
+        bt.w[k] = *reinterpret_cast<const uint4*>(ml.w[p] + static_cast<size_t>(o) * wpr + wc);
+        bt.s[k] = ml.s[p][static_cast<size_t>(o) * G + g];
+        bt.b[k] = ml.b[p][static_cast<size_t>(o) * G + g];
+    }
+}
+
+// VPT = gs / 4 values per prologue thread (gs = 64 or 128).
+template <int MR, int VPT>
+__global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const float* __restrict__ x,
+                                                          int n_in, int UB) {
+    extern __shared__ uint4 lds4[];
+    constexpr int gs = 4 * VPT, lpg = gs / 32, wpg = gs / 8;
+    const int wpr = n_in >> 3, G = n_in / gs;
+    const int C = (wpr + kChunkWords - 1) / kChunkWords;
+    const int Gr = (G + 3) & ~3, Ts = term_stride(G);
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);    // wave-uniform
+    const int nwaves = nt >> 6;
+    uint4* xpl = lds4;                                            // [MR][C*256] swizzled
+    float* xsum_lds = reinterpret_cast<float*>(xpl + MR * C * 256);   // [MR][Gr]
+    float* red = xsum_lds + MR * Gr;                              // [MR][16]
+    float* Tw = red + MR * 16 + wave * (MR * UB * Ts);            // this wave: [MR][UB][Ts]
+    const int n_total = ml.row_begin[ml.count];
+    const int n_units = (n_total + UB - 1) / UB;
+    const int tw = gridDim.x * nwaves;
+    const int items = UB * C;
+    // ---- prologue pass 1 (x loads first): one thread per group loads its
+    //      gs values, adds them in order (kernel/q4gemv.c:244-248) and keeps
+    //      the running max |x| (:258-259).
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        const float* xr = x + static_cast<size_t>(m) * n_in;
+        float amax = 0.0f;
+        for (int base = 0; base < G; base += nt) {                 // uniform trip count
+            const int gg = base + tid;
+            const int gc = gg < G ? gg : G - 1;                    // duplicate: no effect on amax
+            float sum = 0.0f;
+#pragma unroll
+            for (int h = 0; h < gs / 64; h++) {
+                float4 f[16];
+#pragma unroll
+                for (int i = 0; i < 16; i++)
+                    f[i] = reinterpret_cast<const float4*>(xr + gs * gc + 64 * h)[i];
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    sum = __fadd_rn(sum, f[i].x); sum = __fadd_rn(sum, f[i].y);
+                    sum = __fadd_rn(sum, f[i].z); sum = __fadd_rn(sum, f[i].w);
+                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(f[i].x), fabsf(f[i].y)),
+                                             fmaxf(fabsf(f[i].z), fabsf(f[i].w))));
+                }
+            }
+            if (gg < G) xsum_lds[m * Gr + gg] = sum;
+        }
+        amax = wave_max(amax);
+        if (lane == 0) red[m * 16 + wave] = amax;
+    }
+
+    // first batch of this wave's first unit is in flight during the rest of
+    // the prologue
+    const int gw = blockIdx.x * nwaves + wave;
+    Batch cur;
+    if (gw < n_units) load_batch(cur, ml, gw, 0, UB, C, n_total, wpr, G, lane, wpg);
+
+    __syncthreads();
+    // ---- prologue pass 2: one thread per word: int16 x (kernel/q4gemv.c:
+    //      260-270) as byte planes in LDS; words past the row end are zero
+    float xsc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        float a = 0.0f;
+        for (int i = 0; i < nwaves; i++) a = fmaxf(a, red[m * 16 + i]);
+        xsc[m] = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;        // kernel/q4gemv.c:260
+        const float inv = __fdiv_rn(1.0f, xsc[m]);                 // :261
+        const bool exact_clamp = __builtin_isinf(inv);
+        const float* xr = x + static_cast<size_t>(m) * n_in;
+        for (int j = tid; j < C * 256; j += nt) {
+            uint4 pl = make_uint4(0, 0, 0, 0);
+            if (j < wpr) {
+                const float4 v0 = reinterpret_cast<const float4*>(xr + 8 * j)[0];
+                const float4 v1 = reinterpret_cast<const float4*>(xr + 8 * j)[1];
+                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+                pl = quant_word(vv, inv, exact_clamp);
+            }
+            const int cc = j >> 8, jj = j & 255;
+            xpl[(m * C + cc) * 256 + (jj & 3) * 64 + (jj >> 2)] = pl;
+        }
+    }
+    __syncthreads();
+
+    // ---- main loop: each wave streams its own row units
+    for (int unit = gw; unit < n_units; unit += tw) {
+        int cprev = -1;
+        uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
+        for (int i0 = 0; i0 < items; i0 += kBatch) {
+            Batch nxt;
+            if (i0 + kBatch < items)
+                load_batch(nxt, ml, unit, i0 + kBatch, UB, C, n_total, wpr, G, lane, wpg);
+            else if (unit + tw < n_units)
+                load_batch(nxt, ml, unit + tw, 0, UB, C, n_total, wpr, G, lane, wpg);
+#pragma unroll
+            for (int k = 0; k < kBatch; k++) {
+                const int item = i0 + k;
+                if (item >= items) break;                           // uniform
+                const int c = item / UB, u = item - c * UB;
+                const int word0 = c * kChunkWords + lane * 4;
+                const bool lead = word0 < wpr && (lane & (lpg - 1)) == lpg - 1;
+                const int g = word0 / wpg;
+                if (c != cprev) {                                   // uniform: planes of chunk c
+#pragma unroll
+                    for (int m = 0; m < MR; m++)
+#pragma unroll
+                        for (int t = 0; t < 4; t++) {
+                            const uint4 pl = xpl[(m * C + c) * 256 + t * 64 + lane];
+                            xle[m][t] = pl.x; xlo[m][t] = pl.y; xhe[m][t] = pl.z; xho[m][t] = pl.w;
+                        }
+                    cprev = c;
+                }
+                const uint32_t wd[4] = {cur.w[k].x, cur.w[k].y, cur.w[k].z, cur.w[k].w};
+                uint32_t lo4[4], hi4[4];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    lo4[t] = wd[t] & 0x0F0F0F0Fu;          // values 8j+0,2,4,6
+                    hi4[t] = (wd[t] >> 4) & 0x0F0F0F0Fu;   // values 8j+1,3,5,7
+                }
+                const float sf = h2f(cur.s[k]), bf = h2f(cur.b[k]);
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    int ah = 0;
+                    uint32_t al = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        ah = __builtin_amdgcn_sdot4(static_cast<int>(lo4[t]), static_cast<int>(xhe[m][t]), ah, false);
+                        ah = __builtin_amdgcn_sdot4(static_cast<int>(hi4[t]), static_cast<int>(xho[m][t]), ah, false);
+                        al = __builtin_amdgcn_udot4(lo4[t], xle[m][t], al, false);
+                        al = __builtin_amdgcn_udot4(hi4[t], xlo[m][t], al, false);
+                    }
+                    const int part = group_sum(static_cast<int>(static_cast<uint32_t>(ah) * 256u + al), lpg);
+                    if (lead) {
+                        const float dot = __fmul_rn(xsc[m], static_cast<float>(part));
+                        const float bx = __fmul_rn(bf, xsum_lds[m * Gr + g]);
+                        Tw[(m * UB + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
+                    }
+                }
+            }
+            cur = nxt;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (lane < MR * UB) {
+            const int m = lane / UB, u = lane - m * UB, gr = unit * UB + u;
+            if (gr < n_total) {
+                const float4* tp = reinterpret_cast<const float4*>(Tw + (m * UB + u) * Ts);
+                float acc = 0.0f;
+                int gg = 0;
+                for (; gg + 16 <= G; gg += 16) {           // 4 reads in flight, then 16 adds
+                    const float4 a0 = tp[gg / 4], a1 = tp[gg / 4 + 1], a2 = tp[gg / 4 + 2], a3 = tp[gg / 4 + 3];
+                    const float vals[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                                            a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc = __fadd_rn(acc, vals[i]);
+                }
+                const float* tps = Tw + (m * UB + u) * Ts;
+                for (; gg < G; gg++) acc = __fadd_rn(acc, tps[gg]);
+                // the host picks UB dividing every n_out, so a unit never
+                // straddles two matrices and p is wave-uniform
+                const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
+                ml.out[p][static_cast<size_t>(m) * ml.n_out[p] + (gr - ml.row_begin[p])] = acc;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
+}
+
 __global__ void fill_zero_kernel(float* __restrict__ p, long n) {
     const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -382,10 +690,15 @@ std::map<ResKey, Resident> g_res;
 
 int ensure_ws(Workspace& ws, hipStream_t st, size_t words, size_t groups) {
     if (words <= ws.cap_words && groups <= ws.cap_groups && ws.planes) return 0;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(st, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+        return fail(Q4_EARG, "x workspace of this stream must grow during graph capture: "
+                             "run the largest call once on the stream before capturing");
     HIP_TRY(hipStreamSynchronize(st));
-    hipFree(ws.planes);
-    hipFree(ws.xsum);
-    hipFree(ws.xscale);
+    (void)hipFree(ws.planes);
+    (void)hipFree(ws.xsum);
+    (void)hipFree(ws.xscale);
     ws = Workspace{};
     size_t cw = words < 4096 ? 4096 : words, cg = groups < 1024 ? 1024 : groups;
     HIP_TRY(hipMalloc(&ws.planes, cw * sizeof(uint4)));
@@ -415,9 +728,86 @@ hipError_t launch_main(const uint32_t* w, const uint16_t* s, const uint16_t* b,
     return hipGetLastError();
 }
 
-// Prologue + main kernels for m (<= kMaxM) rows already on the device.
-int gemv_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
-              float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws) {
+int num_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+constexpr size_t kStreamLdsMax = 160 * 1024;
+
+template <int MR, int VPT>
+int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st) {
+    auto kern = gemv_stream_kernel<MR, VPT>;
+    const int G = n_in / (4 * VPT);
+    const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
+    const int n_total = ml.row_begin[ml.count];
+    const int cus = num_cus();
+    // 16 waves per workgroup when there are rows for a full grid of them,
+    // else smaller workgroups so that every CU gets some
+    int nwaves = 16;
+    while (nwaves > 4 && n_total < nwaves * cus) nwaves >>= 1;
+    // rows per unit: enough 1 KiB items per unit to fill a batch, more when
+    // rows are plentiful
+    int UB = 1;
+    while (UB < 4 && UB * C < kBatch && n_total >= 2 * UB * nwaves * cus) UB *= 2;
+    while (MR * UB > 64) UB >>= 1;
+    for (int k = 0; k < ml.count; k++)                 // a unit must not straddle matrices
+        while (ml.n_out[k] % UB) UB >>= 1;
+    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, UB);
+    if (lds > kStreamLdsMax) return 0;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(kStreamLdsMax));
+        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
+        attr_set = true;
+    }
+    int per_cu = 0;
+    hipError_t eo = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * nwaves, lds);
+    if (eo != hipSuccess || per_cu < 1) per_cu = 1;
+    const int n_units = (n_total + UB - 1) / UB;
+    const int want = (n_units + nwaves - 1) / nwaves;
+    const int cap = cus * per_cu;                       // every workgroup resident at once
+    const int grid = want < cap ? want : cap;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q4_EHIP, "stream gemv launch: %s", hipGetErrorString(e));
+    return 1;
+}
+
+// The streaming path takes gs 64, x 16-byte aligned and at most 16 chunks
+// (n_in <= 32768).  Returns 1 if it launched, 0 if the call must take
+// the split path, <0 on error.
+template <int MR>
+int try_fused(const MatList& ml, const float* x, int n_in, int gs, hipStream_t st) {
+    if (gs != 64 || n_in == 0 || (reinterpret_cast<uintptr_t>(x) & 15)) return 0;
+    const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
+    if (C > 16) return 0;
+    if (gs == 64) return launch_stream<MR, 16>(ml, x, n_in, st);
+    return 0;                           // other group sizes: split path
+}
+
+int try_fused_m(const MatList& ml, const float* x, int m, int n_in, int gs, hipStream_t st) {
+    switch (m) {
+        case 1: return try_fused<1>(ml, x, n_in, gs, st);
+        case 2: return try_fused<2>(ml, x, n_in, gs, st);
+        default: return 0;      // 3..8 rows: split path (the streaming kernel would spill)
+    }
+}
+
+// Split path: prologue kernel, then the main kernel reading x planes from a
+// per-stream workspace.  Takes every shape the fused path does not.
+int gemv_split(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
+               float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws) {
     const int wpr = n_in / 8, n_groups = n_in / gs;
     int rc = ensure_ws(ws, st, static_cast<size_t>(m) * wpr, static_cast<size_t>(m) * n_groups);
     if (rc) return rc;
@@ -441,9 +831,8 @@ int gemv_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const flo
         switch (m) {
             case 1: e = launch_main<1>(w, s, b, ws, out, n_out, n_in, gs, st); break;
             case 2: e = launch_main<2>(w, s, b, ws, out, n_out, n_in, gs, st); break;
-            case 3:
-            case 4: e = m == 4 ? launch_main<4>(w, s, b, ws, out, n_out, n_in, gs, st)
-                               : launch_main<3>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            case 3: e = launch_main<3>(w, s, b, ws, out, n_out, n_in, gs, st); break;
+            case 4: e = launch_main<4>(w, s, b, ws, out, n_out, n_in, gs, st); break;
             case 5: e = launch_main<5>(w, s, b, ws, out, n_out, n_in, gs, st); break;
             case 6: e = launch_main<6>(w, s, b, ws, out, n_out, n_in, gs, st); break;
             case 7: e = launch_main<7>(w, s, b, ws, out, n_out, n_in, gs, st); break;
@@ -452,6 +841,20 @@ int gemv_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const flo
     }
     if (e != hipSuccess) return fail(Q4_EHIP, "gemv launch: %s", hipGetErrorString(e));
     return 0;
+}
+
+// GEMV of m (<= kMaxM) rows already on the device: fused when possible.
+int gemv_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
+              float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws) {
+    MatList ml{};
+    ml.w[0] = w; ml.s[0] = s; ml.b[0] = b; ml.out[0] = out; ml.n_out[0] = n_out;
+    ml.row_begin[0] = 0;
+    for (int k = 1; k <= kMaxMats; k++) ml.row_begin[k] = n_out;
+    ml.count = 1;
+    int rc = try_fused_m(ml, x, m, n_in, gs, st);
+    if (rc < 0) return rc;
+    if (rc == 1) return 0;
+    return gemv_split(w, s, b, x, out, m, n_out, n_in, gs, st, ws);
 }
 
 int check_gemv_shape(int n_out, int n_in, int gs) {
@@ -478,7 +881,7 @@ int dev_state(DevState** out) {
 template <typename T>
 int grow_pinned(T** p, size_t* cap, size_t n) {
     if (n <= *cap && *p) return 0;
-    if (*p) hipHostFree(*p);
+    if (*p) (void)hipHostFree(*p);
     *p = nullptr;
     *cap = 0;
     size_t c = n < 65536 ? 65536 : n;
@@ -490,7 +893,7 @@ int grow_pinned(T** p, size_t* cap, size_t n) {
 template <typename T>
 int grow_dev(T** p, size_t* cap, size_t n) {
     if (n <= *cap && *p) return 0;
-    if (*p) hipFree(*p);
+    if (*p) (void)hipFree(*p);
     *p = nullptr;
     *cap = 0;
     size_t c = n < 65536 ? 65536 : n;
@@ -541,9 +944,9 @@ int resident(const uint32_t* w, const uint16_t* s, const uint16_t* b, int n_out,
 }
 
 void free_resident(Resident& r) {
-    hipFree(r.w);
-    hipFree(r.s);
-    hipFree(r.b);
+    (void)hipFree(r.w);
+    (void)hipFree(r.s);
+    (void)hipFree(r.b);
 }
 
 int gemv_host(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
@@ -656,10 +1059,10 @@ int q4_release(const void* w) {
     for (auto it = g_res.begin(); it != g_res.end();) {
         if (std::get<1>(it->first) == w) {
             int cur = 0;
-            hipGetDevice(&cur);
-            hipSetDevice(std::get<0>(it->first));
+            (void)hipGetDevice(&cur);
+            (void)hipSetDevice(std::get<0>(it->first));
             free_resident(it->second);
-            hipSetDevice(cur);
+            (void)hipSetDevice(cur);
             it = g_res.erase(it);
             n++;
         } else {
@@ -672,13 +1075,13 @@ int q4_release(const void* w) {
 int q4_release_all(void) {
     std::lock_guard<std::mutex> lock(g_mu);
     int n = 0, cur = 0;
-    hipGetDevice(&cur);
+    (void)hipGetDevice(&cur);
     for (auto& kv : g_res) {
-        hipSetDevice(std::get<0>(kv.first));
+        (void)hipSetDevice(std::get<0>(kv.first));
         free_resident(kv.second);
         n++;
     }
-    hipSetDevice(cur);
+    (void)hipSetDevice(cur);
     g_res.clear();
     return n;
 }
@@ -707,6 +1110,42 @@ int q4_gemv_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biase
                        out + static_cast<size_t>(m0) * n_out, mm, n_out, n_in, gs, st, *ws);
         if (rc) return rc;
     }
+    return 0;
+}
+
+int q4_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const* scales,
+                      const uint16_t* const* biases, float* const* out, const int* n_out,
+                      const float* x, int m, int n_in, int gs, void* stream) {
+    if (count < 1 || count > kMaxMats || !w || !scales || !biases || !out || !n_out)
+        return fail(Q4_EARG, "count=%d (1..%d) or null array", count, kMaxMats);
+    int rc;
+    for (int k = 0; k < count; k++) {
+        if ((rc = check_gemv_shape(n_out[k], n_in, gs))) return rc;
+        if (!w[k] || !scales[k] || !biases[k] || !out[k]) return fail(Q4_EARG, "null pointer in matrix %d", k);
+        if (reinterpret_cast<uintptr_t>(w[k]) & 15) return fail(Q4_EARG, "w[%d] must be 16-byte aligned", k);
+    }
+    if (m < 0) return fail(Q4_EARG, "m=%d", m);
+    if (m == 0) return 0;
+    if (!x) return fail(Q4_EARG, "null x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (m <= kMaxM) {
+        MatList ml{};
+        ml.row_begin[0] = 0;
+        for (int k = 0; k < kMaxMats; k++) {
+            const int kk = k < count ? k : count - 1;
+            ml.w[k] = w[kk]; ml.s[k] = scales[kk]; ml.b[k] = biases[kk]; ml.out[k] = out[kk];
+            ml.n_out[k] = k < count ? n_out[k] : 0;
+            ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
+        }
+        ml.count = count;
+        if (ml.row_begin[count] == 0) return 0;
+        rc = try_fused_m(ml, x, m, n_in, gs, st);
+        if (rc < 0) return rc;
+        if (rc == 1) return 0;
+    }
+    for (int k = 0; k < count; k++)
+        if ((rc = q4_gemv_dev(w[k], scales[k], biases[k], x, out[k], m, n_out[k], n_in, gs, stream)))
+            return rc;
     return 0;
 }
 

@@ -84,6 +84,15 @@ int q4_gemv_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biase
                 const float *x, float *out, int m, int n_out, int n_in, int gs,
                 void *stream);
 
+/* Up to four matrices that share the activations x (q/k/v, gate/up) in one
+ * launch: out[k] is [m][n_out[k]] = W_k x, each row bit-identical to q4_gemv.
+ * w, scales, biases, out and n_out are host arrays of `count` device
+ * pointers / sizes.  No counterpart in the reference, whose caller makes one
+ * q4_gemv call per projection (hetero/cpu_model.py:269-275, :291-292). */
+int q4_gemv_multi_dev(int count, const uint32_t *const *w, const uint16_t *const *scales,
+                      const uint16_t *const *biases, float *const *out, const int *n_out,
+                      const float *x, int m, int n_in, int gs, void *stream);
+
 /* Device q4_dequant: rows [row0,row1) to fp32 [row1-row0][n_in]. */
 int q4_dequant_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
                    float *out, int row0, int row1, int n_in, int gs, void *stream);

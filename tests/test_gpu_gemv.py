@@ -192,3 +192,39 @@ def test_residency_detects_replaced_weights(lib):
     second = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, 64)
     assert_bit_exact(second, o.gemv(w, s, b, x, 64), "second")
     assert lib.q4_release(w.ctypes.data) >= 1
+
+
+def test_multi_dev_grouped(lib):
+    """q4_gemv_multi_dev (q/k/v and gate/up style groups) vs the oracle, bit-exact."""
+    import torch
+    o = oracle.Oracle()
+    for m, shapes in ((1, [(3584, 3584), (3584, 512), (3584, 512)]),
+                      (2, [(1024, 1536), (1024, 2560)]),
+                      (4, [(2048, 96), (2048, 64), (2048, 8), (2048, 40)])):
+        k_in = shapes[0][0]
+        print(f"multi m={m} shapes={shapes}", flush=True)
+        mats_np = [synth.qlinear(300 + i, n, k_in, 64) for i, (_, n) in enumerate(shapes)]
+        x = synth.activations(300, m, k_in)
+        mats = [tuple(torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16)))
+                for w, s, b in mats_np]
+        outs = q4.gemv_multi_dev(mats, torch.from_numpy(x).cuda())
+        torch.cuda.synchronize()
+        for (w, s, b), got in zip(mats_np, outs):
+            want = o.gemv_rows(w, s, b, x, 64)
+            assert_bit_exact(got.cpu().numpy(), want, f"multi m={m} n={w.shape[0]}")
+
+
+def test_dev_all_m_and_paths(lib):
+    """q4_gemv_dev for m = 1..9 at a small and a long K (fused and split paths)."""
+    import torch
+    o = oracle.Oracle()
+    for k_in, n_out in ((1536, 200), (18944, 40), (40960, 16)):
+        w, s, b = synth.qlinear(400 + k_in, n_out, k_in, 64)
+        x = synth.activations(401, 9, k_in)
+        want = o.gemv_rows(w, s, b, x, 64)
+        tw, ts, tb, tx = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16), x))
+        for m in range(1, 10):
+            print(f"dev K={k_in} N={n_out} m={m}", flush=True)
+            got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
+            torch.cuda.synchronize()
+            assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} m={m}")
