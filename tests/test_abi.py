@@ -1,0 +1,95 @@
+"""C-ABI contract of libq4gemv.so, checked on the CPU (no GPU is touched).
+
+* the library is built in-tree where the reference's loader looks
+  (hetero/cpu_model.py:35-37: <package parent>/kernel/libq4gemv.so);
+* it exports every function include/q4gemv.h declares, and the ctypes
+  declarations match the reference's for the two drop-in symbols
+  (hetero/cpu_model.py:41-44);
+* shape errors return the reference's codes before any HIP call
+  (kernel/q4gemv.c:237, :361, :363), other argument errors Q4_EARG.
+"""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from hetero import q4
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "q4gemv.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q4_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return q4.load()
+
+
+def test_library_location_mirrors_reference():
+    assert q4.LIB_PATH == os.path.join(ROOT, "hetero-infer_amd", "kernel", "libq4gemv.so")
+    assert os.path.exists(q4.LIB_PATH), "run python hetero-infer_amd/build.py"
+
+
+def test_exports_every_declared_function(lib):
+    declared = header_functions()
+    assert {"q4_gemv", "q4_dequant"} <= set(declared)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(q4.EXPORTS)
+
+
+def test_dropin_signatures_match_reference(lib):
+    vp, i = ctypes.c_void_p, ctypes.c_int
+    assert list(lib.q4_gemv.argtypes) == [vp] * 5 + [i] * 4
+    assert list(lib.q4_dequant.argtypes) == [vp] * 4 + [i] * 5
+    assert lib.q4_gemv.restype is i and lib.q4_dequant.restype is i
+
+
+def test_shape_errors_before_any_device_call(lib):
+    w = np.zeros((4, 32), np.uint32)
+    s = np.zeros((4, 4), np.uint16)
+    x = np.zeros(256, np.float32)
+    out = np.zeros(4, np.float32)
+    a = (w.ctypes.data, s.ctypes.data, s.ctypes.data, x.ctypes.data, out.ctypes.data)
+    assert lib.q4_gemv(*a, 4, 256, 32, 1) == -1            # gs % 64 (x86 reference)
+    assert lib.q4_gemv(*a, 4, 200, 64, 1) == -1            # n_in % gs
+    assert lib.q4_gemv(*a, 4, 256, 0, 1) == -1             # gs <= 0 (reference would trap)
+    assert lib.q4_gemv_batched(*a, 1, 4, 200, 64, 1) == -1
+    d = (w.ctypes.data, s.ctypes.data, s.ctypes.data, out.ctypes.data)
+    assert lib.q4_dequant(*d, 0, 2, 256, 12, 1) == -1      # gs % 8
+    assert lib.q4_dequant(*d, 3, 3, 256, 64, 1) == 0       # empty range
+    assert lib.q4_dequant(*d, 3, 1, 256, 64, 1) == 0       # reversed range
+    assert lib.q4_gemv_dev(*a[:5], 1, 4, 200, 64, None) == -1
+    assert lib.q4_dequant_dev(*d, 0, 2, 256, 12, None) == -1
+
+
+def test_argument_errors(lib):
+    assert lib.q4_gemv(None, None, None, None, None, 4, 256, 64, 1) == q4.Q4_EARG
+    assert "null" in q4.last_error(lib)
+    assert lib.q4_gemv_dev(None, None, None, None, None, 1, 4, 256, 64, None) == q4.Q4_EARG
+    w = np.zeros(64, np.uint32)
+    mis = w.ctypes.data + 4                                # not 16-byte aligned
+    assert lib.q4_gemv_dev(mis, mis, mis, mis, mis, 1, 4, 256, 64, None) == q4.Q4_EARG
+    arr = (ctypes.c_void_p * 5)()
+    n = (ctypes.c_int * 5)()
+    assert lib.q4_gemv_multi_dev(0, arr, arr, arr, arr, n, None, 1, 256, 64, None) == q4.Q4_EARG
+    assert lib.q4_gemv_multi_dev(5, arr, arr, arr, arr, n, None, 1, 256, 64, None) == q4.Q4_EARG
+
+
+def test_zero_rows_are_noops(lib):
+    # n_out == 0 / m == 0: success without touching any pointer or device
+    assert lib.q4_gemv(None, None, None, None, None, 0, 256, 64, 1) == 0
+    assert lib.q4_gemv_dev(None, None, None, None, None, 0, 4, 256, 64, None) == 0
+    assert lib.q4_gemv_dev(None, None, None, None, None, 1, 0, 256, 64, None) == 0
+
+
+def test_release_without_registrations(lib):
+    assert lib.q4_release(None) == 0
+    assert lib.q4_release_all() >= 0
