@@ -365,11 +365,11 @@ struct MatList {
 // the banks.
 __host__ __device__ inline int term_stride(int G) { return ((G + 3) & ~3) | 4; }
 
-size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int UB) {
+size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU) {
     return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
          + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
          + static_cast<size_t>(mr) * 16 * 4                              // amax per wave
-         + static_cast<size_t>(nwaves) * mr * UB * term_stride(G) * 4;  // term tables
+         + static_cast<size_t>(nwaves) * mr * NU * term_stride(G) * 4;  // term tables
 }
 
 __device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
@@ -384,24 +384,29 @@ struct Batch {
     uint16_t s[kBatch], b[kBatch];
 };
 
-// Issue the loads of items [i0, i0 + kBatch) of unit `unit` (item = c*UB + u:
-// chunk-major, so consecutive items share x planes).  Everything here is
-// wave-uniform except the lane's word offset.  Loads are unconditional from
-// clamped, always-valid addresses: lanes past the row end (whole groups) and
-// rows past the end load data that no leader ever turns into a term.
+// Issue the loads of items [i0, i0 + kBatch) of unit `unit`.  A unit is
+// NU = UB rows (PAIR: UB rows of matrix 0 and the same UB rows of matrix 1);
+// item = c*NU + r, chunk-major so consecutive items share x planes.
+// Everything here is wave-uniform except the lane's word offset.  Loads are
+// unconditional from clamped, always-valid addresses: lanes past the row end
+// (whole groups) and rows past the end load data that no leader ever turns
+// into a term.
+template <bool PAIR>
 __device__ __forceinline__ void load_batch(Batch& bt, const MatList& ml, int unit, int i0, int UB,
                                            int C, int n_total, int wpr, int G, int lane, int wpg) {
+    const int NU = PAIR ? 2 * UB : UB;
 #pragma unroll
     for (int k = 0; k < kBatch; k++) {
         int item = i0 + k;
-        item = item < UB * C ? item : UB * C - 1;
-        const int c = item / UB, u = item - c * UB;
+        item = item < NU * C ? item : NU * C - 1;
+        const int c = item / NU, r = item - c * NU;
+        const int u = PAIR ? (r < UB ? r : r - UB) : r;
         int gr = unit * UB + u;
         gr = gr < n_total ? gr : n_total - 1;
         // p is wave-uniform; readfirstlane makes that explicit, so the
         // kernel-argument reads below are scalar loads
-        const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, gr));
-        const int o = gr - ml.row_begin[p];
+        const int p = __builtin_amdgcn_readfirstlane(PAIR ? (r < UB ? 0 : 1) : mat_of_row(ml, gr));
+        const int o = PAIR ? gr : gr - ml.row_begin[p];
         const int word0 = c * kChunkWords + lane * 4;
         const int wc = word0 < wpr ? word0 : wpr - 4;              // wpr >= 8
         const int g = wc / wpg;
@@ -411,8 +416,34 @@ __device__ __forceinline__ void load_batch(Batch& bt, const MatList& ml, int uni
     }
 }
 
+// Sequential fp32 sum of n terms (ascending), four 16-byte LDS reads in flight.
+__device__ __forceinline__ float chain_sum(const float* tp, int n) {
+    const float4* t4 = reinterpret_cast<const float4*>(tp);
+    float acc = 0.0f;
+    int g = 0;
+    for (; g + 16 <= n; g += 16) {
+        const float4 a0 = t4[g / 4], a1 = t4[g / 4 + 1], a2 = t4[g / 4 + 2], a3 = t4[g / 4 + 3];
+        const float vals[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                                a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = __fadd_rn(acc, vals[i]);
+    }
+    for (; g < n; g++) acc = __fadd_rn(acc, tp[g]);
+    return acc;
+}
+
+// SiLU(g) * u as hetero/cpu_model.py:169-170 and :291-292 compute it in
+// fp32: g / (1 + exp(-g)) * u (expf here; NumPy's float32 exp may differ in
+// the last place).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = expf(-g);
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+}
+
 // VPT = gs / 4 values per prologue thread (gs = 64 or 128).
-template <int MR, int VPT>
+// PAIR: matrices 0 and 1 (gate, up) are computed row for row and the
+// output is out[0] = SiLU(gate) * up.
+template <int MR, int VPT, bool PAIR>
 __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const float* __restrict__ x,
                                                           int n_in, int UB) {
     extern __shared__ uint4 lds4[];
@@ -427,11 +458,12 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     uint4* xpl = lds4;                                            // [MR][C*256] swizzled
     float* xsum_lds = reinterpret_cast<float*>(xpl + MR * C * 256);   // [MR][Gr]
     float* red = xsum_lds + MR * Gr;                              // [MR][16]
-    float* Tw = red + MR * 16 + wave * (MR * UB * Ts);            // this wave: [MR][UB][Ts]
-    const int n_total = ml.row_begin[ml.count];
+    const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
+    float* Tw = red + MR * 16 + wave * (MR * NU * Ts);            // this wave: [MR][NU][Ts]
+    const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
     const int n_units = (n_total + UB - 1) / UB;
     const int tw = gridDim.x * nwaves;
-    const int items = UB * C;
+    const int items = NU * C;
     // ---- prologue pass 1 (x loads first): one thread per group loads its
     //      gs values, adds them in order (kernel/q4gemv.c:244-248) and keeps
     //      the running max |x| (:258-259).
@@ -467,7 +499,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     // the prologue
     const int gw = blockIdx.x * nwaves + wave;
     Batch cur;
-    if (gw < n_units) load_batch(cur, ml, gw, 0, UB, C, n_total, wpr, G, lane, wpg);
+    if (gw < n_units) load_batch<PAIR>(cur, ml, gw, 0, UB, C, n_total, wpr, G, lane, wpg);
 
     __syncthreads();
     // ---- prologue pass 2: one thread per word: int16 x (kernel/q4gemv.c:
@@ -502,14 +534,14 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
         for (int i0 = 0; i0 < items; i0 += kBatch) {
             Batch nxt;
             if (i0 + kBatch < items)
-                load_batch(nxt, ml, unit, i0 + kBatch, UB, C, n_total, wpr, G, lane, wpg);
+                load_batch<PAIR>(nxt, ml, unit, i0 + kBatch, UB, C, n_total, wpr, G, lane, wpg);
             else if (unit + tw < n_units)
-                load_batch(nxt, ml, unit + tw, 0, UB, C, n_total, wpr, G, lane, wpg);
+                load_batch<PAIR>(nxt, ml, unit + tw, 0, UB, C, n_total, wpr, G, lane, wpg);
 #pragma unroll
             for (int k = 0; k < kBatch; k++) {
                 const int item = i0 + k;
                 if (item >= items) break;                           // uniform
-                const int c = item / UB, u = item - c * UB;
+                const int c = item / NU, u = item - c * NU;       // u: row slot in the unit
                 const int word0 = c * kChunkWords + lane * 4;
                 const bool lead = word0 < wpr && (lane & (lpg - 1)) == lpg - 1;
                 const int g = word0 / wpg;
@@ -546,7 +578,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
                     if (lead) {
                         const float dot = __fmul_rn(xsc[m], static_cast<float>(part));
                         const float bx = __fmul_rn(bf, xsum_lds[m * Gr + g]);
-                        Tw[(m * UB + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
+                        Tw[(m * NU + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
                     }
                 }
             }
@@ -558,28 +590,29 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
         if (lane < MR * UB) {
             const int m = lane / UB, u = lane - m * UB, gr = unit * UB + u;
             if (gr < n_total) {
-                const float4* tp = reinterpret_cast<const float4*>(Tw + (m * UB + u) * Ts);
-                float acc = 0.0f;
-                int gg = 0;
-                for (; gg + 16 <= G; gg += 16) {           // 4 reads in flight, then 16 adds
-                    const float4 a0 = tp[gg / 4], a1 = tp[gg / 4 + 1], a2 = tp[gg / 4 + 2], a3 = tp[gg / 4 + 3];
-                    const float vals[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                                            a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
-#pragma unroll
-                    for (int i = 0; i < 16; i++) acc = __fadd_rn(acc, vals[i]);
+                const float acc = chain_sum(Tw + (m * NU + u) * Ts, G);
+                if constexpr (PAIR) {
+                    const float up = chain_sum(Tw + (m * NU + UB + u) * Ts, G);
+                    ml.out[0][static_cast<size_t>(m) * ml.n_out[0] + gr] = silu_mul(acc, up);
+                } else {
+                    // the host picks UB dividing every n_out, so a unit never
+                    // straddles two matrices and p is wave-uniform
+                    const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
+                    ml.out[p][static_cast<size_t>(m) * ml.n_out[p] + (gr - ml.row_begin[p])] = acc;
                 }
-                const float* tps = Tw + (m * UB + u) * Ts;
-                for (; gg < G; gg++) acc = __fadd_rn(acc, tps[gg]);
-                // the host picks UB dividing every n_out, so a unit never
-                // straddles two matrices and p is wave-uniform
-                const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
-                ml.out[p][static_cast<size_t>(m) * ml.n_out[p] + (gr - ml.row_begin[p])] = acc;
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
+}
+
+// h = SiLU(g) * u elementwise (fallback of the fused gate/up launch).
+__global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                float* __restrict__ h, long n) {
+    const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = silu_mul(g[i], u[i]);
 }
 
 __global__ void fill_zero_kernel(float* __restrict__ p, long n) {
@@ -661,7 +694,25 @@ struct Workspace {
     float* xsum = nullptr;
     float* xscale = nullptr;
     size_t cap_words = 0, cap_groups = 0;
+    float* tmp = nullptr;                       // up-projection rows of the unfused MLP
+    size_t cap_tmp = 0;
 };
+
+int ensure_tmp(Workspace& ws, hipStream_t st, size_t n) {
+    if (n <= ws.cap_tmp && ws.tmp) return 0;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(st, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+        return fail(Q4_EARG, "MLP workspace of this stream must grow during graph capture: "
+                             "run the largest call once on the stream before capturing");
+    HIP_TRY(hipStreamSynchronize(st));
+    (void)hipFree(ws.tmp);
+    ws.tmp = nullptr;
+    ws.cap_tmp = 0;
+    HIP_TRY(hipMalloc(&ws.tmp, n * sizeof(float)));
+    ws.cap_tmp = n;
+    return 0;
+}
 
 struct DevState {
     hipStream_t stream = nullptr;               // stream of the host-pointer calls
@@ -699,7 +750,10 @@ int ensure_ws(Workspace& ws, hipStream_t st, size_t words, size_t groups) {
     (void)hipFree(ws.planes);
     (void)hipFree(ws.xsum);
     (void)hipFree(ws.xscale);
-    ws = Workspace{};
+    ws.planes = nullptr;
+    ws.xsum = nullptr;
+    ws.xscale = nullptr;
+    ws.cap_words = ws.cap_groups = 0;
     size_t cw = words < 4096 ? 4096 : words, cg = groups < 1024 ? 1024 : groups;
     HIP_TRY(hipMalloc(&ws.planes, cw * sizeof(uint4)));
     HIP_TRY(hipMalloc(&ws.xsum, cg * sizeof(float)));
@@ -743,25 +797,25 @@ int num_cus() {
 
 constexpr size_t kStreamLdsMax = 160 * 1024;
 
-template <int MR, int VPT>
+template <int MR, int VPT, bool PAIR = false>
 int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st) {
-    auto kern = gemv_stream_kernel<MR, VPT>;
+    auto kern = gemv_stream_kernel<MR, VPT, PAIR>;
     const int G = n_in / (4 * VPT);
     const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
-    const int n_total = ml.row_begin[ml.count];
+    const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
     const int cus = num_cus();
     // 16 waves per workgroup when there are rows for a full grid of them,
     // else smaller workgroups so that every CU gets some
     int nwaves = 16;
-    while (nwaves > 4 && n_total < nwaves * cus) nwaves >>= 1;
+    while (nwaves > 4 && n_total * (PAIR ? 2 : 1) < nwaves * cus) nwaves >>= 1;
     // rows per unit: enough 1 KiB items per unit to fill a batch, more when
     // rows are plentiful
     int UB = 1;
-    while (UB < 4 && UB * C < kBatch && n_total >= 2 * UB * nwaves * cus) UB *= 2;
+    while (UB < 4 && UB * C * (PAIR ? 2 : 1) < kBatch && n_total >= 2 * UB * nwaves * cus) UB *= 2;
     while (MR * UB > 64) UB >>= 1;
     for (int k = 0; k < ml.count; k++)                 // a unit must not straddle matrices
         while (ml.n_out[k] % UB) UB >>= 1;
-    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, UB);
+    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB);
     if (lds > kStreamLdsMax) return 0;
     static bool attr_set = false;
     if (!attr_set) {
@@ -1147,6 +1201,72 @@ int q4_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const
         if ((rc = q4_gemv_dev(w[k], scales[k], biases[k], x, out[k], m, n_out[k], n_in, gs, stream)))
             return rc;
     return 0;
+}
+
+int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,
+                        const uint32_t* up_w, const uint16_t* up_s, const uint16_t* up_b,
+                        const float* x, float* h, int m, int n_inter, int n_in, int gs,
+                        void* stream) {
+    int rc = check_gemv_shape(n_inter, n_in, gs);
+    if (rc) return rc;
+    if (m < 0) return fail(Q4_EARG, "m=%d", m);
+    if (m == 0 || n_inter == 0) return 0;
+    if (!gate_w || !gate_s || !gate_b || !up_w || !up_s || !up_b || !x || !h)
+        return fail(Q4_EARG, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(gate_w) | reinterpret_cast<uintptr_t>(up_w)) & 15)
+        return fail(Q4_EARG, "w must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    for (int m0 = 0; m0 < m; m0 += 2) {
+        const int mm = m - m0 < 2 ? m - m0 : 2;
+        const float* xm = x + static_cast<size_t>(m0) * n_in;
+        float* hm = h + static_cast<size_t>(m0) * n_inter;
+        MatList ml{};
+        ml.w[0] = gate_w; ml.s[0] = gate_s; ml.b[0] = gate_b; ml.out[0] = hm; ml.n_out[0] = n_inter;
+        ml.w[1] = up_w;   ml.s[1] = up_s;   ml.b[1] = up_b;   ml.out[1] = hm; ml.n_out[1] = n_inter;
+        for (int k = 2; k < kMaxMats; k++) {
+            ml.w[k] = up_w; ml.s[k] = up_s; ml.b[k] = up_b; ml.out[k] = hm; ml.n_out[k] = 0;
+        }
+        ml.row_begin[0] = 0;
+        for (int k = 0; k < kMaxMats; k++) ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
+        ml.count = 2;
+        int done = 0;
+        if (gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
+            (n_in / 8 + kChunkWords - 1) / kChunkWords <= 16) {
+            done = mm == 1 ? launch_stream<1, 16, true>(ml, xm, n_in, st)
+                           : launch_stream<2, 16, true>(ml, xm, n_in, st);
+            if (done < 0) return done;
+        }
+        if (!done) {        // unfused: gate into h, up into the workspace, then SiLU * mul
+            Workspace* ws;
+            {
+                std::lock_guard<std::mutex> lock(g_mu);
+                int dev;
+                if ((rc = current_device(&dev))) return rc;
+                ws = &g_dev[dev].ws[st];
+            }
+            const size_t n = static_cast<size_t>(mm) * n_inter;
+            if ((rc = ensure_tmp(*ws, st, n))) return rc;
+            if ((rc = q4_gemv_dev(gate_w, gate_s, gate_b, xm, hm, mm, n_inter, n_in, gs, stream))) return rc;
+            if ((rc = q4_gemv_dev(up_w, up_s, up_b, xm, ws->tmp, mm, n_inter, n_in, gs, stream))) return rc;
+            hipLaunchKernelGGL(silu_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, st, hm, ws->tmp, hm,
+                               static_cast<long>(n));
+            HIP_TRY(hipGetLastError());
+        }
+    }
+    return 0;
+}
+
+int q4_mlp_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,
+               const uint32_t* up_w, const uint16_t* up_s, const uint16_t* up_b,
+               const uint32_t* down_w, const uint16_t* down_s, const uint16_t* down_b,
+               const float* x, float* h, float* out, int m, int n_hidden, int n_inter, int gs,
+               void* stream) {
+    int rc = check_gemv_shape(n_hidden, n_inter, gs);
+    if (rc) return rc;
+    if ((rc = q4_gate_up_silu_dev(gate_w, gate_s, gate_b, up_w, up_s, up_b, x, h, m, n_inter,
+                                  n_hidden, gs, stream)))
+        return rc;
+    return q4_gemv_dev(down_w, down_s, down_b, h, out, m, n_hidden, n_inter, gs, stream);
 }
 
 int q4_dequant_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,

@@ -20,8 +20,8 @@ PKG_PARENT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
 
 EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
-           "q4_last_error", "q4_gemv_dev", "q4_gemv_multi_dev", "q4_dequant_dev",
-           "q4_dequant_bf16_dev")
+           "q4_last_error", "q4_gemv_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
+           "q4_mlp_dev", "q4_dequant_dev", "q4_dequant_bf16_dev")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
@@ -47,6 +47,10 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_gemv_dev.restype = _I
         lib.q4_gemv_multi_dev.argtypes = [_I] + [_VP] * 6 + [_I] * 3 + [_VP]
         lib.q4_gemv_multi_dev.restype = _I
+        lib.q4_gate_up_silu_dev.argtypes = [_VP] * 8 + [_I] * 4 + [_VP]
+        lib.q4_gate_up_silu_dev.restype = _I
+        lib.q4_mlp_dev.argtypes = [_VP] * 12 + [_I] * 4 + [_VP]
+        lib.q4_mlp_dev.restype = _I
         lib.q4_dequant_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
         lib.q4_dequant_dev.restype = _I
         lib.q4_dequant_bf16_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
@@ -133,6 +137,39 @@ def gemv_multi_dev(mats, x, outs=None, stream=None, lib=None):
                                _ptr(x2), m, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gemv_multi_dev")
     return outs
+
+
+def gate_up_silu_dev(gate, up, x, h=None, stream=None, lib=None):
+    """h[m, n_inter] = SiLU(x @ gate^T) * (x @ up^T); gate/up = (w, scales, biases)."""
+    import torch
+    lib = lib or load()
+    n_inter, n_in = gate[0].shape[0], gate[0].shape[1] * 8
+    gs = n_in // gate[1].shape[1]
+    x2 = x.reshape(-1, n_in)
+    if h is None:
+        h = torch.empty((x2.shape[0], n_inter), dtype=torch.float32, device=x.device)
+    rc = lib.q4_gate_up_silu_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), _ptr(x2), _ptr(h),
+                                 x2.shape[0], n_inter, n_in, gs, _stream(stream))
+    check(lib, rc, "q4_gate_up_silu_dev")
+    return h
+
+
+def mlp_dev(gate, up, down, x, h=None, out=None, stream=None, lib=None):
+    """down(SiLU(gate(x)) * up(x)) for 4-bit (w, scales, biases) triples."""
+    import torch
+    lib = lib or load()
+    n_inter, n_hidden = gate[0].shape[0], gate[0].shape[1] * 8
+    gs = n_hidden // gate[1].shape[1]
+    x2 = x.reshape(-1, n_hidden)
+    m = x2.shape[0]
+    if h is None:
+        h = torch.empty((m, n_inter), dtype=torch.float32, device=x.device)
+    if out is None:
+        out = torch.empty((m, n_hidden), dtype=torch.float32, device=x.device)
+    rc = lib.q4_mlp_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), *(_ptr(t) for t in down),
+                        _ptr(x2), _ptr(h), _ptr(out), m, n_hidden, n_inter, gs, _stream(stream))
+    check(lib, rc, "q4_mlp_dev")
+    return out
 
 
 def dequant_dev(w, scales, biases, row0=0, row1=None, out=None, bf16=False, stream=None, lib=None):

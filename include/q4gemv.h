@@ -93,6 +93,27 @@ int q4_gemv_multi_dev(int count, const uint32_t *const *w, const uint16_t *const
                       const uint16_t *const *biases, float *const *out, const int *n_out,
                       const float *x, int m, int n_in, int gs, void *stream);
 
+/* Fused gate/up projection with SiLU * mul: h[m][n_inter] =
+ * SiLU(W_gate x) * (W_up x), SiLU(g) = g / (1 + exp(-g)) in fp32.  The gate
+ * and up rows are the q4_gemv results bit for bit; exp may differ from
+ * NumPy's float32 exp in the last place.  Replaces the first half of
+ * MLP.__call__, hetero/cpu_model.py:291-292 (two q4_gemv calls and the NumPy
+ * silu of :169-170).  Device pointers, asynchronous on `stream`. */
+int q4_gate_up_silu_dev(const uint32_t *gate_w, const uint16_t *gate_s, const uint16_t *gate_b,
+                        const uint32_t *up_w, const uint16_t *up_s, const uint16_t *up_b,
+                        const float *x, float *h, int m, int n_inter, int n_in, int gs,
+                        void *stream);
+
+/* The whole MLP block, hetero/cpu_model.py:291-292:
+ * out[m][n_hidden] = W_down (SiLU(W_gate x) * W_up x), with h[m][n_inter]
+ * as caller-provided scratch (it holds the SiLU * mul activations on
+ * return).  Two launches: the fused gate/up/SiLU one and the down GEMV. */
+int q4_mlp_dev(const uint32_t *gate_w, const uint16_t *gate_s, const uint16_t *gate_b,
+               const uint32_t *up_w, const uint16_t *up_s, const uint16_t *up_b,
+               const uint32_t *down_w, const uint16_t *down_s, const uint16_t *down_b,
+               const float *x, float *h, float *out, int m, int n_hidden, int n_inter, int gs,
+               void *stream);
+
 /* Device q4_dequant: rows [row0,row1) to fp32 [row1-row0][n_in]. */
 int q4_dequant_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
                    float *out, int row0, int row1, int n_in, int gs, void *stream);
