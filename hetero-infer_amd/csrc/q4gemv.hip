@@ -663,6 +663,152 @@ __global__ __launch_bounds__(256) void dequant_kernel(
     }
 }
 
+// ------------------------------------------------ prefill GEMM (bf16 MFMA) --
+//
+// out[M][N] = x[M][K] . W^T for the prompt (M > 16 rows), the contraction the
+// reference hands to BLAS after q4_dequant (hetero/cpu_model.py:119-136).
+// W is dequantised to bf16 inside the B-tile load (fma(q, scale, bias) in
+// fp32, rounded to nearest even: exactly q4_dequant_bf16), x is rounded to
+// bf16 in the A-tile load, and v_mfma_f32_32x32x16_bf16 accumulates in fp32.
+//   * tile BM x BN x 64 (one quantisation group per k-step, so each B row of
+//     a tile has one scale/bias pair), 4 waves as 2 x 2, each wave owning a
+//     (BM/2) x (BN/2) block of 32 x 32 MFMA tiles;
+//   * LDS double-buffered; the next tile's global loads are in flight while
+//     the current tile is multiplied;
+//   * blockIdx.x walks the M blocks: with 4 M blocks and WGs dealt round-robin
+//     to the 8 XCDs, each XCD keeps one M block of x in its L2 and the W tile
+//     of a column of workgroups is read by them back to back.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kGemmLdsK = 72;            // LDS row stride in bf16 (64 + 8 pad: conflict-free)
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    const __bf16 ha = static_cast<__bf16>(a), hb = static_cast<__bf16>(b);   // RNE
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+}
+
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
+    const float* __restrict__ x, const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
+    const uint16_t* __restrict__ bi, float* __restrict__ out, int M, int N, int K) {
+    extern __shared__ uint4 gemm_lds[];
+    uint16_t* As = reinterpret_cast<uint16_t*>(gemm_lds);          // [2][BM][72]
+    uint16_t* Bs = As + 2 * BM * kGemmLdsK;                        // [2][BN][72]
+    constexpr int TM = BM / 64, TN = BN / 64;                      // 32x32 tiles per wave
+    constexpr int A_PER = BM * 16 / 256;                           // float4 of x per thread
+    constexpr int B_PER = BN * 2 / 256;                            // uint4 of w per thread (may be < 1)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int G = K >> 6, wpr = K >> 3;
+
+    float4 ra[A_PER];
+    uint4 rb[B_PER > 0 ? B_PER : 1];
+    uint16_t rs[B_PER > 0 ? B_PER : 1], rbb[B_PER > 0 ? B_PER : 1];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < A_PER; i++) {
+            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
+            const int gm = m0 + row < M ? m0 + row : M - 1;
+            ra[i] = reinterpret_cast<const float4*>(x + static_cast<size_t>(gm) * K + 64 * kt)[c4];
+        }
+#pragma unroll
+        for (int i = 0; i < (B_PER > 0 ? B_PER : 1); i++) {
+            const int idx = tid + 256 * i, row = idx >> 1, half = idx & 1;
+            if (B_PER > 0 || row < BN) {
+                const int gn = n0 + row < N ? n0 + row : N - 1;
+                rb[i] = *reinterpret_cast<const uint4*>(w + static_cast<size_t>(gn) * wpr + 8 * kt + 4 * half);
+                rs[i] = sc[static_cast<size_t>(gn) * G + kt];
+                rbb[i] = bi[static_cast<size_t>(gn) * G + kt];
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_PER; i++) {
+            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
+            uint2 v;
+            v.x = pack_bf16x2(ra[i].x, ra[i].y);
+            v.y = pack_bf16x2(ra[i].z, ra[i].w);
+            *reinterpret_cast<uint2*>(As + (buf * BM + row) * kGemmLdsK + 4 * c4) = v;
+        }
+#pragma unroll
+        for (int i = 0; i < (B_PER > 0 ? B_PER : 1); i++) {
+            const int idx = tid + 256 * i, row = idx >> 1, half = idx & 1;
+            if (B_PER > 0 || row < BN) {
+                const float s = h2f(rs[i]), b = h2f(rbb[i]);
+                const uint32_t wd[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    // even values in the bytes of lo, odd ones in hi; v_cvt_f32_ubyteN
+                    // turns each byte into a float in one instruction
+                    const uint32_t lo = wd[t] & 0x0F0F0F0Fu, hi = (wd[t] >> 4) & 0x0F0F0F0Fu;
+                    float v[8];
+#pragma unroll
+                    for (int n = 0; n < 4; n++) {
+                        v[2 * n] = __builtin_fmaf(static_cast<float>((lo >> (8 * n)) & 0xFFu), s, b);
+                        v[2 * n + 1] = __builtin_fmaf(static_cast<float>((hi >> (8 * n)) & 0xFFu), s, b);
+                    }
+                    uint4 pk;
+                    pk.x = pack_bf16x2(v[0], v[1]); pk.y = pack_bf16x2(v[2], v[3]);
+                    pk.z = pack_bf16x2(v[4], v[5]); pk.w = pack_bf16x2(v[6], v[7]);
+                    *reinterpret_cast<uint4*>(Bs + (buf * BN + row) * kGemmLdsK + 32 * half + 8 * t) = pk;
+                }
+            }
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
+
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < G; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < G) gload(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            bf16x8 a[TM], bv[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int row = wm * (BM / 2) + i * 32 + (lane & 31);
+                a[i] = *reinterpret_cast<const bf16x8*>(As + (cur * BM + row) * kGemmLdsK + 16 * ks + 8 * (lane >> 5));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int row = wn * (BN / 2) + j * 32 + (lane & 31);
+                bv[j] = *reinterpret_cast<const bf16x8*>(Bs + (cur * BN + row) * kGemmLdsK + 16 * ks + 8 * (lane >> 5));
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bv[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < G) lstore(cur ^ 1);
+        __syncthreads();
+    }
+    // C tile layout: lane l, register v holds row 8*(v/4) + 4*(l/32) + v%4, column l%32
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+                if (row < M && col < N) out[static_cast<size_t>(row) * N + col] = acc[i][j][v];
+            }
+}
+
 // ============================================================ host side ===
 
 thread_local char g_err[512] = "";
@@ -1055,6 +1201,25 @@ int dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, void
     return 0;
 }
 
+
+template <int BM, int BN>
+int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x, float* out,
+                int M, int N, int K, hipStream_t st) {
+    auto kern = gemm_q4_bf16_kernel<BM, BN>;
+    const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
+        attr_set = true;
+    }
+    dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, x, w, s, b, out, M, N, K);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================ C-ABI ====
@@ -1267,6 +1432,30 @@ int q4_mlp_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* g
                                   n_hidden, gs, stream)))
         return rc;
     return q4_gemv_dev(down_w, down_s, down_b, h, out, m, n_hidden, n_inter, gs, stream);
+}
+
+
+int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                     const float* x, float* out, int m, int n_out, int n_in, int gs, void* stream) {
+    int rc = check_gemv_shape(n_out, n_in, gs);
+    if (rc) return rc;
+    if (gs != 64) return fail(Q4_EARG, "q4_gemm_bf16_dev takes gs = 64 (got %d)", gs);
+    if (m < 0) return fail(Q4_EARG, "m=%d", m);
+    if (m == 0 || n_out == 0) return 0;
+    if (!w || !scales || !biases || !x || !out) return fail(Q4_EARG, "null pointer");
+    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15)
+        return fail(Q4_EARG, "w and x must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (n_in == 0) {
+        const long n = static_cast<long>(m) * n_out;
+        hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st, out, n);
+        HIP_TRY(hipGetLastError());
+        return 0;
+    }
+    // 128 x 128 tiles once there are enough of them for the CUs, else 128 x 64
+    const long tiles128 = static_cast<long>((m + 127) / 128) * ((n_out + 127) / 128);
+    if (tiles128 >= 2L * num_cus()) return launch_gemm<128, 128>(w, scales, biases, x, out, m, n_out, n_in, st);
+    return launch_gemm<128, 64>(w, scales, biases, x, out, m, n_out, n_in, st);
 }
 
 int q4_dequant_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,

@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
 
 EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
            "q4_last_error", "q4_gemv_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
-           "q4_mlp_dev", "q4_dequant_dev", "q4_dequant_bf16_dev")
+           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_dequant_dev", "q4_dequant_bf16_dev")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
@@ -51,6 +51,8 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_gate_up_silu_dev.restype = _I
         lib.q4_mlp_dev.argtypes = [_VP] * 12 + [_I] * 4 + [_VP]
         lib.q4_mlp_dev.restype = _I
+        lib.q4_gemm_bf16_dev.argtypes = [_VP] * 5 + [_I] * 4 + [_VP]
+        lib.q4_gemm_bf16_dev.restype = _I
         lib.q4_dequant_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
         lib.q4_dequant_dev.restype = _I
         lib.q4_dequant_bf16_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
@@ -169,6 +171,21 @@ def mlp_dev(gate, up, down, x, h=None, out=None, stream=None, lib=None):
     rc = lib.q4_mlp_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), *(_ptr(t) for t in down),
                         _ptr(x2), _ptr(h), _ptr(out), m, n_hidden, n_inter, gs, _stream(stream))
     check(lib, rc, "q4_mlp_dev")
+    return out
+
+
+def gemm_bf16_dev(w, scales, biases, x, out=None, stream=None, lib=None):
+    """Prefill: out[m, n_out] = bf16(x) @ bf16(dequant(W))^T with fp32 accumulation."""
+    import torch
+    lib = lib or load()
+    n_out, n_in = w.shape[0], w.shape[1] * 8
+    gs = n_in // scales.shape[1]
+    x2 = x.reshape(-1, n_in)
+    if out is None:
+        out = torch.empty((x2.shape[0], n_out), dtype=torch.float32, device=x.device)
+    rc = lib.q4_gemm_bf16_dev(_ptr(w), _ptr(scales), _ptr(biases), _ptr(x2), _ptr(out),
+                              x2.shape[0], n_out, n_in, gs, _stream(stream))
+    check(lib, rc, "q4_gemm_bf16_dev")
     return out
 
 

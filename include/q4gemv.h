@@ -114,6 +114,17 @@ int q4_mlp_dev(const uint32_t *gate_w, const uint16_t *gate_s, const uint16_t *g
                const float *x, float *h, float *out, int m, int n_hidden, int n_inter, int gs,
                void *stream);
 
+/* Prefill contraction out[m][n_out] = x[m][n_in] . W^T for prompts (m >
+ * 16 rows): W dequantised to bf16 inside the tile load (the value of
+ * q4_dequant_bf16_dev), x rounded to bf16, fp32 accumulation on the matrix
+ * cores (v_mfma_f32_32x32x16_bf16).  Replaces QLinear._gemm,
+ * hetero/cpu_model.py:119-136 (512-row q4_dequant blocks + an fp32 BLAS
+ * sgemm); the result differs from it by bf16 rounding of both operands.
+ * gs must be 64; w and x 16-byte aligned. */
+int q4_gemm_bf16_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                     const float *x, float *out, int m, int n_out, int n_in, int gs,
+                     void *stream);
+
 /* Device q4_dequant: rows [row0,row1) to fp32 [row1-row0][n_in]. */
 int q4_dequant_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
                    float *out, int row0, int row1, int n_in, int gs, void *stream);
