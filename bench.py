@@ -57,6 +57,158 @@ def gemv_bytes(m, n_out, n_in):
     return n_out * n_in // 2 + 4 * n_out * (n_in // GS) + 4 * m * n_in + 4 * m * n_out
 
 
+def prefill_bench(torch, lib, layers, dev, reps=3):
+    """M=512 prompt over the 28 layers' projections: bf16 MFMA GEMM with the
+    dequant fused into the weight-tile load (q4_gemm_bf16_dev)."""
+    from hetero import q4
+    m = 512
+    xs = {k: torch.randn((m, k), device=dev) for k in (3584, 18944)}
+    outs = {n: torch.empty((m, n), device=dev) for n in (512, 3584, 18944)}
+    stream = torch.cuda.Stream(device=dev)
+    flops = 0
+
+    def step():
+        for layer in layers:
+            for w, s, b in layer:
+                n_out, n_in = w.shape[0], w.shape[1] * 8
+                rc = lib.q4_gemm_bf16_dev(w.data_ptr(), s.data_ptr(), b.data_ptr(), xs[n_in].data_ptr(),
+                                          outs[n_out].data_ptr(), m, n_out, n_in, GS, stream.cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"q4_gemm_bf16_dev rc={rc}: {q4.last_error(lib)}")
+
+    for layer in layers:
+        for w, _, _ in layer:
+            flops += 2 * m * w.shape[0] * w.shape[1] * 8
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        step()
+    with torch.cuda.stream(stream):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": "M=512 prompt, 28 layers x 7 projections (K/N of the decode sweep), "
+                        "group-64 dequant to bf16 fused into the weight-tile load, MFMA GEMM",
+            "ms": round(ms, 3), "tflops": round(tf, 1), "frac_mfma_peak": round(tf / 2500.0, 4),
+            "peak_tflops_bf16_dense": 2500.0, "flops": flops}
+
+
+def decode_weights(torch, cfg, dev, seed=99):
+    """Random-init 4-bit Qwen2 weights (reference tensor names), generated on
+    the GPU and copied to host arrays for the NumPy stage."""
+    import numpy as np
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    host = {}
+    h, inter, v = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"]
+    kvd = h // cfg["num_attention_heads"] * cfg["num_key_value_heads"]
+
+    def lin(name, n_out, n_in, bias=False):
+        w, s, b = make_weights(torch, gen, n_out, n_in, dev)
+        host[f"{name}.weight"] = w.cpu().numpy().view(np.uint32)
+        host[f"{name}.scales"] = s.cpu().numpy().view(np.float16)
+        host[f"{name}.biases"] = b.cpu().numpy().view(np.float16)
+        if bias:
+            host[f"{name}.bias"] = (torch.randn(n_out, device=dev, generator=gen) * 0.02).cpu().numpy()
+
+    lin("model.embed_tokens", v, h)
+    for i in range(cfg["num_hidden_layers"]):
+        p = f"model.layers.{i}"
+        lin(f"{p}.self_attn.q_proj", h, h, True)
+        lin(f"{p}.self_attn.k_proj", kvd, h, True)
+        lin(f"{p}.self_attn.v_proj", kvd, h, True)
+        lin(f"{p}.self_attn.o_proj", h, h)
+        lin(f"{p}.mlp.gate_proj", inter, h)
+        lin(f"{p}.mlp.up_proj", inter, h)
+        lin(f"{p}.mlp.down_proj", h, inter)
+        for nrm in ("input_layernorm", "post_attention_layernorm"):
+            host[f"{p}.{nrm}.weight"] = (1.0 + torch.randn(h, device=dev, generator=gen) * 0.02).cpu().numpy()
+    host["model.norm.weight"] = (1.0 + torch.randn(h, device=dev, generator=gen) * 0.02).cpu().numpy()
+    lin("lm_head", v, h)
+    kv_k = [(torch.randn((cfg["num_key_value_heads"], 2048, h // cfg["num_attention_heads"]),
+                         device=dev, generator=gen)).half().cpu().numpy() for _ in range(cfg["num_hidden_layers"])]
+    kv_v = [(torch.randn((cfg["num_key_value_heads"], 2048, h // cfg["num_attention_heads"]),
+                         device=dev, generator=gen)).half().cpu().numpy() for _ in range(cfg["num_hidden_layers"])]
+    return host, kv_k, kv_v
+
+
+def decode_bench(torch, dev, steps=128, start_token=151643, ref_rows=1, ref_threads=16):
+    """Qwen2.5-7B-architecture decode step (28 layers, fp16 KV cache at 2048
+    context, greedy over 152064): device-resident tok/s, and token agreement
+    with the NumPy stage running the reference kernel on the host."""
+    import copy
+    import numpy as np
+    from hetero import cpu_model
+    from hetero.gpu_model import GpuStage
+
+    cfg = cpu_model.qwen2_7b_config(28)
+    t0 = time.perf_counter()
+    w, kv_k, kv_v = decode_weights(torch, cfg, dev)
+    log(f"decode weights {time.perf_counter() - t0:.1f}s")
+    g = GpuStage(cfg, w, kv_k, kv_v, max_new=steps)
+    g.reset(start_token)
+    g.capture()
+    g.reset(start_token)
+    g.run(2)                                     # warm replays
+    g.reset(start_token)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dev_tokens = g.run(steps)
+    dev_s = time.perf_counter() - t0
+    res = {"workload": "Qwen2-architecture decode: 28 layers, hidden 3584, 28/4 heads, head_dim 128, "
+                       "random-init 4-bit weights, fp16 KV cache at 2048 context, greedy over 152064, "
+                       f"{steps} steps, one HIP graph replay per token",
+           "tok_s": round(steps / dev_s, 1), "ms_per_token": round(dev_s * 1e3 / steps, 3)}
+    ref = reference_decode(cfg, w, kv_k, kv_v, steps, start_token, ref_rows, ref_threads)
+    if ref is not None:
+        ref_tokens, ref_s = ref
+        free = sum(int(a == b) for a, b in zip(dev_tokens, ref_tokens))
+        prefix = next((i for i, (a, b) in enumerate(zip(dev_tokens, ref_tokens)) if a != b), steps)
+        g.reset(start_token)
+        forced = g.generate(steps, tokens_in=[start_token] + ref_tokens[:-1])
+        tf = sum(int(a == b) for a, b in zip(forced, ref_tokens))
+        res.update({"agree_free_running": f"{free}/{steps}", "identical_prefix": prefix,
+                    "agree_teacher_forced": f"{tf}/{steps}",
+                    "cpu_reference_tok_s": round(steps / ref_s, 2),
+                    "cpu_reference": f"NumPy stage (hetero/cpu_model.py) on kernel/q4gemv.c ROWS={ref_rows}, "
+                                     f"{ref_threads} threads"})
+    return res
+
+
+def reference_decode(cfg, w, kv_k, kv_v, steps, start_token, rows, threads):
+    """The same 128 greedy steps by the NumPy stage on the reference kernel
+    compiled from source (host CPU baseline and token oracle)."""
+    import numpy as np
+    import oracle
+    from hetero import cpu_model
+    if not os.path.exists(oracle.ref_path(rows)):
+        return None
+    os.environ.setdefault("HETERO_KERNEL_THREADS", str(max(threads, 1)))
+    cpu_model.NTHREADS = threads
+    stage = cpu_model.Stage(cfg, w, lib=oracle.load_ref(rows))
+    caches = []
+    for k, v in zip(kv_k, kv_v):
+        c = cpu_model.KVCache(np.float16)
+        c.fill(k[None], v[None])
+        caches.append(c)
+    tok, out = start_token, []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        logits = stage(np.array([[tok]]), caches, last_only=True)
+        tok = cpu_model.greedy(logits)
+        out.append(tok)
+    return out, time.perf_counter() - t0
+
+
 def cpu_baseline(budget_s: float = 20.0):
     """Reference kernel/q4gemv.c on this host, tuned as kernel/autotune.py does."""
     import ctypes
@@ -128,7 +280,7 @@ def cpu_baseline(budget_s: float = 20.0):
         + gemv_bytes(1, HEAD_SHAPE[2], HEAD_SHAPE[1])
     t_sweep = LAYERS * t_layer + t_head
     return {"value": round(sweep_bytes / t_sweep / 1e9, 3), "unit": "GB/s", "cores": nt,
-            "kind": "reference",
+            "kind": "reference", "rows": rows,
             "sample": (f"kernel/q4gemv.c (clang -O3 -mavx2 -mfma -mf16c, ROWS={rows}, "
                        f"{nt} threads, tuned over ROWS 1/2/4/8 x threads {threads_opts} in "
                        f"{tune_s:.1f}s) on {cpus} host cpus: {reps} passes over one layer's 7 "
@@ -145,6 +297,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the int4 GEMV path "
@@ -299,11 +454,23 @@ def main():
                                     "GB_s": round(sweep_bytes / (calls_ms * 1e-3) / 1e9, 1),
                                     "launches_per_step": LAYERS * len(LAYER_SHAPES) + 1},
     }
+    if not args.no_prefill:
+        log("prefill ...")
+        result["prefill"] = prefill_bench(torch, lib, layers, dev)
+    rows, threads = 1, 16
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(args.cpu_budget)
+        rows = result["cpu_baseline"].get("rows", 1) or 1
+        threads = result["cpu_baseline"].get("cores", 16) or 16
     else:
         result["cpu_baseline"] = None
+    if not args.no_decode:
+        del layers, head
+        torch.cuda.empty_cache()
+        log("decode ...")
+        result["decode"] = decode_bench(torch, dev, steps=args.decode_steps, ref_rows=rows,
+                                        ref_threads=threads)
     print(json.dumps(result), flush=True)
 
 

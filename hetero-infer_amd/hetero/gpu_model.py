@@ -93,6 +93,7 @@ class GpuStage:
         self.logits = torch.zeros((1, cfg["vocab_size"]), dtype=torch.float32, device=dev)
         self.emb_rows = [torch.zeros((1,) + tuple(a.shape[1:]), dtype=a.dtype, device=dev) for a in self.embed]
         self.positions = torch.arange(self.cap, device=dev)
+        self.hist = torch.zeros(max_new, dtype=torch.int64, device=dev)   # token of each step
         self.stream = torch.cuda.Stream(device=dev)
         self.graph = None
 
@@ -151,6 +152,7 @@ class GpuStage:
         xn = self._rms(x, self.norm_w).contiguous()
         q4.gemv_dev(*self.lm_head, xn, out=self.logits, lib=lib)
         self.tok.copy_(self.logits.argmax(dim=-1))                      # backends.py:106-109
+        self.hist.index_copy_(0, (self.pos - self.s0).clamp_(0, self.hist.numel() - 1), self.tok)
         self.pos.add_(1)
 
     # -- driving --------------------------------------------------------------
@@ -177,6 +179,20 @@ class GpuStage:
 
     def set_token(self, tok: int):
         self.tok.fill_(int(tok))
+
+    def reset(self, tok: int):
+        """Back to the initial context (positions past it are masked and
+        rewritten as decoding proceeds) with `tok` as the next input."""
+        self.pos.fill_(self.s0)
+        self.tok.fill_(int(tok))
+
+    def run(self, n: int) -> List[int]:
+        """n free-running steps as back-to-back graph replays (no host sync in
+        between); returns the n greedy tokens."""
+        for _ in range(n):
+            self.graph.replay()
+        self.torch.cuda.synchronize()
+        return self.hist[:n].tolist()
 
     def step(self) -> int:
         """One decode step (graph replay once captured); returns the greedy token."""
