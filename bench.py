@@ -53,6 +53,22 @@ def make_weights(torch, gen, n_out, n_in, dev):
     return w, s.view(torch.int16), b.view(torch.int16)
 
 
+PMC_SUMMARY = os.path.join("profiles", "gemv_stream_qwen7b_decode_sweep_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per sweep launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (counter values scaled by a 256 MiB copy), or None when the summary is absent."""
+    try:
+        with open(os.path.join(ROOT, PMC_SUMMARY)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def gemv_bytes(m, n_out, n_in):
     return n_out * n_in // 2 + 4 * n_out * (n_in // GS) + 4 * m * n_in + 4 * m * n_out
 
@@ -300,6 +316,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="only the grouped decode sweep (for rocprof runs)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run a 256 MiB device copy: the known-size reference for PMC byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the int4 GEMV path "
@@ -394,11 +414,18 @@ def main():
     ms_per_step, ev_ms = timed(step_grouped, args.steps, args.warmup)
     n_launch = LAYERS * 4 + 1
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
-    calls_ms, _ = timed(step_calls, max(3, args.steps // 2), 1)
+    calls_ms = float("nan") if args.sweep_only else timed(step_calls, max(3, args.steps // 2), 1)[0]
 
+    if args.calibrate:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     # per-shape: 28 back-to-back calls on distinct weights (lm_head: 4 calls, 307 MB each)
     per_shape = {}
-    for j, (name, n_in, n_out) in enumerate(LAYER_SHAPES + [HEAD_SHAPE]):
+    for j, (name, n_in, n_out) in enumerate([] if args.sweep_only else LAYER_SHAPES + [HEAD_SHAPE]):
         items = [layers[l][j] for l in range(LAYERS)] if j < len(LAYER_SHAPES) else [head] * 4
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
@@ -445,7 +472,9 @@ def main():
                    "parallelism": "single GPU"},
         "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(), "traffic_source": PMC_SUMMARY,
+                     "algorithmic_bytes_per_launch": round(sweep_bytes / n_launch),
                      "kernel": "gemv_stream_kernel<1,16> (x prologue fused), averaged over the "
                                "launches of the grouped sweep",
                      "avg_launch_us": round(ev_ms * 1e3 / n_launch, 3)},
@@ -454,6 +483,8 @@ def main():
                                     "GB_s": round(sweep_bytes / (calls_ms * 1e-3) / 1e9, 1),
                                     "launches_per_step": LAYERS * len(LAYER_SHAPES) + 1},
     }
+    if args.sweep_only:
+        args.no_prefill = args.no_cpu_baseline = args.no_decode = True
     if not args.no_prefill:
         log("prefill ...")
         result["prefill"] = prefill_bench(torch, lib, layers, dev)
