@@ -332,23 +332,34 @@ __global__ void gemv_generic_kernel(
 // ---------------------------------------------- streaming single-launch GEMV --
 //
 // One launch per call; weights are streamed row-contiguously (a wave-load
-// moves 1 KiB of one row: 64 lanes x 16 bytes):
-//   * the x prologue runs once per workgroup: 4 threads per group load x
-//     (before any weight load, so they are not queued behind HBM traffic),
-//     chain the group sum in ascending order and find amax; after one
-//     barrier they quantise their own values into int8/uint8 planes in LDS;
-//   * after that every wave works alone on units of UB consecutive rows.  A
-//     unit is a list of (chunk, row) items of 1 KiB each, streamed in
-//     batches of kBatch with the next batch (or the next unit's first batch)
-//     in flight while the current one is computed;
-//   * each group's fp32 term goes to a wave-private LDS table; when a unit
+// moves 1 KiB of one row: 64 lanes x 16 bytes).  Group size 64.
+//   * The x prologue runs once per workgroup.  Every x load is issued before
+//     the first weight load and x is read once: vector-memory results return
+//     in issue order, so an x load issued behind the weight stream would wait
+//     for it.  Each thread loads whole packed words (8 values), stages them
+//     in LDS and takes amax; after one barrier one thread per group chains
+//     the group sum in ascending order from LDS while every thread writes
+//     the int8/uint8 planes of its words of the int16 x into LDS.
+//   * Then every wave works alone on a flat stream of 1 KiB items: the items
+//     of its units (UB consecutive rows; PAIR: UB rows of matrix 0 and the
+//     same UB rows of matrix 1), chunk-major within a unit so consecutive
+//     items share x planes.  A ring of RING items is in flight (the host
+//     picks RING no larger than any working wave's item count): the item
+//     RING ahead is issued right after an item is consumed, from straight-
+//     line code while every refill is live, so each wait is a partial
+//     vmcnt; the last 1..2*RING items run through a tail with conditional
+//     refills, so nothing past the wave's last item is ever loaded.  Lanes
+//     past a row end read through a buffer range that ends with the row:
+//     0, no memory access.
+//   * Each group's fp32 term goes to a wave-private LDS table; when a unit
 //     is done one lane per (m, row) adds its row's terms in ascending group
 //     order -- no workgroup barrier in the main loop.
 // The row a wave works on is wave-uniform (kept in SGPRs), so choosing the
 // matrix of a grouped launch (q/k/v, gate/up: up to kMaxMats sharing x) is
 // scalar work.
 constexpr int kMaxMats = 4;
-constexpr int kBatch = 4;
+constexpr int kEarly = 2;           // ring items issued before the x prologue has its data
+constexpr int kUnitItems = 4;       // rows per unit grow until a unit has this many items
 
 struct MatList {
     const uint32_t* w[kMaxMats];
@@ -365,11 +376,17 @@ struct MatList {
 // the banks.
 __host__ __device__ inline int term_stride(int G) { return ((G + 3) & ~3) | 4; }
 
+// Staged x floats: group g of row m at (m*G + g) * kStageStride floats, so
+// the 16-byte reads of one lane per group land on distinct banks.
+constexpr int kStageStride = 68;
+
 size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU) {
+    const size_t terms = static_cast<size_t>(nwaves) * mr * NU * term_stride(G) * 4;
+    const size_t stage = static_cast<size_t>(mr) * G * kStageStride * 4;
     return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
          + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
          + static_cast<size_t>(mr) * 16 * 4                              // amax per wave
-         + static_cast<size_t>(nwaves) * mr * NU * term_stride(G) * 4;  // term tables
+         + (terms > stage ? terms : stage);                              // term tables | staged x
 }
 
 __device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
@@ -379,41 +396,75 @@ __device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
     return p;
 }
 
-struct Batch {
-    uint4 w[kBatch];
-    uint16_t s[kBatch], b[kBatch];
+// x[p] for a wave-uniform p in an SGPR, as scalar compare/selects in asm: a
+// select written in C++ is folded back into an indexed kernel-argument load,
+// which puts a scalar memory round trip in front of every weight load.
+__device__ __forceinline__ uint64_t sel4(int p, uint64_t a0, uint64_t a1, uint64_t a2, uint64_t a3) {
+    uint64_t r;
+    asm volatile(
+        "s_cmp_eq_u32 %1, 1\n\t"
+        "s_cselect_b64 %0, %3, %2\n\t"
+        "s_cmp_eq_u32 %1, 2\n\t"
+        "s_cselect_b64 %0, %4, %0\n\t"
+        "s_cmp_eq_u32 %1, 3\n\t"
+        "s_cselect_b64 %0, %5, %0"
+        : "=&s"(r) : "s"(p), "s"(a0), "s"(a1), "s"(a2), "s"(a3) : "scc");
+    return r;
+}
+__device__ __forceinline__ int sel4(int p, int a0, int a1, int a2, int a3) {
+    int r;
+    asm volatile(
+        "s_cmp_eq_u32 %1, 1\n\t"
+        "s_cselect_b32 %0, %3, %2\n\t"
+        "s_cmp_eq_u32 %1, 2\n\t"
+        "s_cselect_b32 %0, %4, %0\n\t"
+        "s_cmp_eq_u32 %1, 3\n\t"
+        "s_cselect_b32 %0, %5, %0"
+        : "=&s"(r) : "s"(p), "s"(a0), "s"(a1), "s"(a2), "s"(a3) : "scc");
+    return r;
+}
+template <typename T>
+__device__ __forceinline__ T* pick(T* const (&a)[kMaxMats], int p) {
+    return reinterpret_cast<T*>(sel4(p, reinterpret_cast<uint64_t>(a[0]), reinterpret_cast<uint64_t>(a[1]),
+                                     reinterpret_cast<uint64_t>(a[2]), reinterpret_cast<uint64_t>(a[3])));
+}
+
+struct Item {
+    uint4 w;
+    uint16_t s, b;
 };
 
-// Issue the loads of items [i0, i0 + kBatch) of unit `unit`.  A unit is
-// NU = UB rows (PAIR: UB rows of matrix 0 and the same UB rows of matrix 1);
-// item = c*NU + r, chunk-major so consecutive items share x planes.
-// Everything here is wave-uniform except the lane's word offset.  Loads are
-// unconditional from clamped, always-valid addresses: lanes past the row end
-// (whole groups) and rows past the end load data that no leader ever turns
-// into a term.
+// Raw buffer resource over [p, p + bytes): loads at an offset >= bytes
+// return 0 without a memory access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+constexpr uint32_t kOutOfRange = 0x80000000u;   // any offset past every resource here
+
+// Issue the loads of item (chunk c, row slot r) of unit `unit`.  The row is
+// wave-uniform: each array gets a resource over that row alone, so lanes
+// past the row end read 0 and cost no memory access, and `live` false (a
+// prefetch past the wave's last item) gives an empty resource: every lane
+// reads 0.  No branch, so the waits on earlier loads stay exact.
 template <bool PAIR>
-__device__ __forceinline__ void load_batch(Batch& bt, const MatList& ml, int unit, int i0, int UB,
-                                           int C, int n_total, int wpr, int G, int lane, int wpg) {
-    const int NU = PAIR ? 2 * UB : UB;
-#pragma unroll
-    for (int k = 0; k < kBatch; k++) {
-        int item = i0 + k;
-        item = item < NU * C ? item : NU * C - 1;
-        const int c = item / NU, r = item - c * NU;
-        const int u = PAIR ? (r < UB ? r : r - UB) : r;
-        int gr = unit * UB + u;
-        gr = gr < n_total ? gr : n_total - 1;
-        // p is wave-uniform; readfirstlane makes that explicit, so the
-        // kernel-argument reads below are scalar loads
-        const int p = __builtin_amdgcn_readfirstlane(PAIR ? (r < UB ? 0 : 1) : mat_of_row(ml, gr));
-        const int o = PAIR ? gr : gr - ml.row_begin[p];
-        const int word0 = c * kChunkWords + lane * 4;
-        const int wc = word0 < wpr ? word0 : wpr - 4;              // wpr >= 8
-        const int g = wc / wpg;
-        bt.w[k] = *reinterpret_cast<const uint4*>(ml.w[p] + static_cast<size_t>(o) * wpr + wc);
-        bt.s[k] = ml.s[p][static_cast<size_t>(o) * G + g];
-        bt.b[k] = ml.b[p][static_cast<size_t>(o) * G + g];
-    }
+__device__ __forceinline__ void load_item(Item& it, const MatList& ml, int unit, int c, int r, int UB,
+                                          int n_total, int wpr, int G, int lane, bool live) {
+    const int u = PAIR ? (r < UB ? r : r - UB) : r;
+    int gr = unit * UB + u;
+    gr = gr < n_total ? gr : n_total - 1;
+    // p is wave-uniform; readfirstlane makes that explicit, so the
+    // kernel-argument reads below are scalar loads
+    const int p = __builtin_amdgcn_readfirstlane(PAIR ? (r < UB ? 0 : 1) : mat_of_row(ml, gr));
+    const int o = __builtin_amdgcn_readfirstlane(
+        PAIR ? gr : gr - sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2], ml.row_begin[3]));
+    const uint32_t wbytes = live ? static_cast<uint32_t>(wpr) * 4u : 0u;
+    const uint32_t gbytes = live ? static_cast<uint32_t>(G) * 2u : 0u;
+    const int word0 = c * kChunkWords + lane * 4;
+    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+        buf_rsrc(pick(ml.w, p) + static_cast<size_t>(o) * wpr, wbytes), word0 * 4, 0, 0));
+    const int go = (word0 >> 3) * 2;
+    it.s = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(pick(ml.s, p) + static_cast<size_t>(o) * G, gbytes), go, 0, 0);
+    it.b = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(pick(ml.b, p) + static_cast<size_t>(o) * G, gbytes), go, 0, 0);
 }
 
 // Sequential fp32 sum of n terms (ascending), four 16-byte LDS reads in flight.
@@ -440,15 +491,21 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
 }
 
-// VPT = gs / 4 values per prologue thread (gs = 64 or 128).
-// PAIR: matrices 0 and 1 (gate, up) are computed row for row and the
-// output is out[0] = SiLU(gate) * up.
-template <int MR, int VPT, bool PAIR>
+// Words of x per thread and activation row that the word pass keeps in
+// registers (RW rounds of blockDim.x words); the host picks the instance.
+template <int MR>
+__host__ __device__ constexpr int stream_max_rounds() { return MR == 1 ? 4 : 2; }
+
+// PAIR: matrices 0 and 1 (gate, up) are computed row for row and the output
+// is out[0] = SiLU(gate) * up.
+// Host guarantees: MR * (n_in / 64) <= blockDim.x (one thread per group
+// item), chunks * 256 <= RW * blockDim.x, n_in % 64 == 0, x 16-byte aligned.
+template <int MR, int RW, bool PAIR, int RING>
 __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const float* __restrict__ x,
                                                           int n_in, int UB) {
     extern __shared__ uint4 lds4[];
-    constexpr int gs = 4 * VPT, lpg = gs / 32, wpg = gs / 8;
-    const int wpr = n_in >> 3, G = n_in / gs;
+    constexpr int lpg = 2;                                        // lanes per group
+    const int wpr = n_in >> 3, G = n_in >> 6;
     const int C = (wpr + kChunkWords - 1) / kChunkWords;
     const int Gr = (G + 3) & ~3, Ts = term_stride(G);
     const int tid = threadIdx.x, nt = blockDim.x;
@@ -464,46 +521,91 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     const int n_units = (n_total + UB - 1) / UB;
     const int tw = gridDim.x * nwaves;
     const int items = NU * C;
-    // ---- prologue pass 1 (x loads first): one thread per group loads its
-    //      gs values, adds them in order (kernel/q4gemv.c:244-248) and keeps
-    //      the running max |x| (:258-259).
+
+    // ---- x loads: thread t owns words t, t + nt, ... of every row, 8 values
+    //      each, through a resource over x (words at or past the row end read
+    //      0); waves with no word in a round issue nothing.  These are the
+    //      first loads of the kernel, so the waits further down stay exact.
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(MR * n_in) * 4u);
+    float4 wv[MR][RW][2];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+            if (r * nt + wave * 64 < wpr) {                       // uniform
+                const int j = r * nt + tid;
+                const uint32_t off = j < wpr ? static_cast<uint32_t>(m * n_in + 8 * j) * 4u : kOutOfRange;
+                wv[m][r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+                wv[m][r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+            }
+
+    // ---- the wave's item stream: units gw, gw + tw, ...; item i of a unit
+    //      is (chunk i / NU, row slot i % NU).  Up to kEarly items are
+    //      issued now, the rest of the ring once x is in: a full ring from
+    //      every wave at once would queue ahead of the x loads of later
+    //      waves.  A wave without units loads through empty ranges.
+    const int gw = blockIdx.x * nwaves + wave;
+    const int nu_w = gw < n_units ? (n_units - gw + tw - 1) / tw : 0;
+    const int Q = nu_w * items;
+    constexpr int kE = RING < kEarly ? RING : kEarly;
+    Item ring[RING];
+    int pf_unit = gw, pf_c = 0, pf_r = 0, pf_q = 0;               // prefetch cursor (uniform)
+#pragma unroll
+    for (int d = 0; d < kE; d++) {
+        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, pf_q < Q);
+        pf_q++;
+        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+    }
+
+    // ---- stage the floats in LDS (the term tables' space, free until the
+    //      main loop) and take the running max |x| (kernel/q4gemv.c:258-259,
+    //      NaN-skipping) per row
+    float* stage = red + MR * 16;
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-        const float* xr = x + static_cast<size_t>(m) * n_in;
         float amax = 0.0f;
-        for (int base = 0; base < G; base += nt) {                 // uniform trip count
-            const int gg = base + tid;
-            const int gc = gg < G ? gg : G - 1;                    // duplicate: no effect on amax
-            float sum = 0.0f;
 #pragma unroll
-            for (int h = 0; h < gs / 64; h++) {
-                float4 f[16];
-#pragma unroll
-                for (int i = 0; i < 16; i++)
-                    f[i] = reinterpret_cast<const float4*>(xr + gs * gc + 64 * h)[i];
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    sum = __fadd_rn(sum, f[i].x); sum = __fadd_rn(sum, f[i].y);
-                    sum = __fadd_rn(sum, f[i].z); sum = __fadd_rn(sum, f[i].w);
-                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(f[i].x), fabsf(f[i].y)),
-                                             fmaxf(fabsf(f[i].z), fabsf(f[i].w))));
+        for (int r = 0; r < RW; r++)
+            if (r * nt + wave * 64 < wpr) {                       // uniform
+                const int j = r * nt + tid;
+                if (j < wpr) {
+                    float4* dst = reinterpret_cast<float4*>(stage + (m * G + (j >> 3)) * kStageStride + 8 * (j & 7));
+                    dst[0] = wv[m][r][0];
+                    dst[1] = wv[m][r][1];
                 }
+                const float4 a = wv[m][r][0], b = wv[m][r][1];  // 0 past the row end
+                amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
             }
-            if (gg < G) xsum_lds[m * Gr + gg] = sum;
-        }
         amax = wave_max(amax);
         if (lane == 0) red[m * 16 + wave] = amax;
     }
-
-    // first batch of this wave's first unit is in flight during the rest of
-    // the prologue
-    const int gw = blockIdx.x * nwaves + wave;
-    Batch cur;
-    if (gw < n_units) load_batch<PAIR>(cur, ml, gw, 0, UB, C, n_total, wpr, G, lane, wpg);
-
+#pragma unroll
+    for (int d = kE; d < RING; d++) {
+        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, pf_q < Q);
+        pf_q++;
+        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+    }
     __syncthreads();
-    // ---- prologue pass 2: one thread per word: int16 x (kernel/q4gemv.c:
-    //      260-270) as byte planes in LDS; words past the row end are zero
+
+    // ---- group sums: one thread per (row, group) chains its 64 values in
+    //      ascending order (kernel/q4gemv.c:244-248)
+    if (tid < MR * G) {
+        const float4* gp = reinterpret_cast<const float4*>(stage + tid * kStageStride);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i0 = 0; i0 < 16; i0 += 4) {
+            const float4 v0 = gp[i0], v1 = gp[i0 + 1], v2 = gp[i0 + 2], v3 = gp[i0 + 3];
+            const float vals[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                                    v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) sum = __fadd_rn(sum, vals[i]);
+        }
+        const int m = tid / G;
+        xsum_lds[m * Gr + (tid - m * G)] = sum;
+    }
+
+    // ---- int16 x (kernel/q4gemv.c:260-270) as byte planes in LDS
     float xsc[MR];
 #pragma unroll
     for (int m = 0; m < MR; m++) {
@@ -512,99 +614,125 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
         xsc[m] = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;        // kernel/q4gemv.c:260
         const float inv = __fdiv_rn(1.0f, xsc[m]);                 // :261
         const bool exact_clamp = __builtin_isinf(inv);
-        const float* xr = x + static_cast<size_t>(m) * n_in;
-        for (int j = tid; j < C * 256; j += nt) {
-            uint4 pl = make_uint4(0, 0, 0, 0);
-            if (j < wpr) {
-                const float4 v0 = reinterpret_cast<const float4*>(xr + 8 * j)[0];
-                const float4 v1 = reinterpret_cast<const float4*>(xr + 8 * j)[1];
-                const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-                pl = quant_word(vv, inv, exact_clamp);
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int j = r * nt + tid;
+            if (r * nt + wave * 64 < C * kChunkWords) {           // uniform
+                uint4 pl = make_uint4(0, 0, 0, 0);
+                if (r * nt + wave * 64 < wpr) {                   // uniform
+                    const float vv[8] = {wv[m][r][0].x, wv[m][r][0].y, wv[m][r][0].z, wv[m][r][0].w,
+                                         wv[m][r][1].x, wv[m][r][1].y, wv[m][r][1].z, wv[m][r][1].w};
+                    pl = exact_clamp ? quant_word(vv, inv, true) : quant_word(vv, inv, false);
+                    if (j >= wpr) pl = make_uint4(0, 0, 0, 0);
+                }
+                const int cc = j >> 8, jj = j & 255;
+                xpl[(m * C + cc) * 256 + (jj & 3) * 64 + (jj >> 2)] = pl;
             }
-            const int cc = j >> 8, jj = j & 255;
-            xpl[(m * C + cc) * 256 + (jj & 3) * 64 + (jj >> 2)] = pl;
         }
     }
     __syncthreads();
 
-    // ---- main loop: each wave streams its own row units
-    for (int unit = gw; unit < n_units; unit += tw) {
-        int cprev = -1;
-        uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
-        for (int i0 = 0; i0 < items; i0 += kBatch) {
-            Batch nxt;
-            if (i0 + kBatch < items)
-                load_batch<PAIR>(nxt, ml, unit, i0 + kBatch, UB, C, n_total, wpr, G, lane, wpg);
-            else if (unit + tw < n_units)
-                load_batch<PAIR>(nxt, ml, unit + tw, 0, UB, C, n_total, wpr, G, lane, wpg);
+    // ---- main loop: consume the ring, refill each slot RING items ahead
+    int cu_unit = gw, cu_c = 0, cu_r = 0;                         // consume cursor (uniform)
+    int cprev = -1;
+    uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
+    auto consume = [&](const Item& itm) {
+        const int c = cu_c, u = cu_r;
+        const int word0 = c * kChunkWords + lane * 4;
+        const bool lead = word0 < wpr && (lane & (lpg - 1)) == lpg - 1;
+        const int g = word0 >> 3;
+        if (c != cprev) {                                 // uniform: planes of chunk c
 #pragma unroll
-            for (int k = 0; k < kBatch; k++) {
-                const int item = i0 + k;
-                if (item >= items) break;                           // uniform
-                const int c = item / NU, u = item - c * NU;       // u: row slot in the unit
-                const int word0 = c * kChunkWords + lane * 4;
-                const bool lead = word0 < wpr && (lane & (lpg - 1)) == lpg - 1;
-                const int g = word0 / wpg;
-                if (c != cprev) {                                   // uniform: planes of chunk c
-#pragma unroll
-                    for (int m = 0; m < MR; m++)
-#pragma unroll
-                        for (int t = 0; t < 4; t++) {
-                            const uint4 pl = xpl[(m * C + c) * 256 + t * 64 + lane];
-                            xle[m][t] = pl.x; xlo[m][t] = pl.y; xhe[m][t] = pl.z; xho[m][t] = pl.w;
-                        }
-                    cprev = c;
-                }
-                const uint32_t wd[4] = {cur.w[k].x, cur.w[k].y, cur.w[k].z, cur.w[k].w};
-                uint32_t lo4[4], hi4[4];
+            for (int m = 0; m < MR; m++)
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    lo4[t] = wd[t] & 0x0F0F0F0Fu;          // values 8j+0,2,4,6
-                    hi4[t] = (wd[t] >> 4) & 0x0F0F0F0Fu;   // values 8j+1,3,5,7
+                    const uint4 pl = xpl[(m * C + c) * 256 + t * 64 + lane];
+                    xle[m][t] = pl.x; xlo[m][t] = pl.y; xhe[m][t] = pl.z; xho[m][t] = pl.w;
                 }
-                const float sf = h2f(cur.s[k]), bf = h2f(cur.b[k]);
-#pragma unroll
-                for (int m = 0; m < MR; m++) {
-                    int ah = 0;
-                    uint32_t al = 0;
-#pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        ah = __builtin_amdgcn_sdot4(static_cast<int>(lo4[t]), static_cast<int>(xhe[m][t]), ah, false);
-                        ah = __builtin_amdgcn_sdot4(static_cast<int>(hi4[t]), static_cast<int>(xho[m][t]), ah, false);
-                        al = __builtin_amdgcn_udot4(lo4[t], xle[m][t], al, false);
-                        al = __builtin_amdgcn_udot4(hi4[t], xlo[m][t], al, false);
-                    }
-                    const int part = group_sum(static_cast<int>(static_cast<uint32_t>(ah) * 256u + al), lpg);
-                    if (lead) {
-                        const float dot = __fmul_rn(xsc[m], static_cast<float>(part));
-                        const float bx = __fmul_rn(bf, xsum_lds[m * Gr + g]);
-                        Tw[(m * NU + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
-                    }
-                }
-            }
-            cur = nxt;
+            cprev = c;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        if (lane < MR * UB) {
-            const int m = lane / UB, u = lane - m * UB, gr = unit * UB + u;
-            if (gr < n_total) {
-                const float acc = chain_sum(Tw + (m * NU + u) * Ts, G);
-                if constexpr (PAIR) {
-                    const float up = chain_sum(Tw + (m * NU + UB + u) * Ts, G);
-                    ml.out[0][static_cast<size_t>(m) * ml.n_out[0] + gr] = silu_mul(acc, up);
-                } else {
-                    // the host picks UB dividing every n_out, so a unit never
-                    // straddles two matrices and p is wave-uniform
-                    const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
-                    ml.out[p][static_cast<size_t>(m) * ml.n_out[p] + (gr - ml.row_begin[p])] = acc;
-                }
+        const uint32_t wd[4] = {itm.w.x, itm.w.y, itm.w.z, itm.w.w};
+        uint32_t lo4[4], hi4[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            lo4[t] = wd[t] & 0x0F0F0F0Fu;          // values 8j+0,2,4,6
+            hi4[t] = (wd[t] >> 4) & 0x0F0F0F0Fu;   // values 8j+1,3,5,7
+        }
+        const float sf = h2f(itm.s), bf = h2f(itm.b);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            int ah = 0;
+            uint32_t al = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                ah = __builtin_amdgcn_sdot4(static_cast<int>(lo4[t]), static_cast<int>(xhe[m][t]), ah, false);
+                ah = __builtin_amdgcn_sdot4(static_cast<int>(hi4[t]), static_cast<int>(xho[m][t]), ah, false);
+                al = __builtin_amdgcn_udot4(lo4[t], xle[m][t], al, false);
+                al = __builtin_amdgcn_udot4(hi4[t], xlo[m][t], al, false);
+            }
+            const int part = group_sum(static_cast<int>(static_cast<uint32_t>(ah) * 256u + al), lpg);
+            if (lead) {
+                const float dot = __fmul_rn(xsc[m], static_cast<float>(part));
+                const float bx = __fmul_rn(bf, xsum_lds[m * Gr + g]);
+                Tw[(m * NU + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (++cu_r == NU) {
+            cu_r = 0;
+            if (++cu_c == C) {                            // unit done: ordered chains
+                cu_c = 0;
+                const int unit = cu_unit;
+                cu_unit += tw;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                if (lane < MR * UB) {
+                    const int m = lane / UB, uu = lane - m * UB, gr = unit * UB + uu;
+                    if (gr < n_total) {
+                        const float acc = chain_sum(Tw + (m * NU + uu) * Ts, G);
+                        if constexpr (PAIR) {
+                            const float up = chain_sum(Tw + (m * NU + UB + uu) * Ts, G);
+                            ml.out[0][static_cast<size_t>(m) * ml.n_out[0] + gr] = silu_mul(acc, up);
+                        } else {
+                            // the host picks UB dividing every n_out, so a unit
+                            // never straddles two matrices and p is wave-uniform
+                            const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
+                            const int no = sel4(p, ml.n_out[0], ml.n_out[1], ml.n_out[2], ml.n_out[3]);
+                            const int rb = sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2],
+                                                ml.row_begin[3]);
+                            pick(ml.out, p)[static_cast<size_t>(m) * no + (gr - rb)] = acc;
+                        }
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            }
+        }
+    };
+    auto refill = [&](Item& slot) {
+        load_item<PAIR>(slot, ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, true);
+        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+    };
+    // steady state: every refill is live and unconditional (exact waits)
+    int q0 = 0;
+    for (; q0 + 2 * RING <= Q; q0 += RING) {
+#pragma unroll
+        for (int d = 0; d < RING; d++) {
+            consume(ring[d]);
+            refill(ring[d]);
+        }
+    }
+    // tail: RING..2*RING-1 items left (a working wave has Q >= RING)
+    if (q0 < Q) {                                                 // uniform
+#pragma unroll
+        for (int d = 0; d < RING; d++) {
+            consume(ring[d]);
+            if (q0 + RING + d < Q) refill(ring[d]);               // uniform
+        }
+#pragma unroll
+        for (int d = 0; d < RING; d++)
+            if (q0 + RING + d < Q) consume(ring[d]);              // uniform
     }
 }
 
@@ -943,26 +1071,10 @@ int num_cus() {
 
 constexpr size_t kStreamLdsMax = 160 * 1024;
 
-template <int MR, int VPT, bool PAIR = false>
-int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st) {
-    auto kern = gemv_stream_kernel<MR, VPT, PAIR>;
-    const int G = n_in / (4 * VPT);
-    const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
-    const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
-    const int cus = num_cus();
-    // 16 waves per workgroup when there are rows for a full grid of them,
-    // else smaller workgroups so that every CU gets some
-    int nwaves = 16;
-    while (nwaves > 4 && n_total * (PAIR ? 2 : 1) < nwaves * cus) nwaves >>= 1;
-    // rows per unit: enough 1 KiB items per unit to fill a batch, more when
-    // rows are plentiful
-    int UB = 1;
-    while (UB < 4 && UB * C * (PAIR ? 2 : 1) < kBatch && n_total >= 2 * UB * nwaves * cus) UB *= 2;
-    while (MR * UB > 64) UB >>= 1;
-    for (int k = 0; k < ml.count; k++)                 // a unit must not straddle matrices
-        while (ml.n_out[k] % UB) UB >>= 1;
-    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB);
-    if (lds > kStreamLdsMax) return 0;
+template <int MR, int RW, bool PAIR, int RING>
+int launch_stream_k(const MatList& ml, const float* x, int n_in, int UB, int nwaves, size_t lds, int grid,
+                    hipStream_t st) {
+    auto kern = gemv_stream_kernel<MR, RW, PAIR, RING>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -971,17 +1083,72 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st) {
         if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
         attr_set = true;
     }
-    int per_cu = 0;
-    hipError_t eo = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * nwaves, lds);
-    if (eo != hipSuccess || per_cu < 1) per_cu = 1;
-    const int n_units = (n_total + UB - 1) / UB;
-    const int want = (n_units + nwaves - 1) / nwaves;
-    const int cap = cus * per_cu;                       // every workgroup resident at once
-    const int grid = want < cap ? want : cap;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "stream gemv launch: %s", hipGetErrorString(e));
     return 1;
+}
+
+template <int MR, int RW, bool PAIR>
+int launch_stream_rw(const MatList& ml, const float* x, int n_in, int UB, int nwaves, size_t lds, int n_units,
+                     int items, hipStream_t st) {
+    // occupancy of the largest ring (the most registers)
+    int per_cu = 0;
+    hipError_t eo = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, gemv_stream_kernel<MR, RW, PAIR, 4>, 64 * nwaves, lds);
+    if (eo != hipSuccess || per_cu < 1) per_cu = 1;
+    const int want = (n_units + nwaves - 1) / nwaves;
+    const int cap = num_cus() * per_cu;                 // every workgroup resident at once
+    const int grid = want < cap ? want : cap;
+    // ring: the largest of 8, 2, 1 items that every working wave has
+    const int per_wave = n_units / (grid * nwaves);
+    const int qmin = (per_wave > 0 ? per_wave : 1) * items;
+    if (qmin >= 4) return launch_stream_k<MR, RW, PAIR, 4>(ml, x, n_in, UB, nwaves, lds, grid, st);
+    if (qmin >= 2) return launch_stream_k<MR, RW, PAIR, 2>(ml, x, n_in, UB, nwaves, lds, grid, st);
+    return launch_stream_k<MR, RW, PAIR, 1>(ml, x, n_in, UB, nwaves, lds, grid, st);
+}
+
+template <int MR, bool PAIR = false>
+int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st) {
+    constexpr int kWavesPerCu = 16;                     // 4 waves per SIMD at <= 128 VGPRs
+    constexpr int rmax = stream_max_rounds<MR>();
+    const int G = n_in / 64;
+    const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
+    const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
+    const int cus = num_cus();
+    // smallest workgroup the prologue accepts: one thread per (row, group)
+    // item, and at most rmax words of x per thread and row
+    int minw = (MR * G + 63) / 64;
+    const int wr = (C * kChunkWords + 64 * rmax - 1) / (64 * rmax);
+    if (wr > minw) minw = wr;
+    if (minw > 16) return 0;
+    // rows per unit: 1, or more when rows are plentiful and short
+    int UB = 1;
+    while (UB < 4 && UB * C * (PAIR ? 2 : 1) < kUnitItems && n_total >= 2 * UB * kWavesPerCu * cus) UB *= 2;
+    while (MR * UB > 64) UB >>= 1;
+    for (int k = 0; k < ml.count; k++)                 // a unit must not straddle matrices
+        while (ml.n_out[k] % UB) UB >>= 1;
+    const int n_units = (n_total + UB - 1) / UB;
+    // one unit per wave while the units fit on the chip at once, the waves
+    // spread evenly over the CUs (3584 rows: 256 workgroups of 14 waves)
+    const int target = n_units < kWavesPerCu * cus ? n_units : kWavesPerCu * cus;
+    int nwaves = (target + cus - 1) / cus;
+    if (nwaves < minw) nwaves = minw;
+    if (nwaves > 16) nwaves = 16;
+    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB);
+    if (lds > kStreamLdsMax) return 0;
+    const int rw = (C * kChunkWords + 64 * nwaves - 1) / (64 * nwaves);
+    const int items = (PAIR ? 2 : 1) * UB * C;
+    switch (rw) {
+        case 1: return launch_stream_rw<MR, 1, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
+        case 2: return launch_stream_rw<MR, 2, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
+        // (3 and 4 words per thread: the single-matrix launches of one row)
+        case 3: if constexpr (rmax >= 3 && !PAIR) return launch_stream_rw<MR, 3, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
+                return 0;
+        case 4: if constexpr (rmax >= 4 && !PAIR) return launch_stream_rw<MR, 4, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
+                return 0;
+        default: return 0;
+    }
 }
 
 // The streaming path takes gs 64, x 16-byte aligned and at most 16 chunks
@@ -992,8 +1159,7 @@ int try_fused(const MatList& ml, const float* x, int n_in, int gs, hipStream_t s
     if (gs != 64 || n_in == 0 || (reinterpret_cast<uintptr_t>(x) & 15)) return 0;
     const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
     if (C > 16) return 0;
-    if (gs == 64) return launch_stream<MR, 16>(ml, x, n_in, st);
-    return 0;                           // other group sizes: split path
+    return launch_stream<MR>(ml, x, n_in, st);
 }
 
 int try_fused_m(const MatList& ml, const float* x, int m, int n_in, int gs, hipStream_t st) {
@@ -1397,8 +1563,8 @@ int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const ui
         int done = 0;
         if (gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
             (n_in / 8 + kChunkWords - 1) / kChunkWords <= 16) {
-            done = mm == 1 ? launch_stream<1, 16, true>(ml, xm, n_in, st)
-                           : launch_stream<2, 16, true>(ml, xm, n_in, st);
+            done = mm == 1 ? launch_stream<1, true>(ml, xm, n_in, st)
+                           : launch_stream<2, true>(ml, xm, n_in, st);
             if (done < 0) return done;
         }
         if (!done) {        // unfused: gate into h, up into the workspace, then SiLU * mul
