@@ -3,6 +3,11 @@
 The library sits where the reference's ctypes loader looks for its CPU
 kernel (hetero/cpu_model.py:35-37: <package parent>/kernel/libq4gemv.so), so
 hetero/cpu_model.py here loads it the same way.
+
+csrc/q4gemv.hip (host code, C-ABI and the other kernels) and the instances
+of the streaming GEMV kernel (csrc/q4_stream_inst.hip, once per activation
+rows x gate/up pair x ring size) are compiled as separate objects in
+parallel, then linked into one shared library.
 """
 from __future__ import annotations
 
@@ -10,18 +15,25 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "q4gemv.hip")
+CSRC = os.path.join(HERE, "csrc")
+SRC = os.path.join(CSRC, "q4gemv.hip")
+INST = os.path.join(CSRC, "q4_stream_inst.hip")
 OUT = os.path.join(HERE, "kernel", "libq4gemv.so")
 
 HIPCC_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
-    "-ffp-contract=off",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+    "-ffp-contract=off", "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-command-line-argument",
 ]
+
+# (activation rows, gate/up pair, ring size) of the streaming kernel objects
+STREAM_INSTANCES = [(mr, pair, ring) for mr in (1, 2) for pair in (0, 1) for ring in (1, 2, 4)]
 
 
 def hipcc() -> str:
@@ -31,17 +43,35 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(os.path.dirname(OUT), exist_ok=True)
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, SRC]
+def _run(cmd, what, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError(f"hipcc failed ({r.returncode}) building {SRC}")
-    os.replace(tmp, OUT)
+        raise RuntimeError(f"hipcc failed ({r.returncode}) building {what}")
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    os.makedirs(os.path.dirname(OUT), exist_ok=True)
+    cc = hipcc()
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    jobs = jobs or min(16, os.cpu_count() or 4)
+    with tempfile.TemporaryDirectory(prefix="q4build") as tmpd:
+        units = [(SRC, os.path.join(tmpd, "q4gemv.o"), [])]
+        for mr, pair, ring in STREAM_INSTANCES:
+            obj = os.path.join(tmpd, f"stream_m{mr}_p{pair}_r{ring}.o")
+            units.append((INST, obj, [f"-DQ4_MR={mr}", f"-DQ4_PAIR={pair}", f"-DQ4_RING={ring}"]))
+        with ThreadPoolExecutor(max_workers=jobs) as ex:
+            futs = [ex.submit(_run, [cc, *HIPCC_FLAGS, *inc, *defs, "-c", "-o", obj, src],
+                              f"{os.path.basename(src)} {' '.join(defs)}", verbose)
+                    for src, obj, defs in units]
+            for f in futs:
+                f.result()
+        tmp = OUT + ".tmp"
+        _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *[o for _, o, _ in units]],
+             "link", verbose)
+        os.replace(tmp, OUT)
     return OUT
 
 

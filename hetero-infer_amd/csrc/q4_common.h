@@ -1,0 +1,96 @@
+// Shared by the translation units of libq4gemv.so: constants and the
+// device helpers of the int4 GEMV kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "q4gemv.h"
+
+namespace q4k {
+
+constexpr int kChunkWords = 256;   // words per wave chunk: 64 lanes x 4 words
+
+// ---------------------------------------------------------------- helpers --
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// x86 cvttss2si followed by a 16-bit truncation: values outside the int32
+// range (and NaN) give 0x80000000, whose low half is 0.
+__device__ __forceinline__ int32_t to_i16_like_x86(float r) {
+    int32_t v = (r > -2147483648.0f && r < 2147483648.0f) ? static_cast<int32_t>(r)
+                                                           : static_cast<int32_t>(0x80000000u);
+    return static_cast<int16_t>(v);
+}
+
+// Sum of an int over the `lpg` consecutive lanes of a group (lpg a power of
+// two, 1..64).  Every lane of the wave must execute it.
+__device__ __forceinline__ int group_sum(int v, int lpg) {
+    if (lpg >= 2) v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    if (lpg >= 4) v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+    if (lpg >= 8) v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    if (lpg >= 16) v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false); // row_mirror
+    if (lpg >= 32) v += __shfl_xor(v, 16);
+    if (lpg >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+
+// Max over the wave (NaN-skipping, like the reference's `v > amax` scan):
+// DPP within rows of 16 lanes, then the four row results through SGPRs.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float a) {
+    const int o = __builtin_amdgcn_update_dpp(__float_as_int(a), __float_as_int(a), CTRL, 0xF, 0xF, false);
+    return fmaxf(a, __int_as_float(o));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = dpp_max<0xB1>(v);    // quad_perm 1,0,3,2
+    v = dpp_max<0x4E>(v);    // quad_perm 2,3,0,1
+    v = dpp_max<0x141>(v);   // row_half_mirror
+    v = dpp_max<0x140>(v);   // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// One packed word of x (8 values, MLX order) -> {xl even, xl odd, xh even,
+// xh odd} byte planes of xq = (int16)(x*inv +- 0.5) (kernel/q4gemv.c:266-268).
+// a + copysign(0.5, a) is the reference's `a < 0 ? a - 0.5 : a + 0.5` for
+// every a whose truncation is defined (the two differ only for -0.0, which
+// truncates to 0 either way).  When inv is finite |x*inv| <= 32767.5, so
+// v_cvt_i32_f32 is the x86 truncation (NaN -> 0 on both after the 16-bit
+// cut); `exact_clamp` selects the out-of-range rule for an infinite inv.
+__device__ __forceinline__ uint4 quant_word(const float (&v)[8], float inv, bool exact_clamp) {
+    int32_t q[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+        const float a = __fmul_rn(v[n], inv);
+        const float r = __fadd_rn(a, __builtin_copysignf(0.5f, a));
+        q[n] = exact_clamp ? to_i16_like_x86(r) : static_cast<int32_t>(r);
+    }
+    // pack (q0,q2), (q4,q6), (q1,q3), (q5,q7) as int16 pairs, then gather bytes
+    const uint32_t e0 = (static_cast<uint32_t>(q[0]) & 0xFFFFu) | (static_cast<uint32_t>(q[2]) << 16);
+    const uint32_t e1 = (static_cast<uint32_t>(q[4]) & 0xFFFFu) | (static_cast<uint32_t>(q[6]) << 16);
+    const uint32_t o0 = (static_cast<uint32_t>(q[1]) & 0xFFFFu) | (static_cast<uint32_t>(q[3]) << 16);
+    const uint32_t o1 = (static_cast<uint32_t>(q[5]) & 0xFFFFu) | (static_cast<uint32_t>(q[7]) << 16);
+    // v_perm_b32(hi, lo, sel): byte k of the result = byte sel[k] of {hi:lo}
+    const uint32_t le = __builtin_amdgcn_perm(e1, e0, 0x06040200u);   // low bytes of q0,q2,q4,q6
+    const uint32_t he = __builtin_amdgcn_perm(e1, e0, 0x07050301u);   // high bytes
+    const uint32_t lo = __builtin_amdgcn_perm(o1, o0, 0x06040200u);
+    const uint32_t ho = __builtin_amdgcn_perm(o1, o0, 0x07050301u);
+    return make_uint4(le, lo, he, ho);
+}
+
+// host side, defined in q4gemv.hip
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int num_cus();
+constexpr size_t kStreamLdsMax = 160 * 1024;
+
+}  // namespace q4k

@@ -1,0 +1,445 @@
+// The streaming single-launch GEMV kernel and its launch, shared by
+// q4gemv.hip (which picks the instance) and q4_stream_inst.hip (which
+// compiles the instances, one object per (rows, pair, ring) in parallel).
+#pragma once
+
+#include "q4_common.h"
+
+namespace q4k {
+
+// ---------------------------------------------- streaming single-launch GEMV --
+//
+// One launch per call; weights are streamed row-contiguously (a wave-load
+// moves 1 KiB of one row: 64 lanes x 16 bytes).  Group size 64.
+//   * The x prologue runs once per workgroup.  Every x load is issued before
+//     the first weight load and x is read once: vector-memory results return
+//     in issue order, so an x load issued behind the weight stream would wait
+//     for it.  Each thread loads whole packed words (8 values), stages them
+//     in LDS and takes amax; after one barrier one thread per group chains
+//     the group sum in ascending order from LDS while every thread writes
+//     the int8/uint8 planes of its words of the int16 x into LDS.
+//   * Then every wave works alone on a flat stream of 1 KiB items: the items
+//     of its units (UB consecutive rows; PAIR: UB rows of matrix 0 and the
+//     same UB rows of matrix 1), chunk-major within a unit so consecutive
+//     items share x planes.  A ring of RING items is in flight (the host
+//     picks RING no larger than any working wave's item count): the item
+//     RING ahead is issued right after an item is consumed, from straight-
+//     line code while every refill is live, so each wait is a partial
+//     vmcnt; the last 1..2*RING items run through a tail with conditional
+//     refills, so nothing past the wave's last item is ever loaded.  Lanes
+//     past a row end read through a buffer range that ends with the row:
+//     0, no memory access.
+//   * Each group's fp32 term goes to a wave-private LDS table; when a unit
+//     is done one lane per (m, row) adds its row's terms in ascending group
+//     order -- no workgroup barrier in the main loop.
+// The row a wave works on is wave-uniform (kept in SGPRs), so choosing the
+// matrix of a grouped launch (q/k/v, gate/up: up to kMaxMats sharing x) is
+// scalar work.
+constexpr int kMaxMats = 4;
+constexpr int kEarly = 2;           // ring items issued before the x prologue has its data
+constexpr int kUnitItems = 4;       // rows per unit grow until a unit has this many items
+
+struct MatList {
+    const uint32_t* w[kMaxMats];
+    const uint16_t* s[kMaxMats];
+    const uint16_t* b[kMaxMats];
+    float* out[kMaxMats];
+    int n_out[kMaxMats];
+    int row_begin[kMaxMats + 1];   // prefix sums of n_out
+    int count;
+};
+
+// Row stride of the per-wave term table: a multiple of 4 floats (16-byte
+// reads) that is 4 mod 8 words, so lanes reading different rows spread over
+// the banks.
+__host__ __device__ inline int term_stride(int G) { return ((G + 3) & ~3) | 4; }
+
+// Staged x floats: group g of row m at (m*G + g) * kStageStride floats, so
+// the 16-byte reads of one lane per group land on distinct banks.
+constexpr int kStageStride = 68;
+
+inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU) {
+    const size_t terms = static_cast<size_t>(nwaves) * mr * NU * term_stride(G) * 4;
+    const size_t stage = static_cast<size_t>(mr) * G * kStageStride * 4;
+    return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
+         + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
+         + static_cast<size_t>(mr) * 16 * 4                              // amax per wave
+         + (terms > stage ? terms : stage);                              // term tables | staged x
+}
+
+__device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
+    int p = 0;
+#pragma unroll
+    for (int k = 1; k < kMaxMats; k++) p += (k < ml.count && gr >= ml.row_begin[k]) ? 1 : 0;
+    return p;
+}
+
+// x[p] for a wave-uniform p in an SGPR, as scalar compare/selects in asm: a
+// select written in C++ is folded back into an indexed kernel-argument load,
+// which puts a scalar memory round trip in front of every weight load.
+__device__ __forceinline__ uint64_t sel4(int p, uint64_t a0, uint64_t a1, uint64_t a2, uint64_t a3) {
+    uint64_t r;
+    asm volatile(
+        "s_cmp_eq_u32 %1, 1\n\t"
+        "s_cselect_b64 %0, %3, %2\n\t"
+        "s_cmp_eq_u32 %1, 2\n\t"
+        "s_cselect_b64 %0, %4, %0\n\t"
+        "s_cmp_eq_u32 %1, 3\n\t"
+        "s_cselect_b64 %0, %5, %0"
+        : "=&s"(r) : "s"(p), "s"(a0), "s"(a1), "s"(a2), "s"(a3) : "scc");
+    return r;
+}
+__device__ __forceinline__ int sel4(int p, int a0, int a1, int a2, int a3) {
+    int r;
+    asm volatile(
+        "s_cmp_eq_u32 %1, 1\n\t"
+        "s_cselect_b32 %0, %3, %2\n\t"
+        "s_cmp_eq_u32 %1, 2\n\t"
+        "s_cselect_b32 %0, %4, %0\n\t"
+        "s_cmp_eq_u32 %1, 3\n\t"
+        "s_cselect_b32 %0, %5, %0"
+        : "=&s"(r) : "s"(p), "s"(a0), "s"(a1), "s"(a2), "s"(a3) : "scc");
+    return r;
+}
+template <typename T>
+__device__ __forceinline__ T* pick(T* const (&a)[kMaxMats], int p) {
+    return reinterpret_cast<T*>(sel4(p, reinterpret_cast<uint64_t>(a[0]), reinterpret_cast<uint64_t>(a[1]),
+                                     reinterpret_cast<uint64_t>(a[2]), reinterpret_cast<uint64_t>(a[3])));
+}
+
+struct Item {
+    uint4 w;
+    uint16_t s, b;
+};
+
+// Raw buffer resource over [p, p + bytes): loads at an offset >= bytes
+// return 0 without a memory access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+constexpr uint32_t kOutOfRange = 0x80000000u;   // any offset past every resource here
+
+// Issue the loads of item (chunk c, row slot r) of unit `unit`.  The row is
+// wave-uniform: each array gets a resource over that row alone, so lanes
+// past the row end read 0 and cost no memory access, and `live` false (a
+// prefetch past the wave's last item) gives an empty resource: every lane
+// reads 0.  No branch, so the waits on earlier loads stay exact.
+template <bool PAIR>
+__device__ __forceinline__ void load_item(Item& it, const MatList& ml, int unit, int c, int r, int UB,
+                                          int n_total, int wpr, int G, int lane, bool live) {
+    const int u = PAIR ? (r < UB ? r : r - UB) : r;
+    int gr = unit * UB + u;
+    gr = gr < n_total ? gr : n_total - 1;
+    // p is wave-uniform; readfirstlane makes that explicit, so the
+    // kernel-argument reads below are scalar loads
+    const int p = __builtin_amdgcn_readfirstlane(PAIR ? (r < UB ? 0 : 1) : mat_of_row(ml, gr));
+    const int o = __builtin_amdgcn_readfirstlane(
+        PAIR ? gr : gr - sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2], ml.row_begin[3]));
+    const uint32_t wbytes = live ? static_cast<uint32_t>(wpr) * 4u : 0u;
+    const uint32_t gbytes = live ? static_cast<uint32_t>(G) * 2u : 0u;
+    const int word0 = c * kChunkWords + lane * 4;
+    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+        buf_rsrc(pick(ml.w, p) + static_cast<size_t>(o) * wpr, wbytes), word0 * 4, 0, 0));
+    const int go = (word0 >> 3) * 2;
+    it.s = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(pick(ml.s, p) + static_cast<size_t>(o) * G, gbytes), go, 0, 0);
+    it.b = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(pick(ml.b, p) + static_cast<size_t>(o) * G, gbytes), go, 0, 0);
+}
+
+// Sequential fp32 sum of n terms (ascending), four 16-byte LDS reads in flight.
+__device__ __forceinline__ float chain_sum(const float* tp, int n) {
+    const float4* t4 = reinterpret_cast<const float4*>(tp);
+    float acc = 0.0f;
+    int g = 0;
+    for (; g + 16 <= n; g += 16) {
+        const float4 a0 = t4[g / 4], a1 = t4[g / 4 + 1], a2 = t4[g / 4 + 2], a3 = t4[g / 4 + 3];
+        const float vals[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                                a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc = __fadd_rn(acc, vals[i]);
+    }
+    for (; g < n; g++) acc = __fadd_rn(acc, tp[g]);
+    return acc;
+}
+
+// SiLU(g) * u as hetero/cpu_model.py:169-170 and :291-292 compute it in
+// fp32: g / (1 + exp(-g)) * u (expf here; NumPy's float32 exp may differ in
+// the last place).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = expf(-g);
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+}
+
+// Words of x per thread and activation row that the word pass keeps in
+// registers (RW rounds of blockDim.x words); the host picks the instance.
+template <int MR>
+__host__ __device__ constexpr int stream_max_rounds() { return MR == 1 ? 4 : 2; }
+
+// PAIR: matrices 0 and 1 (gate, up) are computed row for row and the output
+// is out[0] = SiLU(gate) * up.
+// Host guarantees: MR * (n_in / 64) <= blockDim.x (one thread per group
+// item), chunks * 256 <= RW * blockDim.x, n_in % 64 == 0, x 16-byte aligned.
+template <int MR, int RW, bool PAIR, int RING>
+__global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const float* __restrict__ x,
+                                                          int n_in, int UB) {
+    extern __shared__ uint4 lds4[];
+    constexpr int lpg = 2;                                        // lanes per group
+    const int wpr = n_in >> 3, G = n_in >> 6;
+    const int C = (wpr + kChunkWords - 1) / kChunkWords;
+    const int Gr = (G + 3) & ~3, Ts = term_stride(G);
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);    // wave-uniform
+    const int nwaves = nt >> 6;
+    uint4* xpl = lds4;                                            // [MR][C*256] swizzled
+    float* xsum_lds = reinterpret_cast<float*>(xpl + MR * C * 256);   // [MR][Gr]
+    float* red = xsum_lds + MR * Gr;                              // [MR][16]
+    const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
+    float* Tw = red + MR * 16 + wave * (MR * NU * Ts);            // this wave: [MR][NU][Ts]
+    const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
+    const int n_units = (n_total + UB - 1) / UB;
+    const int tw = gridDim.x * nwaves;
+    const int items = NU * C;
+
+    // ---- x loads: thread t owns words t, t + nt, ... of every row, 8 values
+    //      each, through a resource over x (words at or past the row end read
+    //      0); waves with no word in a round issue nothing.  These are the
+    //      first loads of the kernel, so the waits further down stay exact.
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(MR * n_in) * 4u);
+    float4 wv[MR][RW][2];
+#pragma unroll
+    for (int m = 0; m < MR; m++)
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+            if (r * nt + wave * 64 < wpr) {                       // uniform
+                const int j = r * nt + tid;
+                const uint32_t off = j < wpr ? static_cast<uint32_t>(m * n_in + 8 * j) * 4u : kOutOfRange;
+                wv[m][r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+                wv[m][r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+            }
+
+    // ---- the wave's item stream: units gw, gw + tw, ...; item i of a unit
+    //      is (chunk i / NU, row slot i % NU).  Up to kEarly items are
+    //      issued now, the rest of the ring once x is in: a full ring from
+    //      every wave at once would queue ahead of the x loads of later
+    //      waves.  A wave without units loads through empty ranges.
+    const int gw = blockIdx.x * nwaves + wave;
+    const int nu_w = gw < n_units ? (n_units - gw + tw - 1) / tw : 0;
+    const int Q = nu_w * items;
+    constexpr int kE = RING < kEarly ? RING : kEarly;
+    Item ring[RING];
+    int pf_unit = gw, pf_c = 0, pf_r = 0, pf_q = 0;               // prefetch cursor (uniform)
+#pragma unroll
+    for (int d = 0; d < kE; d++) {
+        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, pf_q < Q);
+        pf_q++;
+        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+    }
+
+    // ---- stage the floats in LDS (the term tables' space, free until the
+    //      main loop) and take the running max |x| (kernel/q4gemv.c:258-259,
+    //      NaN-skipping) per row
+    float* stage = red + MR * 16;
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int r = 0; r < RW; r++)
+            if (r * nt + wave * 64 < wpr) {                       // uniform
+                const int j = r * nt + tid;
+                if (j < wpr) {
+                    float4* dst = reinterpret_cast<float4*>(stage + (m * G + (j >> 3)) * kStageStride + 8 * (j & 7));
+                    dst[0] = wv[m][r][0];
+                    dst[1] = wv[m][r][1];
+                }
+                const float4 a = wv[m][r][0], b = wv[m][r][1];  // 0 past the row end
+                amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+            }
+        amax = wave_max(amax);
+        if (lane == 0) red[m * 16 + wave] = amax;
+    }
+#pragma unroll
+    for (int d = kE; d < RING; d++) {
+        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, pf_q < Q);
+        pf_q++;
+        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+    }
+    __syncthreads();
+
+    // ---- group sums: one thread per (row, group) chains its 64 values in
+    //      ascending order (kernel/q4gemv.c:244-248)
+    if (tid < MR * G) {
+        const float4* gp = reinterpret_cast<const float4*>(stage + tid * kStageStride);
+        float sum = 0.0f;
+#pragma unroll
+        for (int i0 = 0; i0 < 16; i0 += 4) {
+            const float4 v0 = gp[i0], v1 = gp[i0 + 1], v2 = gp[i0 + 2], v3 = gp[i0 + 3];
+            const float vals[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                                    v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+#pragma unroll
+            for (int i = 0; i < 16; i++) sum = __fadd_rn(sum, vals[i]);
+        }
+        const int m = tid / G;
+        xsum_lds[m * Gr + (tid - m * G)] = sum;
+    }
+
+    // ---- int16 x (kernel/q4gemv.c:260-270) as byte planes in LDS
+    float xsc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+        float a = 0.0f;
+        for (int i = 0; i < nwaves; i++) a = fmaxf(a, red[m * 16 + i]);
+        xsc[m] = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;        // kernel/q4gemv.c:260
+        const float inv = __fdiv_rn(1.0f, xsc[m]);                 // :261
+        const bool exact_clamp = __builtin_isinf(inv);
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int j = r * nt + tid;
+            if (r * nt + wave * 64 < C * kChunkWords) {           // uniform
+                uint4 pl = make_uint4(0, 0, 0, 0);
+                if (r * nt + wave * 64 < wpr) {                   // uniform
+                    const float vv[8] = {wv[m][r][0].x, wv[m][r][0].y, wv[m][r][0].z, wv[m][r][0].w,
+                                         wv[m][r][1].x, wv[m][r][1].y, wv[m][r][1].z, wv[m][r][1].w};
+                    pl = exact_clamp ? quant_word(vv, inv, true) : quant_word(vv, inv, false);
+                    if (j >= wpr) pl = make_uint4(0, 0, 0, 0);
+                }
+                const int cc = j >> 8, jj = j & 255;
+                xpl[(m * C + cc) * 256 + (jj & 3) * 64 + (jj >> 2)] = pl;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- main loop: consume the ring, refill each slot RING items ahead
+    int cu_unit = gw, cu_c = 0, cu_r = 0;                         // consume cursor (uniform)
+    int cprev = -1;
+    uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
+    auto consume = [&](const Item& itm) {
+        const int c = cu_c, u = cu_r;
+        const int word0 = c * kChunkWords + lane * 4;
+        const bool lead = word0 < wpr && (lane & (lpg - 1)) == lpg - 1;
+        const int g = word0 >> 3;
+        if (c != cprev) {                                 // uniform: planes of chunk c
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const uint4 pl = xpl[(m * C + c) * 256 + t * 64 + lane];
+                    xle[m][t] = pl.x; xlo[m][t] = pl.y; xhe[m][t] = pl.z; xho[m][t] = pl.w;
+                }
+            cprev = c;
+        }
+        const uint32_t wd[4] = {itm.w.x, itm.w.y, itm.w.z, itm.w.w};
+        uint32_t lo4[4], hi4[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            lo4[t] = wd[t] & 0x0F0F0F0Fu;          // values 8j+0,2,4,6
+            hi4[t] = (wd[t] >> 4) & 0x0F0F0F0Fu;   // values 8j+1,3,5,7
+        }
+        const float sf = h2f(itm.s), bf = h2f(itm.b);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            int ah = 0;
+            uint32_t al = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                ah = __builtin_amdgcn_sdot4(static_cast<int>(lo4[t]), static_cast<int>(xhe[m][t]), ah, false);
+                ah = __builtin_amdgcn_sdot4(static_cast<int>(hi4[t]), static_cast<int>(xho[m][t]), ah, false);
+                al = __builtin_amdgcn_udot4(lo4[t], xle[m][t], al, false);
+                al = __builtin_amdgcn_udot4(hi4[t], xlo[m][t], al, false);
+            }
+            const int part = group_sum(static_cast<int>(static_cast<uint32_t>(ah) * 256u + al), lpg);
+            if (lead) {
+                const float dot = __fmul_rn(xsc[m], static_cast<float>(part));
+                const float bx = __fmul_rn(bf, xsum_lds[m * Gr + g]);
+                Tw[(m * NU + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
+            }
+        }
+        if (++cu_r == NU) {
+            cu_r = 0;
+            if (++cu_c == C) {                            // unit done: ordered chains
+                cu_c = 0;
+                const int unit = cu_unit;
+                cu_unit += tw;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                if (lane < MR * UB) {
+                    const int m = lane / UB, uu = lane - m * UB, gr = unit * UB + uu;
+                    if (gr < n_total) {
+                        const float acc = chain_sum(Tw + (m * NU + uu) * Ts, G);
+                        if constexpr (PAIR) {
+                            const float up = chain_sum(Tw + (m * NU + UB + uu) * Ts, G);
+                            ml.out[0][static_cast<size_t>(m) * ml.n_out[0] + gr] = silu_mul(acc, up);
+                        } else {
+                            // the host picks UB dividing every n_out, so a unit
+                            // never straddles two matrices and p is wave-uniform
+                            const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
+                            const int no = sel4(p, ml.n_out[0], ml.n_out[1], ml.n_out[2], ml.n_out[3]);
+                            const int rb = sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2],
+                                                ml.row_begin[3]);
+                            pick(ml.out, p)[static_cast<size_t>(m) * no + (gr - rb)] = acc;
+                        }
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            }
+        }
+    };
+    auto refill = [&](Item& slot) {
+        load_item<PAIR>(slot, ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, true);
+        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+    };
+    // steady state: every refill is live and unconditional (exact waits)
+    int q0 = 0;
+    for (; q0 + 2 * RING <= Q; q0 += RING) {
+#pragma unroll
+        for (int d = 0; d < RING; d++) {
+            consume(ring[d]);
+            refill(ring[d]);
+        }
+    }
+    // tail: RING..2*RING-1 items left (a working wave has Q >= RING)
+    if (q0 < Q) {                                                 // uniform
+#pragma unroll
+        for (int d = 0; d < RING; d++) {
+            consume(ring[d]);
+            if (q0 + RING + d < Q) refill(ring[d]);               // uniform
+        }
+#pragma unroll
+        for (int d = 0; d < RING; d++)
+            if (q0 + RING + d < Q) consume(ring[d]);              // uniform
+    }
+}
+
+// Workgroups of the kernel resident per CU (the ring-4 instance: the most
+// registers of the rings in use).
+template <int MR, int RW, bool PAIR>
+int stream_blocks_per_cu(int nwaves, size_t lds) {
+    int per_cu = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per_cu, gemv_stream_kernel<MR, RW, PAIR, 4>, 64 * nwaves, lds);
+    return (e != hipSuccess || per_cu < 1) ? 1 : per_cu;
+}
+
+template <int MR, int RW, bool PAIR, int RING>
+int launch_stream_k(const MatList& ml, const float* x, int n_in, int UB, int nwaves, size_t lds, int grid,
+                    hipStream_t st) {
+    auto kern = gemv_stream_kernel<MR, RW, PAIR, RING>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(kStreamLdsMax));
+        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q4_EHIP, "stream gemv launch: %s", hipGetErrorString(e));
+    return 1;
+}
+
+}  // namespace q4k

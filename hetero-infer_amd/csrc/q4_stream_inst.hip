@@ -1,0 +1,30 @@
+// Instances of the streaming GEMV kernel, one object per (activation rows,
+// gate/up pair, ring size): the build compiles this file once per
+// -DQ4_MR=<1|2> -DQ4_PAIR=<0|1> -DQ4_RING=<1|2|4>, in parallel.
+#include "q4_stream.h"
+
+#if !defined(Q4_MR) || !defined(Q4_PAIR) || !defined(Q4_RING)
+#error "define Q4_MR, Q4_PAIR and Q4_RING"
+#endif
+
+namespace q4k {
+
+#if Q4_RING == 4
+#define Q4_STREAM_OCC(RW) \
+    template int stream_blocks_per_cu<Q4_MR, RW, static_cast<bool>(Q4_PAIR)>(int, size_t);
+#else
+#define Q4_STREAM_OCC(RW)
+#endif
+#define Q4_STREAM_INST(RW)                                                                      \
+    template int launch_stream_k<Q4_MR, RW, static_cast<bool>(Q4_PAIR), Q4_RING>(              \
+        const MatList&, const float*, int, int, int, size_t, int, hipStream_t);               \
+    Q4_STREAM_OCC(RW)
+
+Q4_STREAM_INST(1)
+Q4_STREAM_INST(2)
+#if Q4_MR == 1 && Q4_PAIR == 0
+Q4_STREAM_INST(3)
+Q4_STREAM_INST(4)
+#endif
+
+}  // namespace q4k
