@@ -21,14 +21,13 @@ namespace q4k {
 //   * Then every wave works alone on a flat stream of 1 KiB items: the items
 //     of its units (UB consecutive rows; PAIR: UB rows of matrix 0 and the
 //     same UB rows of matrix 1), chunk-major within a unit so consecutive
-//     items share x planes.  A ring of RING items is in flight (the host
-//     picks RING no larger than any working wave's item count): the item
-//     RING ahead is issued right after an item is consumed, from straight-
-//     line code while every refill is live, so each wait is a partial
-//     vmcnt; the last 1..2*RING items run through a tail with conditional
-//     refills, so nothing past the wave's last item is ever loaded.  Lanes
-//     past a row end read through a buffer range that ends with the row:
-//     0, no memory access.
+//     items share x planes.  Units are handed to the waves of a workgroup
+//     from an LDS counter as they free up.  A ring of RING items is in
+//     flight (RING divides a unit's items): the item RING ahead is issued
+//     right after an item is consumed, from straight-line code, so each wait
+//     is a partial vmcnt; after the wave's last unit the ring drains without
+//     loads, so nothing past it is ever loaded.  Lanes past a row end read
+//     through a buffer range that ends with the row: 0, no memory access.
 //   * Each group's fp32 term goes to a wave-private LDS table; when a unit
 //     is done one lane per (m, row) adds its row's terms in ascending group
 //     order -- no workgroup barrier in the main loop.
@@ -63,7 +62,7 @@ inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU) 
     const size_t stage = static_cast<size_t>(mr) * G * kStageStride * 4;
     return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
          + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
-         + static_cast<size_t>(mr) * 16 * 4                              // amax per wave
+         + static_cast<size_t>(mr) * 16 * 4 + 16                         // amax per wave, counter
          + (terms > stage ? terms : stage);                              // term tables | staged x
 }
 
@@ -110,6 +109,7 @@ __device__ __forceinline__ T* pick(T* const (&a)[kMaxMats], int p) {
 struct Item {
     uint4 w;
     uint16_t s, b;
+    int unit;                       // wave-uniform
 };
 
 // Raw buffer resource over [p, p + bytes): loads at an offset >= bytes
@@ -127,6 +127,7 @@ constexpr uint32_t kOutOfRange = 0x80000000u;   // any offset past every resourc
 template <bool PAIR>
 __device__ __forceinline__ void load_item(Item& it, const MatList& ml, int unit, int c, int r, int UB,
                                           int n_total, int wpr, int G, int lane, bool live) {
+    it.unit = unit;
     const int u = PAIR ? (r < UB ? r : r - UB) : r;
     int gr = unit * UB + u;
     gr = gr < n_total ? gr : n_total - 1;
@@ -138,11 +139,20 @@ __device__ __forceinline__ void load_item(Item& it, const MatList& ml, int unit,
     const uint32_t wbytes = live ? static_cast<uint32_t>(wpr) * 4u : 0u;
     const uint32_t gbytes = live ? static_cast<uint32_t>(G) * 2u : 0u;
     const int word0 = c * kChunkWords + lane * 4;
-    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-        buf_rsrc(pick(ml.w, p) + static_cast<size_t>(o) * wpr, wbytes), word0 * 4, 0, 0));
     const int go = (word0 >> 3) * 2;
-    it.s = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(pick(ml.s, p) + static_cast<size_t>(o) * G, gbytes), go, 0, 0);
-    it.b = __builtin_amdgcn_raw_buffer_load_b16(buf_rsrc(pick(ml.b, p) + static_cast<size_t>(o) * G, gbytes), go, 0, 0);
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(pick(ml.w, p) + static_cast<size_t>(o) * wpr, wbytes);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(pick(ml.s, p) + static_cast<size_t>(o) * G, gbytes);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(pick(ml.b, p) + static_cast<size_t>(o) * G, gbytes);
+    // the three loads in a fixed order wherever an item is loaded: the
+    // partial waits on the ring are computed from the issue order, which
+    // must then be the same on entry to the main loop as around it
+    __builtin_amdgcn_sched_barrier(0);
+    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, word0 * 4, 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
+    it.s = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    it.b = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 // Sequential fp32 sum of n terms (ascending), four 16-byte LDS reads in flight.
@@ -194,10 +204,10 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     float* xsum_lds = reinterpret_cast<float*>(xpl + MR * C * 256);   // [MR][Gr]
     float* red = xsum_lds + MR * Gr;                              // [MR][16]
     const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
-    float* Tw = red + MR * 16 + wave * (MR * NU * Ts);            // this wave: [MR][NU][Ts]
+    int* claim_ctr = reinterpret_cast<int*>(red + MR * 16);       // units handed out past the first
+    float* Tw = red + MR * 16 + 4 + wave * (MR * NU * Ts);        // this wave: [MR][NU][Ts]
     const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
     const int n_units = (n_total + UB - 1) / UB;
-    const int tw = gridDim.x * nwaves;
     const int items = NU * C;
 
     // ---- x loads: thread t owns words t, t + nt, ... of every row, 8 values
@@ -217,28 +227,31 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
                 wv[m][r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
             }
 
-    // ---- the wave's item stream: units gw, gw + tw, ...; item i of a unit
-    //      is (chunk i / NU, row slot i % NU).  Up to kEarly items are
-    //      issued now, the rest of the ring once x is in: a full ring from
-    //      every wave at once would queue ahead of the x loads of later
-    //      waves.  A wave without units loads through empty ranges.
-    const int gw = blockIdx.x * nwaves + wave;
-    const int nu_w = gw < n_units ? (n_units - gw + tw - 1) / tw : 0;
-    const int Q = nu_w * items;
+    // ---- the wave's item stream.  Workgroup b owns units b, b + grid, ...;
+    //      wave w starts with its k = w-th one and claims further k from an
+    //      LDS counter as it goes: issue arbitration favours a SIMD's oldest
+    //      wave, so a fixed share per wave would leave the youngest waves
+    //      finishing long after the others.  Item i of a unit is (chunk
+    //      i / NU, row slot i % NU).  Up to kEarly items of the first ring are
+    //      issued now, the rest once x is in (a full ring from every wave at
+    //      once would queue ahead of the x loads of later waves).  A wave
+    //      without a first unit loads through empty ranges.
+    const int grid = gridDim.x;
+    const int first_unit = blockIdx.x + wave * grid;
+    const bool has_work = first_unit < n_units;                   // uniform
     constexpr int kE = RING < kEarly ? RING : kEarly;
     Item ring[RING];
-    int pf_unit = gw, pf_c = 0, pf_r = 0, pf_q = 0;               // prefetch cursor (uniform)
+    int pf_unit = first_unit, pf_c = 0, pf_r = 0;                 // prefetch cursor (uniform)
 #pragma unroll
     for (int d = 0; d < kE; d++) {
-        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, pf_q < Q);
-        pf_q++;
-        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, has_work);
+        if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
 
     // ---- stage the floats in LDS (the term tables' space, free until the
     //      main loop) and take the running max |x| (kernel/q4gemv.c:258-259,
     //      NaN-skipping) per row
-    float* stage = red + MR * 16;
+    float* stage = red + MR * 16 + 4;
 #pragma unroll
     for (int m = 0; m < MR; m++) {
         float amax = 0.0f;
@@ -260,11 +273,19 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     }
 #pragma unroll
     for (int d = kE; d < RING; d++) {
-        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, pf_q < Q);
-        pf_q++;
-        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
+        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, has_work);
+        if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
+    if (tid == 0) *claim_ctr = 0;
     __syncthreads();
+
+    // the claim for the wave's second unit, in flight during the rest of the prologue
+    auto claim = [&]() -> int {
+        int v = 0;
+        if (lane == 0) v = __hip_atomic_fetch_add(claim_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        return v + nwaves;                                        // lane 0's value counts
+    };
+    int claimed = claim();
 
     // ---- group sums: one thread per (row, group) chains its 64 values in
     //      ascending order (kernel/q4gemv.c:244-248)
@@ -310,25 +331,27 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     }
     __syncthreads();
 
-    // ---- main loop: consume the ring, refill each slot RING items ahead
-    int cu_unit = gw, cu_c = 0, cu_r = 0;                         // consume cursor (uniform)
-    int cprev = -1;
-    uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
-    auto consume = [&](const Item& itm) {
-        const int c = cu_c, u = cu_r;
+    // ---- main loop: consume the ring, refill each slot RING items ahead.
+    //      A unit is a whole number of ring cycles (the host picks RING
+    //      dividing the items of a unit), so units change -- the claim of the
+    //      next one, the ordered chains of the finished one -- only between
+    //      cycles, and a cycle is straight-line code: its refills are
+    //      unconditional (exact waits).  After the wave's last unit the ring
+    //      drains without loads.
+    // one item: the integer dots of chunk c against row slot u, one fp32
+    // term per group written by the group's last lane
+    auto consume = [&](const Item& itm, int c, int u) {
         const int word0 = c * kChunkWords + lane * 4;
         const bool lead = word0 < wpr && (lane & (lpg - 1)) == lpg - 1;
         const int g = word0 >> 3;
-        if (c != cprev) {                                 // uniform: planes of chunk c
+        uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
 #pragma unroll
-            for (int m = 0; m < MR; m++)
+        for (int m = 0; m < MR; m++)
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    const uint4 pl = xpl[(m * C + c) * 256 + t * 64 + lane];
-                    xle[m][t] = pl.x; xlo[m][t] = pl.y; xhe[m][t] = pl.z; xho[m][t] = pl.w;
-                }
-            cprev = c;
-        }
+            for (int t = 0; t < 4; t++) {
+                const uint4 pl = xpl[(m * C + c) * 256 + t * 64 + lane];
+                xle[m][t] = pl.x; xlo[m][t] = pl.y; xhe[m][t] = pl.z; xho[m][t] = pl.w;
+            }
         const uint32_t wd[4] = {itm.w.x, itm.w.y, itm.w.z, itm.w.w};
         uint32_t lo4[4], hi4[4];
 #pragma unroll
@@ -355,62 +378,88 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
                 Tw[(m * NU + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
             }
         }
-        if (++cu_r == NU) {
-            cu_r = 0;
-            if (++cu_c == C) {                            // unit done: ordered chains
-                cu_c = 0;
-                const int unit = cu_unit;
-                cu_unit += tw;
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-                if (lane < MR * UB) {
-                    const int m = lane / UB, uu = lane - m * UB, gr = unit * UB + uu;
-                    if (gr < n_total) {
-                        const float acc = chain_sum(Tw + (m * NU + uu) * Ts, G);
-                        if constexpr (PAIR) {
-                            const float up = chain_sum(Tw + (m * NU + UB + uu) * Ts, G);
-                            ml.out[0][static_cast<size_t>(m) * ml.n_out[0] + gr] = silu_mul(acc, up);
-                        } else {
-                            // the host picks UB dividing every n_out, so a unit
-                            // never straddles two matrices and p is wave-uniform
-                            const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
-                            const int no = sel4(p, ml.n_out[0], ml.n_out[1], ml.n_out[2], ml.n_out[3]);
-                            const int rb = sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2],
-                                                ml.row_begin[3]);
-                            pick(ml.out, p)[static_cast<size_t>(m) * no + (gr - rb)] = acc;
-                        }
-                    }
+    };
+    // a finished unit: one lane per (m, row) adds the row's terms in
+    // ascending group order
+    auto finish = [&](int unit) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (lane < MR * UB) {
+            const int m = lane / UB, uu = lane - m * UB, gr = unit * UB + uu;
+            if (gr < n_total) {
+                const float acc = chain_sum(Tw + (m * NU + uu) * Ts, G);
+                if constexpr (PAIR) {
+                    const float up = chain_sum(Tw + (m * NU + UB + uu) * Ts, G);
+                    ml.out[0][static_cast<size_t>(m) * ml.n_out[0] + gr] = silu_mul(acc, up);
+                } else {
+                    // the host picks UB dividing every n_out, so a unit
+                    // never straddles two matrices and p is wave-uniform
+                    const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, unit * UB));
+                    const int no = sel4(p, ml.n_out[0], ml.n_out[1], ml.n_out[2], ml.n_out[3]);
+                    const int rb = sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2],
+                                        ml.row_begin[3]);
+                    // through a buffer resource: a store through the selected
+                    // pointer would be a flat store, which makes every later
+                    // wait on the ring a full one
+                    const __amdgpu_buffer_rsrc_t ro =
+                        buf_rsrc(pick(ml.out, p), static_cast<uint32_t>(MR * no) * 4u);
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ro,
+                                                          (m * no + (gr - rb)) * 4, 0, 0);
                 }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
-    auto refill = [&](Item& slot) {
-        load_item<PAIR>(slot, ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, true);
-        if (++pf_r == NU) { pf_r = 0; if (++pf_c == C) { pf_c = 0; pf_unit += tw; } }
-    };
-    // steady state: every refill is live and unconditional (exact waits)
-    int q0 = 0;
-    for (; q0 + 2 * RING <= Q; q0 += RING) {
+    if (has_work) {                                               // uniform
+        const int cyc_per_unit = items / RING;
+        int cyc_pf = 1;                                           // the first ring: cycle 0
+        int cyc_cu = 0, cu_c = 0, cu_r = 0;                       // consume cursor (uniform)
+        int cu_unit = first_unit;
+        // the prefetch cursor has issued every cycle of its unit: move it to
+        // the claimed unit, or report that the wave has none left
+        auto next_unit = [&]() -> bool {
+            const int u = blockIdx.x + __builtin_amdgcn_readfirstlane(claimed) * grid;
+            if (u >= n_units) return false;
+            pf_unit = u;
+            pf_c = 0;
+            pf_r = 0;
+            cyc_pf = 0;
+            claimed = claim();
+            return true;
+        };
+        // one exit, at the bottom: the ring keeps its registers across cycles
+        bool more = cyc_pf < cyc_per_unit || next_unit();
+        while (more) {
+#pragma unroll
+            for (int d = 0; d < RING; d++) {
+                consume(ring[d], cu_c, cu_r);
+                if (++cu_r == NU) { cu_r = 0; ++cu_c; }
+                // the refill may not be scheduled above the consume of its
+                // slot, so that the slot keeps its registers
+                __builtin_amdgcn_sched_barrier(0);
+                load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, true);
+                if (++pf_r == NU) { pf_r = 0; ++pf_c; }
+            }
+            ++cyc_pf;
+            if (++cyc_cu == cyc_per_unit) {                       // uniform: unit done
+                finish(cu_unit);
+                cu_unit = pf_unit;
+                cyc_cu = 0;
+                cu_c = 0;
+                cu_r = 0;
+            }
+            more = cyc_pf < cyc_per_unit || next_unit();
+        }
+        // the last cycle of the last unit
 #pragma unroll
         for (int d = 0; d < RING; d++) {
-            consume(ring[d]);
-            refill(ring[d]);
+            consume(ring[d], cu_c, cu_r);
+            if (++cu_r == NU) { cu_r = 0; ++cu_c; }
         }
-    }
-    // tail: RING..2*RING-1 items left (a working wave has Q >= RING)
-    if (q0 < Q) {                                                 // uniform
-#pragma unroll
-        for (int d = 0; d < RING; d++) {
-            consume(ring[d]);
-            if (q0 + RING + d < Q) refill(ring[d]);               // uniform
-        }
-#pragma unroll
-        for (int d = 0; d < RING; d++)
-            if (q0 + RING + d < Q) consume(ring[d]);              // uniform
+        finish(cu_unit);
     }
 }
 

@@ -76,6 +76,8 @@ int num_cus() {
     Q4_STREAM_EXTERN(MR, RW, PAIR, 1) Q4_STREAM_EXTERN(MR, RW, PAIR, 2) Q4_STREAM_EXTERN(MR, RW, PAIR, 4) \
     extern template int stream_blocks_per_cu<MR, RW, PAIR>(int, size_t);
 Q4_STREAM_RINGS(1, 1, false) Q4_STREAM_RINGS(1, 2, false) Q4_STREAM_RINGS(1, 3, false) Q4_STREAM_RINGS(1, 4, false)
+Q4_STREAM_EXTERN(1, 1, false, 5) Q4_STREAM_EXTERN(1, 2, false, 5) Q4_STREAM_EXTERN(1, 3, false, 5)
+Q4_STREAM_EXTERN(1, 4, false, 5)
 Q4_STREAM_RINGS(1, 1, true) Q4_STREAM_RINGS(1, 2, true)
 Q4_STREAM_RINGS(2, 1, false) Q4_STREAM_RINGS(2, 2, false)
 Q4_STREAM_RINGS(2, 1, true) Q4_STREAM_RINGS(2, 2, true)
@@ -614,11 +616,11 @@ int launch_stream_rw(const MatList& ml, const float* x, int n_in, int UB, int nw
     const int want = (n_units + nwaves - 1) / nwaves;
     const int cap = num_cus() * per_cu;                 // every workgroup resident at once
     const int grid = want < cap ? want : cap;
-    // ring: the largest of 8, 2, 1 items that every working wave has
-    const int per_wave = n_units / (grid * nwaves);
-    const int qmin = (per_wave > 0 ? per_wave : 1) * items;
-    if (qmin >= 4) return launch_stream_k<MR, RW, PAIR, 4>(ml, x, n_in, UB, nwaves, lds, grid, st);
-    if (qmin >= 2) return launch_stream_k<MR, RW, PAIR, 2>(ml, x, n_in, UB, nwaves, lds, grid, st);
+    // ring: a divisor of the unit's items (units change only between rings)
+    if (items % 4 == 0) return launch_stream_k<MR, RW, PAIR, 4>(ml, x, n_in, UB, nwaves, lds, grid, st);
+    if constexpr (MR == 1 && !PAIR)
+        if (items % 5 == 0) return launch_stream_k<MR, RW, PAIR, 5>(ml, x, n_in, UB, nwaves, lds, grid, st);
+    if (items % 2 == 0) return launch_stream_k<MR, RW, PAIR, 2>(ml, x, n_in, UB, nwaves, lds, grid, st);
     return launch_stream_k<MR, RW, PAIR, 1>(ml, x, n_in, UB, nwaves, lds, grid, st);
 }
 
