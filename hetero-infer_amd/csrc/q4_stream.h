@@ -145,13 +145,16 @@ __device__ __forceinline__ void load_item(Item& it, const MatList& ml, int unit,
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(pick(ml.b, p) + static_cast<size_t>(o) * G, gbytes);
     // the three loads in a fixed order wherever an item is loaded: the
     // partial waits on the ring are computed from the issue order, which
-    // must then be the same on entry to the main loop as around it
+    // must then be the same on entry to the main loop as around it.  Read
+    // once, so non-temporal (cache policy nt): the stream does not push x
+    // and the outputs out of L2 and the last-level cache.
+    constexpr int kNonTemporal = 2;
     __builtin_amdgcn_sched_barrier(0);
-    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, word0 * 4, 0, 0));
+    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, word0 * 4, 0, kNonTemporal));
     __builtin_amdgcn_sched_barrier(0);
-    it.s = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
+    it.s = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, kNonTemporal);
     __builtin_amdgcn_sched_barrier(0);
-    it.b = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
+    it.b = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, kNonTemporal);
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -248,9 +251,15 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
 
-    // ---- stage the floats in LDS (the term tables' space, free until the
-    //      main loop) and take the running max |x| (kernel/q4gemv.c:258-259,
-    //      NaN-skipping) per row
+    // ---- group sums (kernel/q4gemv.c:244-248: the group's 64 values added
+    //      in ascending order) and the running max |x| (:258-259,
+    //      NaN-skipping) per row.  A group is 8 consecutive words, so it
+    //      lies in 8 consecutive lanes of one wave.  With one word per
+    //      thread the wave chains its groups itself, lane after lane
+    //      (row_shr:1), while it waits for the other waves' x; otherwise
+    //      the floats are staged in LDS (the term tables' space, free until
+    //      the main loop) and one thread per group chains them after the
+    //      barrier.
     float* stage = red + MR * 16 + 4;
 #pragma unroll
     for (int m = 0; m < MR; m++) {
@@ -259,7 +268,23 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
         for (int r = 0; r < RW; r++)
             if (r * nt + wave * 64 < wpr) {                       // uniform
                 const int j = r * nt + tid;
-                if (j < wpr) {
+                if constexpr (RW == 1) {
+                    const float v8[8] = {wv[m][r][0].x, wv[m][r][0].y, wv[m][r][0].z, wv[m][r][0].w,
+                                         wv[m][r][1].x, wv[m][r][1].y, wv[m][r][1].z, wv[m][r][1].w};
+                    const int sub = lane & 7;
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int step = 0; step < 8; step++) {
+                        // lane 8k+step continues the chain of lane 8k+step-1
+                        float a = step == 0 ? 0.0f
+                                            : __int_as_float(__builtin_amdgcn_update_dpp(
+                                                  0, __float_as_int(acc), 0x111, 0xF, 0xF, false));
+#pragma unroll
+                        for (int i = 0; i < 8; i++) a = __fadd_rn(a, v8[i]);
+                        acc = sub == step ? a : acc;
+                    }
+                    if (sub == 7 && j < wpr) xsum_lds[m * Gr + (j >> 3)] = acc;
+                } else if (j < wpr) {
                     float4* dst = reinterpret_cast<float4*>(stage + (m * G + (j >> 3)) * kStageStride + 8 * (j & 7));
                     dst[0] = wv[m][r][0];
                     dst[1] = wv[m][r][1];
@@ -287,9 +312,9 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     };
     int claimed = claim();
 
-    // ---- group sums: one thread per (row, group) chains its 64 values in
-    //      ascending order (kernel/q4gemv.c:244-248)
-    if (tid < MR * G) {
+    // ---- group sums from the staged floats: one thread per (row, group)
+    //      chains its 64 values in ascending order
+    if (RW > 1 && tid < MR * G) {
         const float4* gp = reinterpret_cast<const float4*>(stage + tid * kStageStride);
         float sum = 0.0f;
 #pragma unroll
