@@ -4,10 +4,11 @@ The library sits where the reference's ctypes loader looks for its CPU
 kernel (hetero/cpu_model.py:35-37: <package parent>/kernel/libq4gemv.so), so
 hetero/cpu_model.py here loads it the same way.
 
-csrc/q4gemv.hip (host code, C-ABI and the other kernels) and the instances
-of the streaming GEMV kernel (csrc/q4_stream_inst.hip, once per activation
-rows x gate/up pair x ring size) are compiled as separate objects in
-parallel, then linked into one shared library.
+csrc/q4gemv.hip (host code, C-ABI and the other kernels), csrc/q4_decode.hip
+(the decode-step kernels of include/q4decode.h) and the instances of the
+streaming GEMV kernel (csrc/q4_stream_inst.hip, once per activation rows x
+gate/up pair x ring size) are compiled as separate objects in parallel, then
+linked into one shared library.
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 SRC = os.path.join(CSRC, "q4gemv.hip")
+DECODE = os.path.join(CSRC, "q4_decode.hip")
 INST = os.path.join(CSRC, "q4_stream_inst.hip")
 OUT = os.path.join(HERE, "kernel", "libq4gemv.so")
 
@@ -58,7 +60,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
     jobs = jobs or min(16, os.cpu_count() or 4)
     with tempfile.TemporaryDirectory(prefix="q4build") as tmpd:
-        units = [(SRC, os.path.join(tmpd, "q4gemv.o"), [])]
+        units = [(SRC, os.path.join(tmpd, "q4gemv.o"), []), (DECODE, os.path.join(tmpd, "q4_decode.o"), [])]
         for mr, pair, ring in STREAM_INSTANCES:
             obj = os.path.join(tmpd, f"stream_m{mr}_p{pair}_r{ring}.o")
             units.append((INST, obj, [f"-DQ4_MR={mr}", f"-DQ4_PAIR={pair}", f"-DQ4_RING={ring}"]))

@@ -1,0 +1,379 @@
+// Decode-step kernels of the device-resident Qwen2 stage (gfx950): the
+// operations around the int4 GEMVs that the reference's NumPy stage
+// (hetero/cpu_model.py) runs on the host.  Declared in q4decode.h.
+//
+// Elementwise fp32 arithmetic follows the reference's expression order with
+// -ffp-contract=off (explicit _rn operations), so RoPE and the bias adds give
+// the NumPy bits; the reductions (RMSNorm's mean, the softmax sums, the
+// attention dot products) are tree reductions, not NumPy's pairwise order.
+#include "q4_common.h"
+#include "q4decode.h"
+
+namespace q4k {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ float wave_maxf(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ uint16_t f2h_rne(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+__device__ __forceinline__ float h2f_bits(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// ------------------------------------------------------------ embedding ---
+// hetero/cpu_model.py:334-338 (Stage.embed) / :67-81 (dequantize):
+// value 8j+n of the row = q * scale + bias with q * scale exact, so one fma.
+__global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
+                                                    const uint16_t* __restrict__ bi, const int64_t* __restrict__ tok,
+                                                    float* __restrict__ out, int n_rows, int n_in, int gs) {
+    const int wpr = n_in >> 3, G = n_in / gs;
+    const int64_t t = *tok;
+    const int row = (t >= 0 && t < n_rows) ? static_cast<int>(t) : (t < 0 ? 0 : n_rows - 1);
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= wpr) return;
+    const uint32_t word = w[static_cast<size_t>(row) * wpr + j];
+    const size_t si = static_cast<size_t>(row) * G + (8 * j) / gs;
+    const float s = h2f_bits(sc[si]), b = h2f_bits(bi[si]);
+    float v[8];
+#pragma unroll
+    for (int n = 0; n < 8; n++) v[n] = __builtin_fmaf(static_cast<float>((word >> (4 * n)) & 0xFu), s, b);
+    float4* o4 = reinterpret_cast<float4*>(out + 8 * static_cast<size_t>(j));
+    o4[0] = make_float4(v[0], v[1], v[2], v[3]);
+    o4[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// ------------------------------------------------ residual add + RMSNorm ---
+// hetero/cpu_model.py:164-166: x * (1 / sqrt(mean(x * x) + eps)) * w, after
+// the residual add of :304-306.  One workgroup; n <= 8 * 1024.
+constexpr int kNormPer = 8;
+__global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ delta,
+                                                          const float* __restrict__ w, float eps,
+                                                          float* __restrict__ y, int n) {
+    __shared__ float red[16];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    float v[kNormPer];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kNormPer; k++) {
+        const int i = k * nt + tid;
+        v[k] = 0.0f;
+        if (i < n) {
+            float a = x[i];
+            if (delta) {
+                a = __fadd_rn(a, delta[i]);
+                x[i] = a;
+            }
+            v[k] = a;
+            ss = __fadd_rn(ss, __fmul_rn(a, a));
+        }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < (nt >> 6); i++) tot = __fadd_rn(tot, red[i]);
+    const float ms = __fdiv_rn(tot, static_cast<float>(n));
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+#pragma unroll
+    for (int k = 0; k < kNormPer; k++) {
+        const int i = k * nt + tid;
+        if (i < n) y[i] = __fmul_rn(__fmul_rn(v[k], r), w[i]);
+    }
+}
+
+// ------------------------------------------- bias + RoPE + KV-cache write ---
+// hetero/cpu_model.py:156-157 (bias), :195-204 (RoPE: x1*cos - x2*sin,
+// x1*sin + x2*cos on the two halves), :207-230 (cache at the position).
+// Items: [0, nh*half) query pairs, then nkv*half key pairs, then nkv*d values.
+__global__ __launch_bounds__(256) void rope_kv_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                      const float* __restrict__ v, const float* __restrict__ bias,
+                                                      const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                      const int64_t* __restrict__ pos_p, uint16_t* __restrict__ kc,
+                                                      uint16_t* __restrict__ vc, float* __restrict__ q_out, int nh,
+                                                      int nkv, int d, int cap) {
+    const int64_t pos = *pos_p;
+    const int half = d >> 1;
+    const int it = blockIdx.x * blockDim.x + threadIdx.x;
+    const int nq = nh * half, nk = nkv * half, nv = nkv * d;
+    if (pos < 0 || pos >= cap) {                   // no valid cache row: only q
+        if (it >= nq) return;
+    }
+    const size_t prow = static_cast<size_t>(pos < 0 ? 0 : (pos >= cap ? cap - 1 : pos));
+    if (it < nq + nk) {
+        const bool is_q = it < nq;
+        const int p = is_q ? it : it - nq;
+        const int head = p / half, i = p - head * half;
+        const float* src = is_q ? q : k;
+        const float* bsrc = is_q ? bias : bias + nh * d;
+        const int e1 = head * d + i, e2 = e1 + half;
+        const float x1 = __fadd_rn(src[e1], bsrc[e1]);
+        const float x2 = __fadd_rn(src[e2], bsrc[e2]);
+        const float c = cos_t[prow * half + i], s = sin_t[prow * half + i];
+        const float o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
+        const float o2 = __fadd_rn(__fmul_rn(x1, s), __fmul_rn(x2, c));
+        if (is_q) {
+            q_out[e1] = o1;
+            q_out[e2] = o2;
+        } else {
+            uint16_t* row = kc + (static_cast<size_t>(head) * cap + prow) * d;
+            row[i] = f2h_rne(o1);
+            row[i + half] = f2h_rne(o2);
+        }
+    } else if (it < nq + nk + nv) {
+        const int e = it - nq - nk;
+        const int head = e / d, i = e - head * d;
+        const float val = __fadd_rn(v[e], bias[(nh + nkv) * d + e]);
+        vc[(static_cast<size_t>(head) * cap + prow) * d + i] = f2h_rne(val);
+    }
+}
+
+// ---------------------------------------------------------- attention ---
+// hetero/cpu_model.py:233-252 for one query token: per query head,
+// s = (q . k_t) * scale over the positions t <= pos, p = exp(s - max s),
+// o = (sum p_t v_t) / (sum p_t).  Workgroup (chunk, kv head) takes 64
+// positions and the G = nh / nkv query heads that share the kv head, and
+// writes its partial (max, sum, unnormalised o); the combine launch merges
+// the chunks (o = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c).
+constexpr int kChunk = 64;
+constexpr int kMaxG = 8;          // query heads per kv head
+constexpr int kMaxD = 128;
+
+__global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restrict__ q,
+                                                           const uint16_t* __restrict__ kc,
+                                                           const uint16_t* __restrict__ vc,
+                                                           const int64_t* __restrict__ pos_p,
+                                                           float* __restrict__ part, int nh, int nkv, int d,
+                                                           int cap, float scale) {
+    __shared__ float q_s[kMaxG][kMaxD];
+    __shared__ uint32_t k_s[kChunk][kMaxD / 2 + 1];     // fp16 pairs, rows padded by one word
+    __shared__ uint32_t v_s[kChunk][kMaxD / 2 + 1];
+    __shared__ float p_s[kMaxG][kChunk];
+    const int chunk = blockIdx.x, kvh = blockIdx.y, n_chunks = gridDim.x;
+    const int G = nh / nkv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t pos = *pos_p;
+    const int c0 = chunk * kChunk;
+    const int64_t lim = pos + 1 < cap ? pos + 1 : cap;      // positions [0, lim)
+    const int valid = lim - c0 >= kChunk ? kChunk : static_cast<int>(lim - c0 > 0 ? lim - c0 : 0);
+    const int dp = d >> 1;                                   // fp16 pairs per row
+    float* my = part;                                        // [nh][n_chunks][d + 2]
+    if (valid == 0) {                                        // chunk past the position
+        for (int e = tid; e < G * (d + 2); e += blockDim.x) {
+            const int g = e / (d + 2), i = e - g * (d + 2);
+            float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2);
+            dst[i] = i == 0 ? -__builtin_inff() : 0.0f;
+        }
+        return;
+    }
+    for (int e = tid; e < G * d; e += blockDim.x) q_s[e / d][e % d] = q[static_cast<size_t>(kvh * G) * d + e];
+    const uint32_t* krow = reinterpret_cast<const uint32_t*>(kc + (static_cast<size_t>(kvh) * cap + c0) * d);
+    const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vc + (static_cast<size_t>(kvh) * cap + c0) * d);
+    for (int e = tid; e < valid * dp; e += blockDim.x) {
+        const int s = e / dp, i = e - s * dp;
+        k_s[s][i] = krow[e];
+        v_s[s][i] = vrow[e];
+    }
+    __syncthreads();
+    // scores: thread (g-set, s): heads g = wave, wave + 4
+    {
+        const int s = lane;
+        for (int g = wave; g < G; g += 4) {
+            float acc = 0.0f;
+            if (s < valid) {
+#pragma unroll 8
+                for (int i = 0; i < dp; i++) {
+                    const uint32_t kk = k_s[s][i];
+                    acc = __builtin_fmaf(q_s[g][2 * i], h2f_bits(static_cast<uint16_t>(kk)), acc);
+                    acc = __builtin_fmaf(q_s[g][2 * i + 1], h2f_bits(static_cast<uint16_t>(kk >> 16)), acc);
+                }
+            }
+            const float sc = s < valid ? __fmul_rn(acc, scale) : -__builtin_inff();
+            const float m = wave_maxf(sc);
+            const float p = s < valid ? expf(__fsub_rn(sc, m)) : 0.0f;
+            const float l = wave_sum(p);
+            p_s[g][s] = p;
+            if (lane == 0) {
+                float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2);
+                dst[0] = m;
+                dst[1] = l;
+            }
+        }
+    }
+    __syncthreads();
+    // unnormalised outputs: thread (g-set, dim pair)
+    for (int e = tid; e < G * dp; e += blockDim.x) {
+        const int g = e / dp, i = e - g * dp;
+        float a0 = 0.0f, a1 = 0.0f;
+        for (int s = 0; s < valid; s++) {
+            const uint32_t vv = v_s[s][i];
+            const float p = p_s[g][s];
+            a0 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(vv)), a0);
+            a1 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(vv >> 16)), a1);
+        }
+        float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2) + 2;
+        dst[2 * i] = a0;
+        dst[2 * i + 1] = a1;
+    }
+}
+
+__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                           int n_chunks, int d) {
+    const int h = blockIdx.x;
+    const float* base = part + static_cast<size_t>(h) * n_chunks * (d + 2);
+    float M = -__builtin_inff();
+    for (int c = 0; c < n_chunks; c++) M = fmaxf(M, base[static_cast<size_t>(c) * (d + 2)]);
+    for (int i = threadIdx.x; i < d; i += blockDim.x) {
+        float L = 0.0f, O = 0.0f;
+        for (int c = 0; c < n_chunks; c++) {
+            const float* pc = base + static_cast<size_t>(c) * (d + 2);
+            const float m = pc[0];
+            if (m == -__builtin_inff()) continue;
+            const float wgt = expf(__fsub_rn(m, M));
+            L = __builtin_fmaf(pc[1], wgt, L);
+            O = __builtin_fmaf(pc[2 + i], wgt, O);
+        }
+        out[static_cast<size_t>(h) * d + i] = __fdiv_rn(O, L);
+    }
+}
+
+// ---------------------------------------------------------------- argmax ---
+// hetero/backends.py:106-109: np.argmax, the first index of the maximum.
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                      int64_t* __restrict__ tok, int64_t* __restrict__ hist,
+                                                      int64_t* __restrict__ pos, int64_t s0, int hist_len) {
+    __shared__ float rv[16];
+    __shared__ int ri[16];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    float bv = -__builtin_inff();
+    int bi = 0x7FFFFFFF;
+    const int n4 = n >> 2;
+    const float4* l4 = reinterpret_cast<const float4*>(logits);
+    for (int i = tid; i < n4; i += nt) {
+        const float4 f = l4[i];
+        better(bv, bi, f.x, 4 * i);
+        better(bv, bi, f.y, 4 * i + 1);
+        better(bv, bi, f.z, 4 * i + 2);
+        better(bv, bi, f.w, 4 * i + 3);
+    }
+    for (int i = 4 * n4 + tid; i < n; i += nt) better(bv, bi, logits[i], i);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        better(bv, bi, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        rv[tid >> 6] = bv;
+        ri[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < (nt >> 6); w++) better(bv, bi, rv[w], ri[w]);
+        const int best = bi == 0x7FFFFFFF ? 0 : bi;
+        *tok = best;
+        const int64_t p = *pos;
+        const int64_t k = p - s0;
+        if (k >= 0 && k < hist_len) hist[k] = best;
+        *pos = p + 1;
+    }
+}
+
+int check_launch(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q4_EHIP, "%s launch: %s", what, hipGetErrorString(e));
+    return 0;
+}
+
+}  // namespace
+}  // namespace q4k
+
+using namespace q4k;
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+int q4_embed_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const int64_t* tok,
+                 float* out, int n_rows, int n_in, int gs, void* stream) {
+    if (!w || !scales || !biases || !tok || !out) return fail(Q4_EARG, "q4_embed_dev: null pointer");
+    if (n_rows <= 0 || n_in <= 0 || gs <= 0 || n_in % gs || gs % 8 || (reinterpret_cast<uintptr_t>(out) & 15))
+        return fail(Q4_EARG, "q4_embed_dev: bad sizes (n_rows %d, n_in %d, gs %d) or out not 16-byte aligned",
+                    n_rows, n_in, gs);
+    const int wpr = n_in / 8;
+    hipLaunchKernelGGL(embed_kernel, dim3((wpr + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream), w,
+                       scales, biases, tok, out, n_rows, n_in, gs);
+    return check_launch("q4_embed_dev");
+}
+
+int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, float* y, int n, void* stream) {
+    if (!x || !w || !y) return fail(Q4_EARG, "q4_add_rmsnorm_dev: null pointer");
+    if (n <= 0 || n > kNormPer * 1024) return fail(Q4_EARG, "q4_add_rmsnorm_dev: n = %d outside [1, %d]", n,
+                                                   kNormPer * 1024);
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), x, delta, w,
+                       eps, y, n);
+    return check_launch("q4_add_rmsnorm_dev");
+}
+
+int q4_rope_kv_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
+                   const float* sin_t, const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache, float* q_out,
+                   int n_heads, int n_kv, int head_dim, int cap, void* stream) {
+    if (!q || !k || !v || !bias || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !q_out)
+        return fail(Q4_EARG, "q4_rope_kv_dev: null pointer");
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || head_dim <= 0 || head_dim % 2 || cap <= 0)
+        return fail(Q4_EARG, "q4_rope_kv_dev: bad sizes (heads %d, kv heads %d, head_dim %d, cap %d)", n_heads,
+                    n_kv, head_dim, cap);
+    const int items = n_heads * (head_dim / 2) + n_kv * (head_dim / 2) + n_kv * head_dim;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((items + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       q, k, v, bias, cos_t, sin_t, pos, k_cache, v_cache, q_out, n_heads, n_kv, head_dim, cap);
+    return check_launch("q4_rope_kv_dev");
+}
+
+long q4_attention_scratch_floats(int n_heads, int head_dim, int cap) {
+    if (n_heads <= 0 || head_dim <= 0 || cap <= 0) return 0;
+    const long n_chunks = (cap + kChunk - 1) / kChunk;
+    return static_cast<long>(n_heads) * n_chunks * (head_dim + 2);
+}
+
+int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int64_t* pos,
+                     float* out, float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale,
+                     void* stream) {
+    if (!q || !k_cache || !v_cache || !pos || !out || !scratch) return fail(Q4_EARG, "q4_attention_dev: null pointer");
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kMaxG || head_dim <= 0 || head_dim % 2 ||
+        head_dim > kMaxD || cap <= 0)
+        return fail(Q4_EARG, "q4_attention_dev: unsupported sizes (heads %d, kv heads %d, head_dim %d, cap %d)",
+                    n_heads, n_kv, head_dim, cap);
+    const int n_chunks = (cap + kChunk - 1) / kChunk;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(attn_partial_kernel, dim3(n_chunks, n_kv), dim3(256), 0, st, q, k_cache, v_cache, pos,
+                       scratch, n_heads, n_kv, head_dim, cap, scale);
+    if (int rc = check_launch("q4_attention_dev (partial)")) return rc;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(128), 0, st, scratch, out, n_chunks, head_dim);
+    return check_launch("q4_attention_dev (combine)");
+}
+
+int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0, int hist_len,
+                  void* stream) {
+    if (!logits || !tok || !pos || (hist_len > 0 && !hist)) return fail(Q4_EARG, "q4_argmax_dev: null pointer");
+    if (n <= 0 || (reinterpret_cast<uintptr_t>(logits) & 15)) return fail(Q4_EARG, "q4_argmax_dev: bad n %d or logits not 16-byte aligned", n);
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), logits, n, tok, hist,
+                       pos, s0, hist_len);
+    return check_launch("q4_argmax_dev");
+}
+
+}  // extern "C"
+#pragma GCC visibility pop

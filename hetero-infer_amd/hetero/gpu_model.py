@@ -1,18 +1,22 @@
 """Device-resident Qwen2 decode step on one MI355X.
 
 The same stage as hetero/cpu_model.py (the reference's
-hetero/cpu_model.py:164-368), with every tensor resident in HBM:
-  * 4-bit projections through libq4gemv.so's device entry points: q/k/v in
-    one grouped launch (q4_gemv_multi_dev), o_proj and lm_head as single
-    launches, the MLP as the fused gate/up/SiLU*mul launch plus down
-    (q4_mlp_dev) -- every GEMV result is the reference q4_gemv's bit for bit;
-  * RMSNorm, RoPE, the fp16 KV cache and GQA attention as torch fp32 ops
-    (torch is plumbing here: device memory, streams, graph capture);
-  * greedy argmax on the device.
-The token id and the position live in device tensors and attention runs
-over the whole fixed-size cache with a position mask, so one decode step is
+hetero/cpu_model.py:164-368), with every tensor resident in HBM and every
+operation a kernel of libq4gemv.so:
+  * 4-bit projections through the streaming GEMV: q/k/v in one grouped launch
+    (q4_gemv_multi_dev), o_proj, the fused gate/up/SiLU*mul launch plus down
+    (q4_mlp_dev) and lm_head -- every GEMV result is the reference q4_gemv's
+    bit for bit given the same input;
+  * the rest from include/q4decode.h: the embedding row (q4_embed_dev), the
+    residual adds fused with the next RMSNorm (q4_add_rmsnorm_dev), bias +
+    RoPE + the fp16 KV-cache write (q4_rope_kv_dev), GQA attention split over
+    the context (q4_attention_dev) and the greedy argmax with the step's
+    bookkeeping (q4_argmax_dev).
+The token id and the position live in device tensors and attention covers
+positions [0, pos] of a fixed-size cache, so one decode step is
 position-independent and is captured once as a HIP graph; generating n
-tokens is n graph replays with no host work in between.
+tokens is n graph replays with no host work in between.  torch only
+allocates the buffers and captures the graph.
 """
 from __future__ import annotations
 
@@ -58,12 +62,13 @@ class GpuStage:
             p = f"model.layers.{i}"
             L = {
                 "qkv": [mat(f"{p}.self_attn.{x}_proj") for x in ("q", "k", "v")],
-                "qkv_bias": t(np.concatenate([w[f"{p}.self_attn.{x}_proj.bias"] for x in ("q", "k", "v")])),
+                "qkv_bias": t(np.concatenate([w[f"{p}.self_attn.{x}_proj.bias"] for x in ("q", "k", "v")])
+                              .astype(np.float32)),
                 "o": mat(f"{p}.self_attn.o_proj"),
                 "gate": mat(f"{p}.mlp.gate_proj"), "up": mat(f"{p}.mlp.up_proj"),
                 "down": mat(f"{p}.mlp.down_proj"),
-                "in_w": t(w[f"{p}.input_layernorm.weight"]),
-                "post_w": t(w[f"{p}.post_attention_layernorm.weight"]),
+                "in_w": t(w[f"{p}.input_layernorm.weight"].astype(np.float32)),      # cpu_model.py:298-299
+                "post_w": t(w[f"{p}.post_attention_layernorm.weight"].astype(np.float32)),
             }
             kc = torch.zeros((self.nkv, self.cap, self.hd), dtype=torch.float16, device=dev)
             vc = torch.zeros_like(kc)
@@ -71,7 +76,7 @@ class GpuStage:
             vc[:, :self.s0] = t(kv_v[i].astype(np.float16)).view(torch.float16)
             L["k_cache"], L["v_cache"] = kc, vc
             self.layers.append(L)
-        self.norm_w = t(w["model.norm.weight"])
+        self.norm_w = t(w["model.norm.weight"].astype(np.float32))
         self.lm_head = mat("lm_head")
         # RoPE table exactly as the reference builds it (cpu_model.py:180-193)
         half = self.hd // 2
@@ -91,69 +96,49 @@ class GpuStage:
         self.attn = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
         self.o = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
         self.logits = torch.zeros((1, cfg["vocab_size"]), dtype=torch.float32, device=dev)
-        self.emb_rows = [torch.zeros((1,) + tuple(a.shape[1:]), dtype=a.dtype, device=dev) for a in self.embed]
         self.positions = torch.arange(self.cap, device=dev)
         self.hist = torch.zeros(max_new, dtype=torch.int64, device=dev)   # token of each step
+        self.hn = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
+        self.q_rot = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
+        n_scr = self.lib.q4_attention_scratch_floats(self.nh, self.hd, self.cap)
+        self.attn_scratch = torch.zeros(n_scr, dtype=torch.float32, device=dev)
+        self.scale = float(np.float32(self.hd ** -0.5))            # cpu_model.py:261
         self.stream = torch.cuda.Stream(device=dev)
         self.graph = None
 
-    # -- pieces -------------------------------------------------------------
-    def _rms(self, x, w):                                               # cpu_model.py:164-166
-        return x * (1.0 / self.torch.sqrt((x * x).mean(-1, keepdim=True) + self.eps)) * w
-
-    def _rope(self, x, nheads):                                         # cpu_model.py:195-204
-        torch = self.torch
-        xh = x.view(nheads, self.hd)
-        cos = self.cos.index_select(0, self.pos)                        # [1, half]
-        sin = self.sin.index_select(0, self.pos)
-        half = self.hd // 2
-        x1, x2 = xh[:, :half], xh[:, half:]
-        return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)
-
-    def _attention(self, q, L):                                         # cpu_model.py:233-252
-        torch = self.torch
-        g = self.nh // self.nkv
-        kf = L["k_cache"].float()                                       # [KH, cap, D]
-        vf = L["v_cache"].float()
-        qh = q.view(self.nkv, g, self.hd).transpose(1, 2).contiguous()  # [KH, D, G]
-        s = torch.matmul(kf, qh) * (self.hd ** -0.5)                    # [KH, cap, G]
-        mask = (self.positions > self.pos).view(1, -1, 1)
-        s = s.masked_fill(mask, float("-inf"))
-        s = s - s.amax(dim=1, keepdim=True)
-        e = torch.exp(s)
-        e = e / e.sum(dim=1, keepdim=True)
-        p = e.transpose(1, 2).contiguous()                              # [KH, G, cap]
-        return torch.matmul(p, vf).reshape(1, self.h)                   # [KH, G, D] -> [1, H]
-
+    # -- one step -----------------------------------------------------------
     def _step(self):
-        torch = self.torch
         lib = self.lib
-        # embedding: gather the packed row on the device, dequantise it (cpu_model.py:334-338)
-        for dst, src in zip(self.emb_rows, self.embed):
-            dst.copy_(src.index_select(0, self.tok))
-        q4.dequant_dev(*self.emb_rows, 0, 1, out=self.x, lib=lib)
-        x = self.x
-        kvd = self.nkv * self.hd
-        for L in self.layers:                                           # cpu_model.py:304-306
-            hn = self._rms(x, L["in_w"]).contiguous()
-            q4.gemv_multi_dev(L["qkv"], hn, outs=[self.q, self.k, self.v], lib=lib)
-            b = L["qkv_bias"]
-            q = self._rope(self.q + b[:self.h], self.nh)
-            k = self._rope(self.k + b[self.h:self.h + kvd], self.nkv)
-            v = (self.v + b[self.h + kvd:]).view(self.nkv, self.hd)
-            L["k_cache"].index_copy_(1, self.pos, k.to(torch.float16).unsqueeze(1))
-            L["v_cache"].index_copy_(1, self.pos, v.to(torch.float16).unsqueeze(1))
-            self.attn.copy_(self._attention(q, L))
+        st = self.torch.cuda.current_stream().cuda_stream
+        ck = lambda rc, what: q4.check(lib, rc, what)
+        P = lambda t: t.data_ptr()
+        h, gs = self.h, self.gs
+        ew, es, eb = self.embed
+        # embedding row (cpu_model.py:334-338), then the first RMSNorm
+        ck(lib.q4_embed_dev(P(ew), P(es), P(eb), P(self.tok), P(self.x), ew.shape[0], h, gs, st), "embed")
+        ck(lib.q4_add_rmsnorm_dev(P(self.x), None, P(self.layers[0]["in_w"]), self.eps, P(self.hn), h, st),
+           "rmsnorm")
+        for i, L in enumerate(self.layers):                             # cpu_model.py:304-306
+            q4.gemv_multi_dev(L["qkv"], self.hn, outs=[self.q, self.k, self.v], lib=lib)
+            ck(lib.q4_rope_kv_dev(P(self.q), P(self.k), P(self.v), P(L["qkv_bias"]), P(self.cos), P(self.sin),
+                                  P(self.pos), P(L["k_cache"]), P(L["v_cache"]), P(self.q_rot),
+                                  self.nh, self.nkv, self.hd, self.cap, st), "rope_kv")
+            ck(lib.q4_attention_dev(P(self.q_rot), P(L["k_cache"]), P(L["v_cache"]), P(self.pos), P(self.attn),
+                                    P(self.attn_scratch), self.nh, self.nkv, self.hd, self.cap, self.scale, st),
+               "attention")
             q4.gemv_dev(*L["o"], self.attn, out=self.o, lib=lib)
-            x = x + self.o
-            hn2 = self._rms(x, L["post_w"]).contiguous()
-            q4.mlp_dev(L["gate"], L["up"], L["down"], hn2, h=self.hbuf, out=self.mlp_out, lib=lib)
-            x = x + self.mlp_out
-        xn = self._rms(x, self.norm_w).contiguous()
-        q4.gemv_dev(*self.lm_head, xn, out=self.logits, lib=lib)
-        self.tok.copy_(self.logits.argmax(dim=-1))                      # backends.py:106-109
-        self.hist.index_copy_(0, (self.pos - self.s0).clamp_(0, self.hist.numel() - 1), self.tok)
-        self.pos.add_(1)
+            # x = x + attn; hn = rms_norm(x, post_w)
+            ck(lib.q4_add_rmsnorm_dev(P(self.x), P(self.o), P(L["post_w"]), self.eps, P(self.hn), h, st),
+               "add_rmsnorm")
+            q4.mlp_dev(L["gate"], L["up"], L["down"], self.hn, h=self.hbuf, out=self.mlp_out, lib=lib)
+            # x = x + mlp; hn = the next layer's input norm, or the final norm
+            nxt = self.layers[i + 1]["in_w"] if i + 1 < len(self.layers) else self.norm_w
+            ck(lib.q4_add_rmsnorm_dev(P(self.x), P(self.mlp_out), P(nxt), self.eps, P(self.hn), h, st),
+               "add_rmsnorm")
+        q4.gemv_dev(*self.lm_head, self.hn, out=self.logits, lib=lib)
+        # greedy token (backends.py:106-109), history slot, position + 1
+        ck(lib.q4_argmax_dev(P(self.logits), self.logits.shape[1], P(self.tok), P(self.hist), P(self.pos),
+                             self.s0, self.hist.numel(), st), "argmax")
 
     # -- driving --------------------------------------------------------------
     def capture(self):

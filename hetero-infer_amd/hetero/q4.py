@@ -21,11 +21,14 @@ LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
 
 EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
            "q4_last_error", "q4_gemv_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
-           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_dequant_dev", "q4_dequant_bf16_dev")
+           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_dequant_dev", "q4_dequant_bf16_dev",
+           # decode-step kernels (include/q4decode.h)
+           "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
+           "q4_attention_dev", "q4_argmax_dev")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
-_VP, _I = ctypes.c_void_p, ctypes.c_int
+_VP, _I, _F, _L = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_long
 
 
 def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
@@ -57,6 +60,19 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_dequant_dev.restype = _I
         lib.q4_dequant_bf16_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
         lib.q4_dequant_bf16_dev.restype = _I
+    if hasattr(lib, "q4_embed_dev"):
+        lib.q4_embed_dev.argtypes = [_VP] * 5 + [_I] * 3 + [_VP]
+        lib.q4_embed_dev.restype = _I
+        lib.q4_add_rmsnorm_dev.argtypes = [_VP] * 3 + [_F, _VP, _I, _VP]
+        lib.q4_add_rmsnorm_dev.restype = _I
+        lib.q4_rope_kv_dev.argtypes = [_VP] * 10 + [_I] * 4 + [_VP]
+        lib.q4_rope_kv_dev.restype = _I
+        lib.q4_attention_scratch_floats.argtypes = [_I] * 3
+        lib.q4_attention_scratch_floats.restype = _L
+        lib.q4_attention_dev.argtypes = [_VP] * 6 + [_I] * 4 + [_F, _VP]
+        lib.q4_attention_dev.restype = _I
+        lib.q4_argmax_dev.argtypes = [_VP, _I, _VP, _VP, _VP, ctypes.c_int64, _I, _VP]
+        lib.q4_argmax_dev.restype = _I
     return lib
 
 

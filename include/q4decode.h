@@ -1,0 +1,77 @@
+/* Decode-step kernels of the device-resident Qwen2 stage on MI355X (gfx950).
+ *
+ * These are the device counterparts of the NumPy operations around the int4
+ * GEMVs in the reference stage (hetero/cpu_model.py).  The reference runs them
+ * on the host; here they run on the GPU so that a whole decode step is one
+ * HIP graph replay with every tensor resident in HBM.  They have no
+ * counterpart in the reference's kernel ABI (kernel/q4gemv.c), so they sit in
+ * a header of their own.
+ *
+ * All pointers are device pointers; every call is asynchronous on `stream`
+ * (a hipStream_t, NULL = the null stream) and capturable in a HIP graph (no
+ * allocation, no memset).  The decode position and the token live in device
+ * memory (int64), so a captured step is position-independent.
+ *
+ * Return codes as in q4gemv.h: 0 success, Q4_EHIP, Q4_EARG (text in
+ * q4_last_error()).
+ */
+#ifndef Q4DECODE_H
+#define Q4DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Embedding row of token *tok (clamped into [0, n_rows)) dequantised to fp32:
+ * out[i] = fma(q, scale, bias) of row *tok of the packed table, as
+ * hetero/cpu_model.py:334-338 (Stage.embed) and :67-81 (dequantize) compute
+ * it.  w [n_rows][n_in/8], scales/biases fp16 [n_rows][n_in/gs]. */
+int q4_embed_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const int64_t* tok,
+                 float* out, int n_rows, int n_in, int gs, void* stream);
+
+/* Residual add and RMSNorm (hetero/cpu_model.py:164-166 rms_norm, :304-306
+ * the residual adds of DecoderLayer): if delta is not NULL, x += delta
+ * (in place); then y = x * (1 / sqrt(mean(x*x) + eps)) * w.  n <= 8192. */
+int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, float* y, int n,
+                       void* stream);
+
+/* q/k/v projection biases, rotary embedding and the KV-cache write at the
+ * position *pos (hetero/cpu_model.py:156-157 QLinear bias, :195-204 RoPE
+ * non-traditional half split, :207-230 KVCache.update_and_fetch):
+ *   q_out = rope(q + bias[0:nh*d]),  k = rope(k + bias[nh*d : (nh+nkv)*d]),
+ *   v = v + bias[(nh+nkv)*d :]; k and v are stored as fp16 (round to nearest
+ *   even) at [kv head][*pos][:] of k_cache / v_cache [nkv][cap][d].
+ * cos_t / sin_t are the fp32 tables [cap][d/2] (angle = position * inv_freq).
+ * Nothing is written when *pos is outside [0, cap). */
+int q4_rope_kv_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
+                   const float* sin_t, const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache,
+                   float* q_out, int n_heads, int n_kv, int head_dim, int cap, void* stream);
+
+/* Floats of scratch memory q4_attention_dev needs for these sizes. */
+long q4_attention_scratch_floats(int n_heads, int head_dim, int cap);
+
+/* Grouped-query attention of one query token over cache positions
+ * [0, *pos] (hetero/cpu_model.py:233-252 sdpa: scores q.k * scale, softmax
+ * with the maximum subtracted, weighted sum of v; query head h uses kv head
+ * h / (n_heads / n_kv)).  q [n_heads][d] fp32, caches fp16 [nkv][cap][d],
+ * out [n_heads][d] fp32.  The context is split in chunks of 64 positions
+ * (one workgroup per kv head and chunk), whose partial softmax results are
+ * combined by a second launch; scratch holds them
+ * (q4_attention_scratch_floats). */
+int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int64_t* pos,
+                     float* out, float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale,
+                     void* stream);
+
+/* Greedy token (hetero/backends.py:106-109, NumpyBackend.sample: argmax,
+ * the first index of the maximum) and the step's bookkeeping: *tok = argmax,
+ * hist[*pos - s0] = *tok when that index is in [0, hist_len), *pos += 1. */
+int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0,
+                  int hist_len, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4DECODE_H */

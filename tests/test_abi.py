@@ -2,7 +2,7 @@
 
 * the library is built in-tree where the reference's loader looks
   (hetero/cpu_model.py:35-37: <package parent>/kernel/libq4gemv.so);
-* it exports every function include/q4gemv.h declares, and the ctypes
+* it exports every function include/*.h declares, and the ctypes
   declarations match the reference's for the two drop-in symbols
   (hetero/cpu_model.py:41-44);
 * shape errors return the reference's codes before any HIP call
@@ -18,13 +18,20 @@ import pytest
 from hetero import q4
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "q4gemv.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("q4gemv.h", "q4decode.h")]
 
 
 def header_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(q4_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(q4_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_every_header_is_checked():
+    assert sorted(HEADERS) == sorted(os.path.join(ROOT, "include", h)
+                                     for h in os.listdir(os.path.join(ROOT, "include")) if h.endswith(".h"))
 
 
 @pytest.fixture(scope="module")
@@ -93,3 +100,19 @@ def test_zero_rows_are_noops(lib):
 def test_release_without_registrations(lib):
     assert lib.q4_release(None) == 0
     assert lib.q4_release_all() >= 0
+
+
+def test_decode_kernel_argument_errors(lib):
+    """Argument checks of the decode-step entry points, before any launch."""
+    assert lib.q4_add_rmsnorm_dev(None, None, None, 1e-6, None, 16, None) == q4.Q4_EARG
+    x = np.zeros(16, np.float32)
+    p = x.ctypes.data
+    assert lib.q4_add_rmsnorm_dev(p, None, p, 1e-6, p, 0, None) == q4.Q4_EARG
+    assert lib.q4_add_rmsnorm_dev(p, None, p, 1e-6, p, 8193, None) == q4.Q4_EARG
+    assert lib.q4_embed_dev(p, p, p, p, p, 10, 100, 64, None) == q4.Q4_EARG          # n_in % gs
+    assert lib.q4_rope_kv_dev(*([p] * 10), 28, 5, 128, 64, None) == q4.Q4_EARG      # heads % kv heads
+    assert lib.q4_attention_dev(*([p] * 6), 72, 4, 128, 64, 0.1, None) == q4.Q4_EARG  # 18 heads per kv head
+    assert lib.q4_attention_dev(*([p] * 6), 28, 4, 256, 64, 0.1, None) == q4.Q4_EARG  # head_dim > 128
+    assert lib.q4_argmax_dev(None, 10, p, p, p, 0, 1, None) == q4.Q4_EARG
+    assert lib.q4_attention_scratch_floats(28, 128, 2048) == 28 * 32 * 130
+    assert lib.q4_attention_scratch_floats(28, 128, 2049) == 28 * 33 * 130
