@@ -157,7 +157,7 @@ def decode_weights(torch, cfg, dev, seed=99):
     return host, kv_k, kv_v
 
 
-def decode_bench(torch, dev, steps=128, start_token=151643, ref_rows=1, ref_threads=16):
+def decode_bench(torch, dev, steps=128, start_token=151643, ref_rows=1, ref_threads=16, check=True):
     """Qwen2.5-7B-architecture decode step (28 layers, fp16 KV cache at 2048
     context, greedy over 152064): device-resident tok/s, and token agreement
     with the NumPy stage running the reference kernel on the host."""
@@ -184,7 +184,7 @@ def decode_bench(torch, dev, steps=128, start_token=151643, ref_rows=1, ref_thre
                        "random-init 4-bit weights, fp16 KV cache at 2048 context, greedy over 152064, "
                        f"{steps} steps, one HIP graph replay per token",
            "tok_s": round(steps / dev_s, 1), "ms_per_token": round(dev_s * 1e3 / steps, 3)}
-    ref = reference_decode(cfg, w, kv_k, kv_v, steps, start_token, ref_rows, ref_threads)
+    ref = reference_decode(cfg, w, kv_k, kv_v, steps, start_token, ref_rows, ref_threads) if check else None
     if ref is not None:
         ref_tokens, ref_s = ref
         free = sum(int(a == b) for a, b in zip(dev_tokens, ref_tokens))
@@ -318,6 +318,10 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--sweep-only", action="store_true",
                     help="only the grouped decode sweep (for rocprof runs)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode step (for rocprof runs)")
+    ap.add_argument("--no-decode-check", action="store_true",
+                    help="skip the token-agreement run of the NumPy stage on the host")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a 256 MiB device copy: the known-size reference for PMC byte counters")
     args = ap.parse_args()
@@ -331,6 +335,10 @@ def main():
     from hetero import q4
     lib = q4.load()
     dev = torch.device("cuda:0")
+    if args.decode_only:
+        res = decode_bench(torch, dev, steps=args.decode_steps, check=not args.no_decode_check)
+        print(json.dumps({"decode": res}), flush=True)
+        return
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
     t_setup = time.perf_counter()

@@ -149,16 +149,28 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const float* __restrict__ 
 constexpr int kChunk = 64;
 constexpr int kMaxG = 8;          // query heads per kv head
 constexpr int kMaxD = 128;
+constexpr int kRowU4 = kMaxD / 8 + 1;   // LDS row of a chunk: 16 uint4 of fp16 + 1 pad (16-byte reads spread over the banks)
+constexpr int kMaxChunks = 1024;        // cap <= 65536
 
+// ROPE: q, k and v are the raw projection outputs; the workgroup applies
+// the biases and the rotary embedding to its G query heads (as
+// rope_kv_kernel does), and the workgroup whose chunk holds the position
+// also rotates the new key, writes the new key and value rows to the cache
+// and takes them from registers instead of the cache.
+template <bool ROPE>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restrict__ q,
-                                                           const uint16_t* __restrict__ kc,
-                                                           const uint16_t* __restrict__ vc,
+                                                           uint16_t* __restrict__ kc,
+                                                           uint16_t* __restrict__ vc,
                                                            const int64_t* __restrict__ pos_p,
                                                            float* __restrict__ part, int nh, int nkv, int d,
-                                                           int cap, float scale) {
-    __shared__ float q_s[kMaxG][kMaxD];
-    __shared__ uint32_t k_s[kChunk][kMaxD / 2 + 1];     // fp16 pairs, rows padded by one word
-    __shared__ uint32_t v_s[kChunk][kMaxD / 2 + 1];
+                                                           int cap, float scale, const float* __restrict__ kraw,
+                                                           const float* __restrict__ vraw,
+                                                           const float* __restrict__ bias,
+                                                           const float* __restrict__ cos_t,
+                                                           const float* __restrict__ sin_t) {
+    __shared__ float4 q_s[kMaxG][kMaxD / 4];
+    __shared__ uint4 k_s[kChunk][kRowU4];
+    __shared__ uint4 v_s[kChunk][kRowU4];
     __shared__ float p_s[kMaxG][kChunk];
     const int chunk = blockIdx.x, kvh = blockIdx.y, n_chunks = gridDim.x;
     const int G = nh / nkv;
@@ -167,7 +179,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     const int c0 = chunk * kChunk;
     const int64_t lim = pos + 1 < cap ? pos + 1 : cap;      // positions [0, lim)
     const int valid = lim - c0 >= kChunk ? kChunk : static_cast<int>(lim - c0 > 0 ? lim - c0 : 0);
-    const int dp = d >> 1;                                   // fp16 pairs per row
+    const int du4 = d >> 3;                                  // uint4 (8 fp16) per row
     float* my = part;                                        // [nh][n_chunks][d + 2]
     if (valid == 0) {                                        // chunk past the position
         for (int e = tid; e < G * (d + 2); e += blockDim.x) {
@@ -177,26 +189,125 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         }
         return;
     }
-    for (int e = tid; e < G * d; e += blockDim.x) q_s[e / d][e % d] = q[static_cast<size_t>(kvh * G) * d + e];
-    const uint32_t* krow = reinterpret_cast<const uint32_t*>(kc + (static_cast<size_t>(kvh) * cap + c0) * d);
-    const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vc + (static_cast<size_t>(kvh) * cap + c0) * d);
-    for (int e = tid; e < valid * dp; e += blockDim.x) {
-        const int s = e / dp, i = e - s * dp;
-        k_s[s][i] = krow[e];
-        v_s[s][i] = vrow[e];
+    // the chunk's new row (the position) comes from registers, not the cache
+    const bool fresh = ROPE && pos >= c0 && pos < c0 + kChunk && pos < cap;
+    // every load up front: q, the chunk's K and V rows (4 uint4 each per
+    // thread at d = 128); rows past `valid` (and a fresh row) are not read
+    const uint4* k4p = reinterpret_cast<const uint4*>(kc + (static_cast<size_t>(kvh) * cap + c0) * d);
+    const uint4* v4p = reinterpret_cast<const uint4*>(vc + (static_cast<size_t>(kvh) * cap + c0) * d);
+    const int nkv4 = (fresh ? valid - 1 : valid) * du4;
+    uint4 kv[4], vv[4];
+    if constexpr (ROPE) {
+        // hetero/cpu_model.py:156-157 (bias) and :195-204 (RoPE), the same
+        // fp32 operations as rope_kv_kernel
+        const int half = d >> 1;
+        const size_t prow = static_cast<size_t>(pos < 0 ? 0 : (pos >= cap ? cap - 1 : pos));
+        float qa[2][2], qb[2][2], cs[2][2];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int e = r * 256 + tid;
+            if (e < G * half) {
+                const int g = e / half, i = e - g * half;
+                const int e1 = (kvh * G + g) * d + i;
+                qa[r][0] = q[e1]; qa[r][1] = q[e1 + half];
+                qb[r][0] = bias[e1]; qb[r][1] = bias[e1 + half];
+                cs[r][0] = cos_t[prow * half + i]; cs[r][1] = sin_t[prow * half + i];
+            }
+        }
+        float nk[2] = {0.f, 0.f}, nkb[2] = {0.f, 0.f}, nkc[2] = {0.f, 0.f}, nv = 0.f, nvb = 0.f;
+        if (fresh) {
+            if (tid < half) {
+                const int e1 = kvh * d + tid;
+                nk[0] = kraw[e1]; nk[1] = kraw[e1 + half];
+                nkb[0] = bias[nh * d + e1]; nkb[1] = bias[nh * d + e1 + half];
+                nkc[0] = cos_t[prow * half + tid]; nkc[1] = sin_t[prow * half + tid];
+            } else if (tid < half + d) {
+                const int e = kvh * d + (tid - half);
+                nv = vraw[e];
+                nvb = bias[(nh + nkv) * d + e];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int e = r * 256 + tid;
+            if (e < nkv4) {
+                kv[r] = k4p[e];
+                vv[r] = v4p[e];
+            }
+        }
+        float* qf = reinterpret_cast<float*>(&q_s[0][0]);
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int e = r * 256 + tid;
+            if (e < G * half) {
+                const int g = e / half, i = e - g * half;
+                const float x1 = __fadd_rn(qa[r][0], qb[r][0]), x2 = __fadd_rn(qa[r][1], qb[r][1]);
+                const float c = cs[r][0], sn = cs[r][1];
+                qf[g * kMaxD + i] = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn));
+                qf[g * kMaxD + i + half] = __fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, c));
+            }
+        }
+        if (fresh) {
+            const int row = static_cast<int>(pos - c0);
+            uint16_t* kl = reinterpret_cast<uint16_t*>(&k_s[row][0]);
+            uint16_t* vl = reinterpret_cast<uint16_t*>(&v_s[row][0]);
+            uint16_t* kg = kc + (static_cast<size_t>(kvh) * cap + pos) * d;
+            uint16_t* vg = vc + (static_cast<size_t>(kvh) * cap + pos) * d;
+            if (tid < half) {
+                const float x1 = __fadd_rn(nk[0], nkb[0]), x2 = __fadd_rn(nk[1], nkb[1]);
+                const float c = nkc[0], sn = nkc[1];
+                const uint16_t h1 = f2h_rne(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn)));
+                const uint16_t h2 = f2h_rne(__fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, c)));
+                kl[tid] = h1; kl[tid + half] = h2;
+                kg[tid] = h1; kg[tid + half] = h2;
+            } else if (tid < half + d) {
+                const uint16_t hv = f2h_rne(__fadd_rn(nv, nvb));
+                vl[tid - half] = hv;
+                vg[tid - half] = hv;
+            }
+        }
+    } else {
+        const float4* q4p = reinterpret_cast<const float4*>(q + static_cast<size_t>(kvh * G) * d);
+        const int nq4 = G * d / 4;
+        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tid < nq4) qv = q4p[tid];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int e = r * 256 + tid;
+            if (e < nkv4) {
+                kv[r] = k4p[e];
+                vv[r] = v4p[e];
+            }
+        }
+        if (tid < nq4) q_s[tid / (d / 4)][tid % (d / 4)] = qv;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int e = r * 256 + tid;
+        if (e < nkv4) {
+            k_s[e / du4][e % du4] = kv[r];
+            v_s[e / du4][e % du4] = vv[r];
+        }
     }
     __syncthreads();
-    // scores: thread (g-set, s): heads g = wave, wave + 4
+    // scores: lane = position, heads wave and wave + 4
     {
         const int s = lane;
         for (int g = wave; g < G; g += 4) {
             float acc = 0.0f;
             if (s < valid) {
-#pragma unroll 8
-                for (int i = 0; i < dp; i++) {
-                    const uint32_t kk = k_s[s][i];
-                    acc = __builtin_fmaf(q_s[g][2 * i], h2f_bits(static_cast<uint16_t>(kk)), acc);
-                    acc = __builtin_fmaf(q_s[g][2 * i + 1], h2f_bits(static_cast<uint16_t>(kk >> 16)), acc);
+#pragma unroll 4
+                for (int c = 0; c < du4; c++) {
+                    const uint4 kk = k_s[s][c];
+                    const float4 qa = q_s[g][2 * c], qb = q_s[g][2 * c + 1];
+                    acc = __builtin_fmaf(qa.x, h2f_bits(static_cast<uint16_t>(kk.x)), acc);
+                    acc = __builtin_fmaf(qa.y, h2f_bits(static_cast<uint16_t>(kk.x >> 16)), acc);
+                    acc = __builtin_fmaf(qa.z, h2f_bits(static_cast<uint16_t>(kk.y)), acc);
+                    acc = __builtin_fmaf(qa.w, h2f_bits(static_cast<uint16_t>(kk.y >> 16)), acc);
+                    acc = __builtin_fmaf(qb.x, h2f_bits(static_cast<uint16_t>(kk.z)), acc);
+                    acc = __builtin_fmaf(qb.y, h2f_bits(static_cast<uint16_t>(kk.z >> 16)), acc);
+                    acc = __builtin_fmaf(qb.z, h2f_bits(static_cast<uint16_t>(kk.w)), acc);
+                    acc = __builtin_fmaf(qb.w, h2f_bits(static_cast<uint16_t>(kk.w >> 16)), acc);
                 }
             }
             const float sc = s < valid ? __fmul_rn(acc, scale) : -__builtin_inff();
@@ -212,38 +323,72 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         }
     }
     __syncthreads();
-    // unnormalised outputs: thread (g-set, dim pair)
+    // unnormalised outputs: thread (head, fp16 pair of the row)
+    const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v_s[0][0]);
+    constexpr int kRowW = kRowU4 * 4;
+    const int dp = d >> 1;
     for (int e = tid; e < G * dp; e += blockDim.x) {
         const int g = e / dp, i = e - g * dp;
         float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 8
         for (int s = 0; s < valid; s++) {
-            const uint32_t vv = v_s[s][i];
+            const uint32_t w2 = vw[s * kRowW + i];
             const float p = p_s[g][s];
-            a0 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(vv)), a0);
-            a1 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(vv >> 16)), a1);
+            a0 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(w2)), a0);
+            a1 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(w2 >> 16)), a1);
         }
         float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2) + 2;
-        dst[2 * i] = a0;
-        dst[2 * i + 1] = a1;
+        reinterpret_cast<float2*>(dst)[i] = make_float2(a0, a1);
     }
 }
 
-__global__ __launch_bounds__(128) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
+// one workgroup per query head: M = max_c m_c, w_c = e^(m_c - M),
+// o = sum_c w_c o_c / sum_c w_c l_c
+__global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            int n_chunks, int d) {
-    const int h = blockIdx.x;
-    const float* base = part + static_cast<size_t>(h) * n_chunks * (d + 2);
+    __shared__ float w_s[kMaxChunks];
+    __shared__ float red[8];
+    const int h = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
+    const int stride = d + 2;
+    const float* base = part + static_cast<size_t>(h) * n_chunks * stride;
+    float mloc = -__builtin_inff();
+    for (int c = tid; c < n_chunks; c += nt) {
+        const float m = base[static_cast<size_t>(c) * stride];
+        w_s[c] = m;
+        mloc = fmaxf(mloc, m);
+    }
+    mloc = wave_maxf(mloc);
+    if ((tid & 63) == 0) red[tid >> 6] = mloc;
+    __syncthreads();
     float M = -__builtin_inff();
-    for (int c = 0; c < n_chunks; c++) M = fmaxf(M, base[static_cast<size_t>(c) * (d + 2)]);
-    for (int i = threadIdx.x; i < d; i += blockDim.x) {
-        float L = 0.0f, O = 0.0f;
-        for (int c = 0; c < n_chunks; c++) {
-            const float* pc = base + static_cast<size_t>(c) * (d + 2);
-            const float m = pc[0];
-            if (m == -__builtin_inff()) continue;
-            const float wgt = expf(__fsub_rn(m, M));
-            L = __builtin_fmaf(pc[1], wgt, L);
-            O = __builtin_fmaf(pc[2 + i], wgt, O);
-        }
+    for (int i = 0; i < (nt >> 6); i++) M = fmaxf(M, red[i]);
+    __syncthreads();
+    float lloc = 0.0f;
+    for (int c = tid; c < n_chunks; c += nt) {
+        const float m = w_s[c];
+        const float wgt = m == -__builtin_inff() ? 0.0f : expf(__fsub_rn(m, M));
+        w_s[c] = wgt;
+        lloc = __builtin_fmaf(base[static_cast<size_t>(c) * stride + 1], wgt, lloc);
+    }
+    lloc = wave_sum(lloc);
+    if ((tid & 63) == 0) red[tid >> 6] = lloc;
+    __syncthreads();
+    float L = 0.0f;
+    for (int i = 0; i < (nt >> 6); i++) L = __fadd_rn(L, red[i]);
+    // threads (part, dim): part k of nparts takes chunks k, k + nparts, ...;
+    // the parts are then added in order (d divides the 256 threads)
+    const int i = tid % d, part_k = tid / d;
+    const int nparts = nt / d;
+    float O = 0.0f;
+#pragma unroll 16
+    for (int c = part_k; c < n_chunks; c += nparts)
+        O = __builtin_fmaf(base[static_cast<size_t>(c) * stride + 2 + i], w_s[c], O);
+    __syncthreads();
+    float* o_s = w_s;                                        // the weights are no longer read
+    o_s[part_k * d + i] = O;
+    __syncthreads();
+    if (part_k == 0) {
+        for (int k = 1; k < nparts; k++) O = __fadd_rn(O, o_s[k * d + i]);
         out[static_cast<size_t>(h) * d + i] = __fdiv_rn(O, L);
     }
 }
@@ -358,12 +503,38 @@ int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_
         return fail(Q4_EARG, "q4_attention_dev: unsupported sizes (heads %d, kv heads %d, head_dim %d, cap %d)",
                     n_heads, n_kv, head_dim, cap);
     const int n_chunks = (cap + kChunk - 1) / kChunk;
+    if (n_chunks > kMaxChunks || head_dim % 8 || 256 % head_dim || (reinterpret_cast<uintptr_t>(q) & 15) ||
+        (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
+        (reinterpret_cast<uintptr_t>(scratch) & 7))
+        return fail(Q4_EARG, "q4_attention_dev: cap %d over %d, head_dim %d not a multiple of 8 dividing 256, "
+                             "or a pointer not 16-byte aligned", cap, kMaxChunks * kChunk, head_dim);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(attn_partial_kernel, dim3(n_chunks, n_kv), dim3(256), 0, st, q, k_cache, v_cache, pos,
-                       scratch, n_heads, n_kv, head_dim, cap, scale);
+    hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(n_chunks, n_kv), dim3(256), 0, st, q,
+                       const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache), pos, scratch, n_heads, n_kv,
+                       head_dim, cap, scale, nullptr, nullptr, nullptr, nullptr, nullptr);
     if (int rc = check_launch("q4_attention_dev (partial)")) return rc;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(128), 0, st, scratch, out, n_chunks, head_dim);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(256), 0, st, scratch, out, n_chunks, head_dim);
     return check_launch("q4_attention_dev (combine)");
+}
+
+int q4_attention_rope_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
+                          const float* sin_t, const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache, float* out,
+                          float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream) {
+    if (!q || !k || !v || !bias || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !out || !scratch)
+        return fail(Q4_EARG, "q4_attention_rope_dev: null pointer");
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kMaxG || head_dim <= 0 || head_dim % 8 ||
+        256 % head_dim || head_dim > kMaxD || cap <= 0 || (cap + kChunk - 1) / kChunk > kMaxChunks ||
+        (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
+        (reinterpret_cast<uintptr_t>(scratch) & 7))
+        return fail(Q4_EARG, "q4_attention_rope_dev: unsupported sizes (heads %d, kv heads %d, head_dim %d, cap %d) "
+                             "or a pointer not aligned", n_heads, n_kv, head_dim, cap);
+    const int n_chunks = (cap + kChunk - 1) / kChunk;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(attn_partial_kernel<true>, dim3(n_chunks, n_kv), dim3(256), 0, st, q, k_cache, v_cache, pos,
+                       scratch, n_heads, n_kv, head_dim, cap, scale, k, v, bias, cos_t, sin_t);
+    if (int rc = check_launch("q4_attention_rope_dev (partial)")) return rc;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(256), 0, st, scratch, out, n_chunks, head_dim);
+    return check_launch("q4_attention_rope_dev (combine)");
 }
 
 int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0, int hist_len,

@@ -9,8 +9,8 @@ operation a kernel of libq4gemv.so:
     bit for bit given the same input;
   * the rest from include/q4decode.h: the embedding row (q4_embed_dev), the
     residual adds fused with the next RMSNorm (q4_add_rmsnorm_dev), bias +
-    RoPE + the fp16 KV-cache write (q4_rope_kv_dev), GQA attention split over
-    the context (q4_attention_dev) and the greedy argmax with the step's
+    RoPE + the fp16 KV-cache write fused with GQA attention split over the
+    context (q4_attention_rope_dev) and the greedy argmax with the step's
     bookkeeping (q4_argmax_dev).
 The token id and the position live in device tensors and attention covers
 positions [0, pos] of a fixed-size cache, so one decode step is
@@ -99,7 +99,6 @@ class GpuStage:
         self.positions = torch.arange(self.cap, device=dev)
         self.hist = torch.zeros(max_new, dtype=torch.int64, device=dev)   # token of each step
         self.hn = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
-        self.q_rot = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
         n_scr = self.lib.q4_attention_scratch_floats(self.nh, self.hd, self.cap)
         self.attn_scratch = torch.zeros(n_scr, dtype=torch.float32, device=dev)
         self.scale = float(np.float32(self.hd ** -0.5))            # cpu_model.py:261
@@ -120,11 +119,10 @@ class GpuStage:
            "rmsnorm")
         for i, L in enumerate(self.layers):                             # cpu_model.py:304-306
             q4.gemv_multi_dev(L["qkv"], self.hn, outs=[self.q, self.k, self.v], lib=lib)
-            ck(lib.q4_rope_kv_dev(P(self.q), P(self.k), P(self.v), P(L["qkv_bias"]), P(self.cos), P(self.sin),
-                                  P(self.pos), P(L["k_cache"]), P(L["v_cache"]), P(self.q_rot),
-                                  self.nh, self.nkv, self.hd, self.cap, st), "rope_kv")
-            ck(lib.q4_attention_dev(P(self.q_rot), P(L["k_cache"]), P(L["v_cache"]), P(self.pos), P(self.attn),
-                                    P(self.attn_scratch), self.nh, self.nkv, self.hd, self.cap, self.scale, st),
+            # bias + RoPE + the KV-cache write fused into the attention launches
+            ck(lib.q4_attention_rope_dev(P(self.q), P(self.k), P(self.v), P(L["qkv_bias"]), P(self.cos),
+                                         P(self.sin), P(self.pos), P(L["k_cache"]), P(L["v_cache"]), P(self.attn),
+                                         P(self.attn_scratch), self.nh, self.nkv, self.hd, self.cap, self.scale, st),
                "attention")
             q4.gemv_dev(*L["o"], self.attn, out=self.o, lib=lib)
             # x = x + attn; hn = rms_norm(x, post_w)

@@ -24,7 +24,7 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_dequant_dev", "q4_dequant_bf16_dev",
            # decode-step kernels (include/q4decode.h)
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
-           "q4_attention_dev", "q4_argmax_dev")
+           "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
@@ -71,6 +71,8 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_attention_scratch_floats.restype = _L
         lib.q4_attention_dev.argtypes = [_VP] * 6 + [_I] * 4 + [_F, _VP]
         lib.q4_attention_dev.restype = _I
+        lib.q4_attention_rope_dev.argtypes = [_VP] * 11 + [_I] * 4 + [_F, _VP]
+        lib.q4_attention_rope_dev.restype = _I
         lib.q4_argmax_dev.argtypes = [_VP, _I, _VP, _VP, _VP, ctypes.c_int64, _I, _VP]
         lib.q4_argmax_dev.restype = _I
     return lib

@@ -64,6 +64,16 @@ int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_
                      float* out, float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale,
                      void* stream);
 
+/* q4_rope_kv_dev followed by q4_attention_dev, in the same two launches as
+ * q4_attention_dev: q, k, v are the raw projection outputs (fp32 [n_heads*d],
+ * [n_kv*d], [n_kv*d]) and bias/cos_t/sin_t are as for q4_rope_kv_dev; the
+ * workgroups apply bias and RoPE to the query heads they need, and the one
+ * whose chunk holds *pos writes the new key and value rows to the cache and
+ * uses them directly.  Results equal the two calls in sequence. */
+int q4_attention_rope_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
+                          const float* sin_t, const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache, float* out,
+                          float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream);
+
 /* Greedy token (hetero/backends.py:106-109, NumpyBackend.sample: argmax,
  * the first index of the maximum) and the step's bookkeeping: *tok = argmax,
  * hist[*pos - s0] = *tok when that index is in [0, hist_len), *pos += 1. */

@@ -113,6 +113,8 @@ def test_decode_kernel_argument_errors(lib):
     assert lib.q4_rope_kv_dev(*([p] * 10), 28, 5, 128, 64, None) == q4.Q4_EARG      # heads % kv heads
     assert lib.q4_attention_dev(*([p] * 6), 72, 4, 128, 64, 0.1, None) == q4.Q4_EARG  # 18 heads per kv head
     assert lib.q4_attention_dev(*([p] * 6), 28, 4, 256, 64, 0.1, None) == q4.Q4_EARG  # head_dim > 128
+    assert lib.q4_attention_rope_dev(*([p] * 11), 72, 4, 128, 64, 0.1, None) == q4.Q4_EARG
+    assert lib.q4_attention_rope_dev(*([p] * 10), None, 28, 4, 128, 64, 0.1, None) == q4.Q4_EARG
     assert lib.q4_argmax_dev(None, 10, p, p, p, 0, 1, None) == q4.Q4_EARG
     assert lib.q4_attention_scratch_floats(28, 128, 2048) == 28 * 32 * 130
     assert lib.q4_attention_scratch_floats(28, 128, 2049) == 28 * 33 * 130

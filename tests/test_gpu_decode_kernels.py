@@ -10,6 +10,8 @@
 * attention: within 1e-5 (norm-wise) of an fp64 masked GQA softmax over the
   fp16 cache (hetero/cpu_model.py:233-252), at positions on both sides of
   the 64-position chunk boundaries;
+* fused RoPE + attention: bit-exact (output and both caches) with
+  q4_rope_kv_dev followed by q4_attention_dev over a run of decode positions;
 * argmax: the first index of the maximum, with planted ties, and the step
   bookkeeping (token, history slot, position + 1).
 """
@@ -159,6 +161,44 @@ def test_attention(torch, lib, nh, nkv):
         assert rc == 0, q4.last_error(lib)
         ref = attention_ref(q_np, kc_np, vc_np, p, nh, nkv, float(scale))
         assert oracle.normwise_rel(out.cpu().numpy(), ref) < ATTN_TOL, p
+
+
+@pytest.mark.parametrize("nh,nkv", [(28, 4), (8, 8), (16, 2)])
+def test_attention_rope_matches_separate_calls(torch, lib, nh, nkv):
+    rng = np.random.default_rng(8)
+    d, cap = 128, 150
+    half = d // 2
+    scale = float(np.float32(d ** -0.5))
+    inv = 1e6 ** (-np.arange(0, half, dtype=np.float32) * 2.0 / d)
+    ang = np.arange(cap, dtype=np.float32)[:, None] * inv[None, :]
+    dev = torch.device("cuda")
+    tc = torch.from_numpy(np.cos(ang)).to(dev)
+    ts = torch.from_numpy(np.sin(ang)).to(dev)
+    tb = torch.from_numpy(rng.normal(0, 0.1, (nh + 2 * nkv) * d).astype(np.float32)).to(dev)
+    # both caches start from the same history
+    kc_a = torch.from_numpy(rng.normal(0, 1, (nkv, cap, d)).astype(np.float16)).to(dev)
+    vc_a = torch.from_numpy(rng.normal(0, 1, (nkv, cap, d)).astype(np.float16)).to(dev)
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    q_rot = torch.empty(nh * d, device=dev)
+    out_a, out_b = torch.empty(nh * d, device=dev), torch.empty(nh * d, device=dev)
+    scratch = torch.empty(lib.q4_attention_scratch_floats(nh, d, cap), device=dev)
+    for p in (0, 1, 2, 62, 63, 64, 65, 100, 127, 128, cap - 1, cap, cap + 5):
+        q, k, v = (torch.from_numpy(rng.normal(0, 1, n * d).astype(np.float32)).to(dev) for n in (nh, nkv, nkv))
+        pos = torch.tensor([p], dtype=torch.int64, device=dev)
+        rc = lib.q4_rope_kv_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(), tb.data_ptr(), tc.data_ptr(), ts.data_ptr(),
+                                pos.data_ptr(), kc_a.data_ptr(), vc_a.data_ptr(), q_rot.data_ptr(), nh, nkv, d, cap,
+                                sp(torch))
+        assert rc == 0, q4.last_error(lib)
+        rc = lib.q4_attention_dev(q_rot.data_ptr(), kc_a.data_ptr(), vc_a.data_ptr(), pos.data_ptr(),
+                                  out_a.data_ptr(), scratch.data_ptr(), nh, nkv, d, cap, scale, sp(torch))
+        assert rc == 0, q4.last_error(lib)
+        rc = lib.q4_attention_rope_dev(q.data_ptr(), k.data_ptr(), v.data_ptr(), tb.data_ptr(), tc.data_ptr(),
+                                       ts.data_ptr(), pos.data_ptr(), kc_b.data_ptr(), vc_b.data_ptr(),
+                                       out_b.data_ptr(), scratch.data_ptr(), nh, nkv, d, cap, scale, sp(torch))
+        assert rc == 0, q4.last_error(lib)
+        assert torch.equal(out_a.view(torch.int32), out_b.view(torch.int32)), p
+        assert torch.equal(kc_a.view(torch.int16), kc_b.view(torch.int16)), p
+        assert torch.equal(vc_a.view(torch.int16), vc_b.view(torch.int16)), p
 
 
 def test_argmax_first_index_and_bookkeeping(torch, lib):
