@@ -48,6 +48,20 @@ __device__ __forceinline__ float dpp_max(float a) {
     return fmaxf(a, __int_as_float(o));
 }
 
+// Butterfly sum over the 64 lanes (every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
+    return v;
+}
+
+// 1 / sqrt(mean + eps) of RMSNorm from the sum of squares of n values
+// (hetero/cpu_model.py:164-166).
+__device__ __forceinline__ float rms_factor(float sum_sq, int n, float eps) {
+    const float ms = __fdiv_rn(sum_sq, static_cast<float>(n));
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = dpp_max<0xB1>(v);    // quad_perm 1,0,3,2
     v = dpp_max<0x4E>(v);    // quad_perm 2,3,0,1

@@ -12,12 +12,6 @@
 namespace q4k {
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
-    return v;
-}
-
 __device__ __forceinline__ float wave_maxf(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -56,18 +50,22 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 
 // ------------------------------------------------ residual add + RMSNorm ---
 // hetero/cpu_model.py:164-166: x * (1 / sqrt(mean(x * x) + eps)) * w, after
-// the residual add of :304-306.  One workgroup; n <= 8 * 1024.
+// the residual add of :304-306.  One workgroup; n <= 8 * 1024.  Thread t
+// owns the 8 consecutive values of word t and adds their squares in order;
+// the wave sums (wave_sum) are added in wave order.  The streaming GEMV's
+// norm prologue sums in exactly this order, so its input is y bit for bit.
 constexpr int kNormPer = 8;
 __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ delta,
                                                           const float* __restrict__ w, float eps,
                                                           float* __restrict__ y, int n) {
     __shared__ float red[16];
     const int tid = threadIdx.x, nt = blockDim.x;
+    const int i0 = tid * kNormPer;
     float v[kNormPer];
     float ss = 0.0f;
 #pragma unroll
     for (int k = 0; k < kNormPer; k++) {
-        const int i = k * nt + tid;
+        const int i = i0 + k;
         v[k] = 0.0f;
         if (i < n) {
             float a = x[i];
@@ -84,11 +82,10 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x
     __syncthreads();
     float tot = 0.0f;
     for (int i = 0; i < (nt >> 6); i++) tot = __fadd_rn(tot, red[i]);
-    const float ms = __fdiv_rn(tot, static_cast<float>(n));
-    const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+    const float r = rms_factor(tot, n, eps);
 #pragma unroll
     for (int k = 0; k < kNormPer; k++) {
-        const int i = k * nt + tid;
+        const int i = i0 + k;
         if (i < n) y[i] = __fmul_rn(__fmul_rn(v[k], r), w[i]);
     }
 }

@@ -48,6 +48,16 @@ struct MatList {
     int count;
 };
 
+// The norm prologue (NORM instances): the kernel's input is
+// rmsnorm(x + delta) * w, computed by every workgroup from x, delta (NULL:
+// x alone) and w; workgroup 0 also stores x + delta to x_out (if not NULL).
+struct NormArgs {
+    const float* delta;
+    const float* w;
+    float* x_out;
+    float eps;
+};
+
 // Row stride of the per-wave term table: a multiple of 4 floats (16-byte
 // reads) that is 4 mod 8 words, so lanes reading different rows spread over
 // the banks.
@@ -189,11 +199,16 @@ __host__ __device__ constexpr int stream_max_rounds() { return MR == 1 ? 4 : 2; 
 
 // PAIR: matrices 0 and 1 (gate, up) are computed row for row and the output
 // is out[0] = SiLU(gate) * up.
+// NORM: the input is the RMSNorm of a residual sum (NormArgs), with the sum
+// of squares taken in the order of add_rmsnorm_kernel (one word per thread,
+// wave sums in wave order), so the input is bit for bit the one that
+// kernel writes.  MR = 1 and RW = 1 only.
 // Host guarantees: MR * (n_in / 64) <= blockDim.x (one thread per group
 // item), chunks * 256 <= RW * blockDim.x, n_in % 64 == 0, x 16-byte aligned.
-template <int MR, int RW, bool PAIR, int RING>
+template <int MR, int RW, bool PAIR, int RING, bool NORM>
 __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const float* __restrict__ x,
-                                                          int n_in, int UB) {
+                                                          int n_in, int UB, NormArgs na) {
+    static_assert(!NORM || (MR == 1 && RW == 1), "the norm prologue takes one row, one word per thread");
     extern __shared__ uint4 lds4[];
     constexpr int lpg = 2;                                        // lanes per group
     const int wpr = n_in >> 3, G = n_in >> 6;
@@ -229,6 +244,21 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
                 wv[m][r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
                 wv[m][r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
             }
+    // NORM: the thread's word of delta and of the norm weights (a NULL
+    // delta reads through an empty range: no access)
+    float4 nd[2], nw[2];
+    if constexpr (NORM) {
+        const uint32_t nb = static_cast<uint32_t>(n_in) * 4u;
+        const __amdgpu_buffer_rsrc_t dr = buf_rsrc(na.delta ? na.delta : x, na.delta ? nb : 0u);
+        const __amdgpu_buffer_rsrc_t wr = buf_rsrc(na.w, nb);
+        if (wave * 64 < wpr) {                                    // uniform
+            const uint32_t off = tid < wpr ? static_cast<uint32_t>(8 * tid) * 4u : kOutOfRange;
+            nd[0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(dr, off, 0, 0));
+            nd[1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(dr, off + 16, 0, 0));
+            nw[0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+            nw[1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wr, off + 16, 0, 0));
+        }
+    }
 
     // ---- the wave's item stream.  Workgroup b owns units b, b + grid, ...;
     //      wave w starts with its k = w-th one and claims further k from an
@@ -261,6 +291,43 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     //      the main loop) and one thread per group chains them after the
     //      barrier.
     float* stage = red + MR * 16 + 4;
+    if constexpr (NORM) {
+        // hetero/cpu_model.py:304-306 (x + delta) and :164-166 (RMSNorm); the
+        // sum of squares goes through the staging space (free until the
+        // main loop), the amax slots stay untouched
+        float ss = 0.0f;
+        float v[8] = {wv[0][0][0].x, wv[0][0][0].y, wv[0][0][0].z, wv[0][0][0].w,
+                      wv[0][0][1].x, wv[0][0][1].y, wv[0][0][1].z, wv[0][0][1].w};
+        if (wave * 64 < wpr) {                                    // uniform
+            if (na.delta) {                                       // uniform
+                const float d8[8] = {nd[0].x, nd[0].y, nd[0].z, nd[0].w, nd[1].x, nd[1].y, nd[1].z, nd[1].w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = __fadd_rn(v[i], d8[i]);
+                if (na.x_out && blockIdx.x == 0) {                // uniform
+                    const __amdgpu_buffer_rsrc_t xo = buf_rsrc(na.x_out, static_cast<uint32_t>(n_in) * 4u);
+                    const uint32_t off = tid < wpr ? static_cast<uint32_t>(8 * tid) * 4u : kOutOfRange;
+                    using u32x4 = unsigned int __attribute__((__vector_size__(16)));
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, make_float4(v[0], v[1], v[2], v[3])), xo, off, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, make_float4(v[4], v[5], v[6], v[7])), xo, off + 16, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) stage[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < nwaves; i++) tot = __fadd_rn(tot, stage[i]);
+        const float r = rms_factor(tot, n_in, na.eps);
+        const float w8[8] = {nw[0].x, nw[0].y, nw[0].z, nw[0].w, nw[1].x, nw[1].y, nw[1].z, nw[1].w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = __fmul_rn(__fmul_rn(v[i], r), w8[i]);
+        wv[0][0][0] = make_float4(v[0], v[1], v[2], v[3]);
+        wv[0][0][1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
 #pragma unroll
     for (int m = 0; m < MR; m++) {
         float amax = 0.0f;
@@ -490,18 +557,18 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
 
 // Workgroups of the kernel resident per CU (the ring-4 instance: the most
 // registers of the rings in use).
-template <int MR, int RW, bool PAIR>
+template <int MR, int RW, bool PAIR, bool NORM>
 int stream_blocks_per_cu(int nwaves, size_t lds) {
     int per_cu = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, gemv_stream_kernel<MR, RW, PAIR, 4>, 64 * nwaves, lds);
+        &per_cu, gemv_stream_kernel<MR, RW, PAIR, 4, NORM>, 64 * nwaves, lds);
     return (e != hipSuccess || per_cu < 1) ? 1 : per_cu;
 }
 
-template <int MR, int RW, bool PAIR, int RING>
-int launch_stream_k(const MatList& ml, const float* x, int n_in, int UB, int nwaves, size_t lds, int grid,
-                    hipStream_t st) {
-    auto kern = gemv_stream_kernel<MR, RW, PAIR, RING>;
+template <int MR, int RW, bool PAIR, int RING, bool NORM>
+int launch_stream_k(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
+                    size_t lds, int grid, hipStream_t st) {
+    auto kern = gemv_stream_kernel<MR, RW, PAIR, RING, NORM>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -510,7 +577,7 @@ int launch_stream_k(const MatList& ml, const float* x, int n_in, int UB, int nwa
         if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
         attr_set = true;
     }
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB, na);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "stream gemv launch: %s", hipGetErrorString(e));
     return 1;

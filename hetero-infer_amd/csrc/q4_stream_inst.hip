@@ -1,6 +1,7 @@
 // Instances of the streaming GEMV kernel, one object per (activation rows,
-// gate/up pair, ring size): the build compiles this file once per
-// -DQ4_MR=<1|2> -DQ4_PAIR=<0|1> -DQ4_RING=<1|2|4|5>, in parallel.
+// gate/up pair, ring size), one-row objects with the norm prologue too: the
+// build compiles this file once per -DQ4_MR=<1|2> -DQ4_PAIR=<0|1>
+// -DQ4_RING=<1|2|4|5>, in parallel.
 #include "q4_stream.h"
 
 #if !defined(Q4_MR) || !defined(Q4_PAIR) || !defined(Q4_RING)
@@ -10,21 +11,24 @@
 namespace q4k {
 
 #if Q4_RING == 4
-#define Q4_STREAM_OCC(RW) \
-    template int stream_blocks_per_cu<Q4_MR, RW, static_cast<bool>(Q4_PAIR)>(int, size_t);
+#define Q4_STREAM_OCC(RW, NORM) \
+    template int stream_blocks_per_cu<Q4_MR, RW, static_cast<bool>(Q4_PAIR), NORM>(int, size_t);
 #else
-#define Q4_STREAM_OCC(RW)
+#define Q4_STREAM_OCC(RW, NORM)
 #endif
-#define Q4_STREAM_INST(RW)                                                                      \
-    template int launch_stream_k<Q4_MR, RW, static_cast<bool>(Q4_PAIR), Q4_RING>(              \
-        const MatList&, const float*, int, int, int, size_t, int, hipStream_t);               \
-    Q4_STREAM_OCC(RW)
+#define Q4_STREAM_INST(RW, NORM)                                                                      \
+    template int launch_stream_k<Q4_MR, RW, static_cast<bool>(Q4_PAIR), Q4_RING, NORM>(              \
+        const MatList&, const float*, const NormArgs&, int, int, int, size_t, int, hipStream_t);     \
+    Q4_STREAM_OCC(RW, NORM)
 
-Q4_STREAM_INST(1)
-Q4_STREAM_INST(2)
+Q4_STREAM_INST(1, false)
+Q4_STREAM_INST(2, false)
 #if Q4_MR == 1 && Q4_PAIR == 0
-Q4_STREAM_INST(3)
-Q4_STREAM_INST(4)
+Q4_STREAM_INST(3, false)
+Q4_STREAM_INST(4, false)
+#endif
+#if Q4_MR == 1
+Q4_STREAM_INST(1, true)   // the norm prologue: one row, one word per thread
 #endif
 
 }  // namespace q4k

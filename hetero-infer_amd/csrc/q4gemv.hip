@@ -39,6 +39,7 @@
 #include <vector>
 
 #include "q4_stream.h"
+#include "q4decode.h"
 
 namespace q4k {
 
@@ -69,18 +70,23 @@ int num_cus() {
 // The streaming kernel's instances are compiled in q4_stream_inst.hip
 // (a build with -DQ4_SINGLE_TU instantiates them here instead).
 #ifndef Q4_SINGLE_TU
-#define Q4_STREAM_EXTERN(MR, RW, PAIR, RING)                                                   \
-    extern template int launch_stream_k<MR, RW, PAIR, RING>(const MatList&, const float*, int, int, \
-                                                            int, size_t, int, hipStream_t);
-#define Q4_STREAM_RINGS(MR, RW, PAIR)                                                               \
-    Q4_STREAM_EXTERN(MR, RW, PAIR, 1) Q4_STREAM_EXTERN(MR, RW, PAIR, 2) Q4_STREAM_EXTERN(MR, RW, PAIR, 4) \
-    extern template int stream_blocks_per_cu<MR, RW, PAIR>(int, size_t);
-Q4_STREAM_RINGS(1, 1, false) Q4_STREAM_RINGS(1, 2, false) Q4_STREAM_RINGS(1, 3, false) Q4_STREAM_RINGS(1, 4, false)
-Q4_STREAM_EXTERN(1, 1, false, 5) Q4_STREAM_EXTERN(1, 2, false, 5) Q4_STREAM_EXTERN(1, 3, false, 5)
-Q4_STREAM_EXTERN(1, 4, false, 5)
-Q4_STREAM_RINGS(1, 1, true) Q4_STREAM_RINGS(1, 2, true)
-Q4_STREAM_RINGS(2, 1, false) Q4_STREAM_RINGS(2, 2, false)
-Q4_STREAM_RINGS(2, 1, true) Q4_STREAM_RINGS(2, 2, true)
+#define Q4_STREAM_EXTERN(MR, RW, PAIR, RING, NORM)                                              \
+    extern template int launch_stream_k<MR, RW, PAIR, RING, NORM>(const MatList&, const float*,   \
+                                                                  const NormArgs&, int, int, int, \
+                                                                  size_t, int, hipStream_t);
+#define Q4_STREAM_RINGS(MR, RW, PAIR, NORM)                                                         \
+    Q4_STREAM_EXTERN(MR, RW, PAIR, 1, NORM) Q4_STREAM_EXTERN(MR, RW, PAIR, 2, NORM)                 \
+    Q4_STREAM_EXTERN(MR, RW, PAIR, 4, NORM)                                                         \
+    extern template int stream_blocks_per_cu<MR, RW, PAIR, NORM>(int, size_t);
+Q4_STREAM_RINGS(1, 1, false, false) Q4_STREAM_RINGS(1, 2, false, false)
+Q4_STREAM_RINGS(1, 3, false, false) Q4_STREAM_RINGS(1, 4, false, false)
+Q4_STREAM_EXTERN(1, 1, false, 5, false) Q4_STREAM_EXTERN(1, 2, false, 5, false)
+Q4_STREAM_EXTERN(1, 3, false, 5, false) Q4_STREAM_EXTERN(1, 4, false, 5, false)
+Q4_STREAM_RINGS(1, 1, true, false) Q4_STREAM_RINGS(1, 2, true, false)
+Q4_STREAM_RINGS(2, 1, false, false) Q4_STREAM_RINGS(2, 2, false, false)
+Q4_STREAM_RINGS(2, 1, true, false) Q4_STREAM_RINGS(2, 2, true, false)
+Q4_STREAM_RINGS(1, 1, false, true) Q4_STREAM_EXTERN(1, 1, false, 5, true)
+Q4_STREAM_RINGS(1, 1, true, true)
 #undef Q4_STREAM_RINGS
 #undef Q4_STREAM_EXTERN
 #endif
@@ -609,25 +615,29 @@ hipError_t launch_main(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 }
 
 
-template <int MR, int RW, bool PAIR>
-int launch_stream_rw(const MatList& ml, const float* x, int n_in, int UB, int nwaves, size_t lds, int n_units,
-                     int items, hipStream_t st) {
-    const int per_cu = stream_blocks_per_cu<MR, RW, PAIR>(nwaves, lds);
+template <int MR, int RW, bool PAIR, bool NORM>
+int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
+                     size_t lds, int n_units, int items, hipStream_t st) {
+    const int per_cu = stream_blocks_per_cu<MR, RW, PAIR, NORM>(nwaves, lds);
     const int want = (n_units + nwaves - 1) / nwaves;
     const int cap = num_cus() * per_cu;                 // every workgroup resident at once
     const int grid = want < cap ? want : cap;
     // ring: a divisor of the unit's items (units change only between rings)
-    if (items % 4 == 0) return launch_stream_k<MR, RW, PAIR, 4>(ml, x, n_in, UB, nwaves, lds, grid, st);
+    if (items % 4 == 0) return launch_stream_k<MR, RW, PAIR, 4, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
     if constexpr (MR == 1 && !PAIR)
-        if (items % 5 == 0) return launch_stream_k<MR, RW, PAIR, 5>(ml, x, n_in, UB, nwaves, lds, grid, st);
-    if (items % 2 == 0) return launch_stream_k<MR, RW, PAIR, 2>(ml, x, n_in, UB, nwaves, lds, grid, st);
-    return launch_stream_k<MR, RW, PAIR, 1>(ml, x, n_in, UB, nwaves, lds, grid, st);
+        if (items % 5 == 0)
+            return launch_stream_k<MR, RW, PAIR, 5, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+    if (items % 2 == 0) return launch_stream_k<MR, RW, PAIR, 2, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+    return launch_stream_k<MR, RW, PAIR, 1, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
 }
 
-template <int MR, bool PAIR = false>
-int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st) {
+// NORM: the norm prologue (one row; one word of x per thread, so at least
+// n_in / 512 waves -- n_in <= 8192).  Returns 0 if the shape does not fit.
+template <int MR, bool PAIR = false, bool NORM = false>
+int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, const NormArgs& na = NormArgs{}) {
+    static_assert(!NORM || MR == 1, "the norm prologue takes one row");
     constexpr int kWavesPerCu = 16;                     // 4 waves per SIMD at <= 128 VGPRs
-    constexpr int rmax = stream_max_rounds<MR>();
+    constexpr int rmax = NORM ? 1 : stream_max_rounds<MR>();
     const int G = n_in / 64;
     const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
     const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
@@ -655,14 +665,21 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st) {
     if (lds > kStreamLdsMax) return 0;
     const int rw = (C * kChunkWords + 64 * nwaves - 1) / (64 * nwaves);
     const int items = (PAIR ? 2 : 1) * UB * C;
+    if constexpr (NORM)
+        return rw == 1 ? launch_stream_rw<MR, 1, PAIR, true>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st)
+                       : 0;
     switch (rw) {
-        case 1: return launch_stream_rw<MR, 1, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
-        case 2: return launch_stream_rw<MR, 2, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
+        case 1: return launch_stream_rw<MR, 1, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+        case 2: return launch_stream_rw<MR, 2, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
         // (3 and 4 words per thread: the single-matrix launches of one row)
-        case 3: if constexpr (rmax >= 3 && !PAIR) return launch_stream_rw<MR, 3, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
-                return 0;
-        case 4: if constexpr (rmax >= 4 && !PAIR) return launch_stream_rw<MR, 4, PAIR>(ml, x, n_in, UB, nwaves, lds, n_units, items, st);
-                return 0;
+        case 3:
+            if constexpr (rmax >= 3 && !PAIR)
+                return launch_stream_rw<MR, 3, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+            return 0;
+        case 4:
+            if constexpr (rmax >= 4 && !PAIR)
+                return launch_stream_rw<MR, 4, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+            return 0;
         default: return 0;
     }
 }
@@ -902,6 +919,22 @@ int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const f
     return 0;
 }
 
+// The arguments of the norm-prologue entry points: gs 64, n_in in
+// [64, 8192], the vectors 16-byte aligned, x_out overlapping neither input.
+int check_norm_args(const char* who, const float* x, const float* delta, const float* norm_w, const float* x_out,
+                    int n_in, int gs) {
+    if (!x || !norm_w) return fail(Q4_EARG, "%s: null x or norm weights", who);
+    if (gs != 64) return fail(Q4_EARG, "%s takes gs = 64 (got %d)", who, gs);
+    if (n_in <= 0 || n_in > 8192) return fail(Q4_EARG, "%s: n_in = %d outside [64, 8192]", who, n_in);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(delta) |
+                         reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(x_out);
+    if (al & 15) return fail(Q4_EARG, "%s: x, delta, norm_w and x_out must be 16-byte aligned", who);
+    auto overlap = [n_in](const float* a, const float* b) { return a && b && a < b + n_in && b < a + n_in; };
+    if (overlap(x_out, x) || overlap(x_out, delta))
+        return fail(Q4_EARG, "%s: x_out overlaps x or delta", who);
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================ C-ABI ====
@@ -1102,6 +1135,62 @@ int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const ui
         }
     }
     return 0;
+}
+
+int q4_norm_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const* scales,
+                           const uint16_t* const* biases, float* const* out, const int* n_out, const float* x,
+                           const float* delta, const float* norm_w, float eps, float* x_out, int n_in, int gs,
+                           void* stream) {
+    if (count < 1 || count > kMaxMats || !w || !scales || !biases || !out || !n_out)
+        return fail(Q4_EARG, "q4_norm_gemv_multi_dev: count=%d (1..%d) or null array", count, kMaxMats);
+    int rc;
+    for (int k = 0; k < count; k++) {
+        if ((rc = check_gemv_shape(n_out[k], n_in, gs))) return rc;
+        if (!w[k] || !scales[k] || !biases[k] || !out[k]) return fail(Q4_EARG, "null pointer in matrix %d", k);
+        if (reinterpret_cast<uintptr_t>(w[k]) & 15) return fail(Q4_EARG, "w[%d] must be 16-byte aligned", k);
+    }
+    if ((rc = check_norm_args("q4_norm_gemv_multi_dev", x, delta, norm_w, x_out, n_in, gs))) return rc;
+    MatList ml{};
+    ml.row_begin[0] = 0;
+    for (int k = 0; k < kMaxMats; k++) {
+        const int kk = k < count ? k : count - 1;
+        ml.w[k] = w[kk]; ml.s[k] = scales[kk]; ml.b[k] = biases[kk]; ml.out[k] = out[kk];
+        ml.n_out[k] = k < count ? n_out[k] : 0;
+        ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
+    }
+    ml.count = count;
+    if (ml.row_begin[count] == 0) return fail(Q4_EARG, "q4_norm_gemv_multi_dev: no output rows");
+    const NormArgs na{delta, norm_w, x_out, eps};
+    rc = launch_stream<1, false, true>(ml, x, n_in, static_cast<hipStream_t>(stream), na);
+    if (rc == 0) return fail(Q4_EARG, "q4_norm_gemv_multi_dev: n_in = %d does not fit the norm prologue", n_in);
+    return rc < 0 ? rc : 0;
+}
+
+int q4_norm_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,
+                             const uint32_t* up_w, const uint16_t* up_s, const uint16_t* up_b, const float* x,
+                             const float* delta, const float* norm_w, float eps, float* x_out, float* h,
+                             int n_inter, int n_in, int gs, void* stream) {
+    int rc = check_gemv_shape(n_inter, n_in, gs);
+    if (rc) return rc;
+    if (n_inter == 0) return fail(Q4_EARG, "q4_norm_gate_up_silu_dev: no output rows");
+    if (!gate_w || !gate_s || !gate_b || !up_w || !up_s || !up_b || !h)
+        return fail(Q4_EARG, "q4_norm_gate_up_silu_dev: null pointer");
+    if ((reinterpret_cast<uintptr_t>(gate_w) | reinterpret_cast<uintptr_t>(up_w)) & 15)
+        return fail(Q4_EARG, "w must be 16-byte aligned");
+    if ((rc = check_norm_args("q4_norm_gate_up_silu_dev", x, delta, norm_w, x_out, n_in, gs))) return rc;
+    MatList ml{};
+    ml.w[0] = gate_w; ml.s[0] = gate_s; ml.b[0] = gate_b; ml.out[0] = h; ml.n_out[0] = n_inter;
+    ml.w[1] = up_w;   ml.s[1] = up_s;   ml.b[1] = up_b;   ml.out[1] = h; ml.n_out[1] = n_inter;
+    for (int k = 2; k < kMaxMats; k++) {
+        ml.w[k] = up_w; ml.s[k] = up_s; ml.b[k] = up_b; ml.out[k] = h; ml.n_out[k] = 0;
+    }
+    ml.row_begin[0] = 0;
+    for (int k = 0; k < kMaxMats; k++) ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
+    ml.count = 2;
+    const NormArgs na{delta, norm_w, x_out, eps};
+    rc = launch_stream<1, true, true>(ml, x, n_in, static_cast<hipStream_t>(stream), na);
+    if (rc == 0) return fail(Q4_EARG, "q4_norm_gate_up_silu_dev: n_in = %d does not fit the norm prologue", n_in);
+    return rc < 0 ? rc : 0;
 }
 
 int q4_mlp_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,

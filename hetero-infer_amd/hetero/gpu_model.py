@@ -3,13 +3,14 @@
 The same stage as hetero/cpu_model.py (the reference's
 hetero/cpu_model.py:164-368), with every tensor resident in HBM and every
 operation a kernel of libq4gemv.so:
-  * 4-bit projections through the streaming GEMV: q/k/v in one grouped launch
-    (q4_gemv_multi_dev), o_proj, the fused gate/up/SiLU*mul launch plus down
-    (q4_mlp_dev) and lm_head -- every GEMV result is the reference q4_gemv's
-    bit for bit given the same input;
-  * the rest from include/q4decode.h: the embedding row (q4_embed_dev), the
-    residual adds fused with the next RMSNorm (q4_add_rmsnorm_dev), bias +
-    RoPE + the fp16 KV-cache write fused with GQA attention split over the
+  * 4-bit projections through the streaming GEMV: q/k/v in one grouped
+    launch, o_proj, the fused gate/up/SiLU*mul launch, down and lm_head --
+    every GEMV result is the reference q4_gemv's bit for bit given the same
+    input.  Each residual add and RMSNorm is folded into the prologue of the
+    GEMV that follows it (q4_norm_gemv_multi_dev for q/k/v and lm_head,
+    q4_norm_gate_up_silu_dev for gate/up; include/q4decode.h);
+  * the rest from include/q4decode.h: the embedding row (q4_embed_dev), bias
+    + RoPE + the fp16 KV-cache write fused with GQA attention split over the
     context (q4_attention_rope_dev) and the greedy argmax with the step's
     bookkeeping (q4_argmax_dev).
 The token id and the position live in device tensors and attention covers
@@ -86,7 +87,10 @@ class GpuStage:
         # step state and static buffers
         self.tok = torch.zeros(1, dtype=torch.int64, device=dev)
         self.pos = torch.full((1,), self.s0, dtype=torch.int64, device=dev)
-        self.x = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
+        # the residual stream, in two buffers: each fused norm + GEMV reads
+        # one and writes x + delta to the other
+        self.xbuf = (torch.zeros(self.h, dtype=torch.float32, device=dev),
+                     torch.zeros(self.h, dtype=torch.float32, device=dev))
         self.hbuf = torch.zeros((1, self.inter), dtype=torch.float32, device=dev)
         self.mlp_out = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
         self.q = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
@@ -98,7 +102,6 @@ class GpuStage:
         self.logits = torch.zeros((1, cfg["vocab_size"]), dtype=torch.float32, device=dev)
         self.positions = torch.arange(self.cap, device=dev)
         self.hist = torch.zeros(max_new, dtype=torch.int64, device=dev)   # token of each step
-        self.hn = torch.zeros((1, self.h), dtype=torch.float32, device=dev)
         n_scr = self.lib.q4_attention_scratch_floats(self.nh, self.hd, self.cap)
         self.attn_scratch = torch.zeros(n_scr, dtype=torch.float32, device=dev)
         self.scale = float(np.float32(self.hd ** -0.5))            # cpu_model.py:261
@@ -113,27 +116,31 @@ class GpuStage:
         P = lambda t: t.data_ptr()
         h, gs = self.h, self.gs
         ew, es, eb = self.embed
-        # embedding row (cpu_model.py:334-338), then the first RMSNorm
-        ck(lib.q4_embed_dev(P(ew), P(es), P(eb), P(self.tok), P(self.x), ew.shape[0], h, gs, st), "embed")
-        ck(lib.q4_add_rmsnorm_dev(P(self.x), None, P(self.layers[0]["in_w"]), self.eps, P(self.hn), h, st),
-           "rmsnorm")
-        for i, L in enumerate(self.layers):                             # cpu_model.py:304-306
-            q4.gemv_multi_dev(L["qkv"], self.hn, outs=[self.q, self.k, self.v], lib=lib)
+        # embedding row (cpu_model.py:334-338)
+        cur, other = self.xbuf
+        ck(lib.q4_embed_dev(P(ew), P(es), P(eb), P(self.tok), P(cur), ew.shape[0], h, gs, st), "embed")
+        delta = None
+        for L in self.layers:                                           # cpu_model.py:304-306
+            # x = x + mlp (of the layer before); q/k/v of rms_norm(x, in_w)
+            q4.norm_gemv_multi_dev(L["qkv"], cur, delta, L["in_w"], self.eps,
+                                   x_out=other if delta is not None else None, outs=[self.q, self.k, self.v],
+                                   lib=lib)
+            if delta is not None:
+                cur, other = other, cur
             # bias + RoPE + the KV-cache write fused into the attention launches
             ck(lib.q4_attention_rope_dev(P(self.q), P(self.k), P(self.v), P(L["qkv_bias"]), P(self.cos),
                                          P(self.sin), P(self.pos), P(L["k_cache"]), P(L["v_cache"]), P(self.attn),
                                          P(self.attn_scratch), self.nh, self.nkv, self.hd, self.cap, self.scale, st),
                "attention")
             q4.gemv_dev(*L["o"], self.attn, out=self.o, lib=lib)
-            # x = x + attn; hn = rms_norm(x, post_w)
-            ck(lib.q4_add_rmsnorm_dev(P(self.x), P(self.o), P(L["post_w"]), self.eps, P(self.hn), h, st),
-               "add_rmsnorm")
-            q4.mlp_dev(L["gate"], L["up"], L["down"], self.hn, h=self.hbuf, out=self.mlp_out, lib=lib)
-            # x = x + mlp; hn = the next layer's input norm, or the final norm
-            nxt = self.layers[i + 1]["in_w"] if i + 1 < len(self.layers) else self.norm_w
-            ck(lib.q4_add_rmsnorm_dev(P(self.x), P(self.mlp_out), P(nxt), self.eps, P(self.hn), h, st),
-               "add_rmsnorm")
-        q4.gemv_dev(*self.lm_head, self.hn, out=self.logits, lib=lib)
+            # x = x + attn; SiLU(gate) * up of rms_norm(x, post_w), then down
+            q4.norm_gate_up_silu_dev(L["gate"], L["up"], cur, self.o, L["post_w"], self.eps, x_out=other,
+                                     h=self.hbuf, lib=lib)
+            cur, other = other, cur
+            q4.gemv_dev(*L["down"], self.hbuf, out=self.mlp_out, lib=lib)
+            delta = self.mlp_out
+        # x = x + mlp; lm_head of the final norm (cpu_model.py:367)
+        q4.norm_gemv_multi_dev([self.lm_head], cur, delta, self.norm_w, self.eps, outs=[self.logits], lib=lib)
         # greedy token (backends.py:106-109), history slot, position + 1
         ck(lib.q4_argmax_dev(P(self.logits), self.logits.shape[1], P(self.tok), P(self.hist), P(self.pos),
                              self.s0, self.hist.numel(), st), "argmax")

@@ -24,7 +24,8 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_dequant_dev", "q4_dequant_bf16_dev",
            # decode-step kernels (include/q4decode.h)
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
-           "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev")
+           "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev",
+           "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
@@ -73,6 +74,10 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_attention_dev.restype = _I
         lib.q4_attention_rope_dev.argtypes = [_VP] * 11 + [_I] * 4 + [_F, _VP]
         lib.q4_attention_rope_dev.restype = _I
+        lib.q4_norm_gemv_multi_dev.argtypes = [_I] + [_VP] * 8 + [_F, _VP, _I, _I, _VP]
+        lib.q4_norm_gemv_multi_dev.restype = _I
+        lib.q4_norm_gate_up_silu_dev.argtypes = [_VP] * 9 + [_F, _VP, _VP, _I, _I, _I, _VP]
+        lib.q4_norm_gate_up_silu_dev.restype = _I
         lib.q4_argmax_dev.argtypes = [_VP, _I, _VP, _VP, _VP, ctypes.c_int64, _I, _VP]
         lib.q4_argmax_dev.restype = _I
     return lib
@@ -117,6 +122,10 @@ def _ptr(t) -> int:
     return t.data_ptr()
 
 
+def _ptr_or_null(t):
+    return None if t is None else _ptr(t)
+
+
 def _stream(stream=None) -> int:
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
@@ -157,6 +166,42 @@ def gemv_multi_dev(mats, x, outs=None, stream=None, lib=None):
                                _ptr(x2), m, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gemv_multi_dev")
     return outs
+
+
+def norm_gemv_multi_dev(mats, x, delta, norm_w, eps, x_out=None, outs=None, stream=None, lib=None):
+    """gemv_multi_dev of rmsnorm(x + delta) * norm_w (one row), the norm in
+    the GEMV prologue; x_out (if given, with delta) receives x + delta."""
+    import torch
+    lib = lib or load()
+    n_in = mats[0][0].shape[1] * 8
+    gs = n_in // mats[0][1].shape[1]
+    if outs is None:
+        outs = [torch.empty((1, w.shape[0]), dtype=torch.float32, device=x.device) for w, _, _ in mats]
+    k = len(mats)
+    arr = lambda vals: (ctypes.c_void_p * k)(*vals)
+    rc = lib.q4_norm_gemv_multi_dev(k, arr([_ptr(a[0]) for a in mats]), arr([_ptr(a[1]) for a in mats]),
+                                    arr([_ptr(a[2]) for a in mats]), arr([_ptr(o) for o in outs]),
+                                    (ctypes.c_int * k)(*[a[0].shape[0] for a in mats]), _ptr(x),
+                                    _ptr_or_null(delta), _ptr(norm_w), eps, _ptr_or_null(x_out), n_in, gs,
+                                    _stream(stream))
+    check(lib, rc, "q4_norm_gemv_multi_dev")
+    return outs
+
+
+def norm_gate_up_silu_dev(gate, up, x, delta, norm_w, eps, x_out=None, h=None, stream=None, lib=None):
+    """gate_up_silu_dev of rmsnorm(x + delta) * norm_w (one row), the norm in
+    the GEMV prologue; x_out (if given, with delta) receives x + delta."""
+    import torch
+    lib = lib or load()
+    n_inter, n_in = gate[0].shape[0], gate[0].shape[1] * 8
+    gs = n_in // gate[1].shape[1]
+    if h is None:
+        h = torch.empty((1, n_inter), dtype=torch.float32, device=x.device)
+    rc = lib.q4_norm_gate_up_silu_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), _ptr(x),
+                                      _ptr_or_null(delta), _ptr(norm_w), eps, _ptr_or_null(x_out), _ptr(h),
+                                      n_inter, n_in, gs, _stream(stream))
+    check(lib, rc, "q4_norm_gate_up_silu_dev")
+    return h
 
 
 def gate_up_silu_dev(gate, up, x, h=None, stream=None, lib=None):

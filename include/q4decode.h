@@ -37,6 +37,31 @@ int q4_embed_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* bias
 int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, float* y, int n,
                        void* stream);
 
+/* The GEMVs that follow a residual add + RMSNorm, with the norm folded into
+ * their prologue (every workgroup normalises the input itself, so the
+ * separate q4_add_rmsnorm_dev launch goes away):
+ *   xs = x + delta (x alone when delta is NULL),
+ *   input = xs * (1 / sqrt(mean(xs*xs) + eps)) * norm_w  -- the bits of
+ *     q4_add_rmsnorm_dev's y for the same x, delta, norm_w, eps;
+ *   x_out (may be NULL; written only when delta is not NULL) receives xs, so a
+ *     caller alternates two residual buffers instead of updating x in place.
+ * One activation row; gs 64; 64 <= n_in <= 8192; x, delta, norm_w, x_out
+ * 16-byte aligned, x_out overlapping neither x nor delta.
+ * q4_norm_gemv_multi_dev: out[k] = W_k input as q4_gemv_multi_dev computes
+ * it (the q/k/v projections after input_layernorm, hetero/cpu_model.py:305
+ * and :271-273; lm_head after the final norm, :355 and :367).
+ * q4_norm_gate_up_silu_dev: h = SiLU(W_gate input) * (W_up input) as
+ * q4_gate_up_silu_dev computes it (the MLP after post_attention_layernorm,
+ * :306 and :292). */
+int q4_norm_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const* scales,
+                           const uint16_t* const* biases, float* const* out, const int* n_out, const float* x,
+                           const float* delta, const float* norm_w, float eps, float* x_out, int n_in, int gs,
+                           void* stream);
+int q4_norm_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,
+                             const uint32_t* up_w, const uint16_t* up_s, const uint16_t* up_b, const float* x,
+                             const float* delta, const float* norm_w, float eps, float* x_out, float* h,
+                             int n_inter, int n_in, int gs, void* stream);
+
 /* q/k/v projection biases, rotary embedding and the KV-cache write at the
  * position *pos (hetero/cpu_model.py:156-157 QLinear bias, :195-204 RoPE
  * non-traditional half split, :207-230 KVCache.update_and_fetch):

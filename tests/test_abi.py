@@ -116,5 +116,11 @@ def test_decode_kernel_argument_errors(lib):
     assert lib.q4_attention_rope_dev(*([p] * 11), 72, 4, 128, 64, 0.1, None) == q4.Q4_EARG
     assert lib.q4_attention_rope_dev(*([p] * 10), None, 28, 4, 128, 64, 0.1, None) == q4.Q4_EARG
     assert lib.q4_argmax_dev(None, 10, p, p, p, 0, 1, None) == q4.Q4_EARG
+    # norm-prologue GEMVs: bad count, n_in past 8192, x_out aliasing x, gs != 64
+    assert lib.q4_norm_gemv_multi_dev(0, None, None, None, None, None, p, None, p, 1e-6, None, 256, 64,
+                                      None) == q4.Q4_EARG
+    assert lib.q4_norm_gate_up_silu_dev(*([p] * 6), p, None, p, 1e-6, None, p, 64, 8256, 64, None) == q4.Q4_EARG
+    assert lib.q4_norm_gate_up_silu_dev(*([p] * 6), p, p, p, 1e-6, p, p, 64, 256, 64, None) == q4.Q4_EARG
+    assert lib.q4_norm_gate_up_silu_dev(*([p] * 6), p, None, p, 1e-6, None, p, 64, 256, 128, None) == q4.Q4_EARG
     assert lib.q4_attention_scratch_floats(28, 128, 2048) == 28 * 32 * 130
     assert lib.q4_attention_scratch_floats(28, 128, 2049) == 28 * 33 * 130
