@@ -483,8 +483,8 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(), "traffic_source": PMC_SUMMARY,
                      "algorithmic_bytes_per_launch": round(sweep_bytes / n_launch),
-                     "kernel": "gemv_stream_kernel<1,16> (x prologue fused), averaged over the "
-                               "launches of the grouped sweep",
+                     "kernel": "gemv_stream_kernel<MR=1, RW, PAIR, RING, NORM=false> (x prologue "
+                               "fused), averaged over the launches of the grouped sweep",
                      "avg_launch_us": round(ev_ms * 1e3 / n_launch, 3)},
         "per_shape": per_shape,
         "one_call_per_projection": {"ms_per_step": round(calls_ms, 4),
