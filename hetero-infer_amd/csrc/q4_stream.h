@@ -36,7 +36,7 @@ namespace q4k {
 // scalar work.
 constexpr int kMaxMats = 4;
 constexpr int kEarly = 2;           // ring items issued before the x prologue has its data
-constexpr int kUnitItems = 4;       // rows per unit grow until a unit has this many items
+constexpr int kUnitItems = 16;      // rows per unit grow until a unit has this many items
 
 struct MatList {
     const uint32_t* w[kMaxMats];
@@ -155,16 +155,19 @@ __device__ __forceinline__ void load_item(Item& it, const MatList& ml, int unit,
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(pick(ml.b, p) + static_cast<size_t>(o) * G, gbytes);
     // the three loads in a fixed order wherever an item is loaded: the
     // partial waits on the ring are computed from the issue order, which
-    // must then be the same on entry to the main loop as around it.  Read
-    // once, so non-temporal (cache policy nt): the stream does not push x
-    // and the outputs out of L2 and the last-level cache.
+    // must then be the same on entry to the main loop as around it.  The
+    // weights are read once, so non-temporal (cache policy nt): the stream
+    // does not push x and the outputs out of L2 and the last-level cache.
+    // Scales and biases keep the default policy: an item reads a 64-byte
+    // window of them that shares its edge sectors with the row's next item
+    // and with the neighbouring rows.
     constexpr int kNonTemporal = 2;
     __builtin_amdgcn_sched_barrier(0);
     it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, word0 * 4, 0, kNonTemporal));
     __builtin_amdgcn_sched_barrier(0);
-    it.s = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, kNonTemporal);
+    it.s = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    it.b = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, kNonTemporal);
+    it.b = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
 }
 

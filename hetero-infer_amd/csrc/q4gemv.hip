@@ -648,9 +648,11 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, c
     const int wr = (C * kChunkWords + 64 * rmax - 1) / (64 * rmax);
     if (wr > minw) minw = wr;
     if (minw > 16) return 0;
-    // rows per unit: 1, or more when rows are plentiful and short
+    // rows per unit: 1, or more when rows are plentiful and short -- up to 8
+    // rows and kUnitItems items, while every wave still gets two units (the
+    // end of a unit costs a serial chain, a unit too many per wave a tail)
     int UB = 1;
-    while (UB < 4 && UB * C * (PAIR ? 2 : 1) < kUnitItems && n_total >= 2 * UB * kWavesPerCu * cus) UB *= 2;
+    while (UB < 8 && UB * C * (PAIR ? 2 : 1) < kUnitItems && n_total >= 4 * UB * kWavesPerCu * cus) UB *= 2;
     while (MR * UB > 64) UB >>= 1;
     for (int k = 0; k < ml.count; k++)                 // a unit must not straddle matrices
         while (ml.n_out[k] % UB) UB >>= 1;
