@@ -48,11 +48,32 @@ __device__ __forceinline__ float dpp_max(float a) {
     return fmaxf(a, __int_as_float(o));
 }
 
-// Butterfly sum over the 64 lanes (every lane gets the total).
+// Raw buffer resource over [p, p + bytes): loads at an offset >= bytes
+// return 0 without a memory access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
+}
+constexpr uint32_t kOutOfRange = 0x80000000u;   // any offset past every resource here
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float a) {
+    const int o = __builtin_amdgcn_update_dpp(__float_as_int(a), __float_as_int(a), CTRL, 0xF, 0xF, false);
+    return __fadd_rn(a, __int_as_float(o));
+}
+
+// Sum over the 64 lanes, the same value in every lane: DPP pairs, quads,
+// halves and rows of 16 (every lane of a row ends with the row's sum),
+// then the four row sums added in row order.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o));
-    return v;
+    v = dpp_add<0xB1>(v);    // quad_perm 1,0,3,2
+    v = dpp_add<0x4E>(v);    // quad_perm 2,3,0,1
+    v = dpp_add<0x141>(v);   // row_half_mirror
+    v = dpp_add<0x140>(v);   // row_mirror
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return __fadd_rn(__fadd_rn(__fadd_rn(r0, r1), r2), r3);
 }
 
 // 1 / sqrt(mean + eps) of RMSNorm from the sum of squares of n values

@@ -12,12 +12,6 @@
 namespace q4k {
 namespace {
 
-__device__ __forceinline__ float wave_maxf(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-
 __device__ __forceinline__ uint16_t f2h_rne(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
 }
@@ -154,7 +148,9 @@ constexpr int kMaxChunks = 1024;        // cap <= 65536
 // rope_kv_kernel does), and the workgroup whose chunk holds the position
 // also rotates the new key, writes the new key and value rows to the cache
 // and takes them from registers instead of the cache.
-template <bool ROPE>
+// G: query heads per kv head, a template parameter so that the per-head
+// loops unroll and their LDS reads are issued together.
+template <bool ROPE, int G>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restrict__ q,
                                                            uint16_t* __restrict__ kc,
                                                            uint16_t* __restrict__ vc,
@@ -168,9 +164,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     __shared__ float4 q_s[kMaxG][kMaxD / 4];
     __shared__ uint4 k_s[kChunk][kRowU4];
     __shared__ uint4 v_s[kChunk][kRowU4];
-    __shared__ float p_s[kMaxG][kChunk];
+    __shared__ __attribute__((aligned(16))) float p_s[kMaxG][kChunk];
+    __shared__ float sc_part[4][kMaxG][kChunk];
     const int chunk = blockIdx.x, kvh = blockIdx.y, n_chunks = gridDim.x;
-    const int G = nh / nkv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t pos = *pos_p;
     const int c0 = chunk * kChunk;
@@ -189,11 +185,24 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     // the chunk's new row (the position) comes from registers, not the cache
     const bool fresh = ROPE && pos >= c0 && pos < c0 + kChunk && pos < cap;
     // every load up front: q, the chunk's K and V rows (4 uint4 each per
-    // thread at d = 128); rows past `valid` (and a fresh row) are not read
-    const uint4* k4p = reinterpret_cast<const uint4*>(kc + (static_cast<size_t>(kvh) * cap + c0) * d);
-    const uint4* v4p = reinterpret_cast<const uint4*>(vc + (static_cast<size_t>(kvh) * cap + c0) * d);
+    // thread at d = 128), unconditional, through resources that end with the
+    // rows to read: rows past `valid` (and a fresh row) read 0 without an
+    // access, and the staging registers stay registers
     const int nkv4 = (fresh ? valid - 1 : valid) * du4;
+    const __amdgpu_buffer_rsrc_t kr =
+        buf_rsrc(kc + (static_cast<size_t>(kvh) * cap + c0) * d, static_cast<uint32_t>(nkv4) * 16u);
+    const __amdgpu_buffer_rsrc_t vr =
+        buf_rsrc(vc + (static_cast<size_t>(kvh) * cap + c0) * d, static_cast<uint32_t>(nkv4) * 16u);
     uint4 kv[4], vv[4];
+    uint16_t fh1 = 0, fh2 = 0;                               // the fresh row's values of this thread
+    auto load_kv = [&]() {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t off = static_cast<uint32_t>(r * 256 + tid) * 16u;
+            kv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+            vv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
+        }
+    };
     if constexpr (ROPE) {
         // hetero/cpu_model.py:156-157 (bias) and :195-204 (RoPE), the same
         // fp32 operations as rope_kv_kernel
@@ -224,14 +233,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
                 nvb = bias[(nh + nkv) * d + e];
             }
         }
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int e = r * 256 + tid;
-            if (e < nkv4) {
-                kv[r] = k4p[e];
-                vv[r] = v4p[e];
-            }
-        }
+        load_kv();
         float* qf = reinterpret_cast<float*>(&q_s[0][0]);
 #pragma unroll
         for (int r = 0; r < 2; r++) {
@@ -245,22 +247,17 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
             }
         }
         if (fresh) {
-            const int row = static_cast<int>(pos - c0);
-            uint16_t* kl = reinterpret_cast<uint16_t*>(&k_s[row][0]);
-            uint16_t* vl = reinterpret_cast<uint16_t*>(&v_s[row][0]);
             uint16_t* kg = kc + (static_cast<size_t>(kvh) * cap + pos) * d;
             uint16_t* vg = vc + (static_cast<size_t>(kvh) * cap + pos) * d;
             if (tid < half) {
                 const float x1 = __fadd_rn(nk[0], nkb[0]), x2 = __fadd_rn(nk[1], nkb[1]);
                 const float c = nkc[0], sn = nkc[1];
-                const uint16_t h1 = f2h_rne(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn)));
-                const uint16_t h2 = f2h_rne(__fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, c)));
-                kl[tid] = h1; kl[tid + half] = h2;
-                kg[tid] = h1; kg[tid + half] = h2;
+                fh1 = f2h_rne(__fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, sn)));
+                fh2 = f2h_rne(__fadd_rn(__fmul_rn(x1, sn), __fmul_rn(x2, c)));
+                kg[tid] = fh1; kg[tid + half] = fh2;
             } else if (tid < half + d) {
-                const uint16_t hv = f2h_rne(__fadd_rn(nv, nvb));
-                vl[tid - half] = hv;
-                vg[tid - half] = hv;
+                fh1 = f2h_rne(__fadd_rn(nv, nvb));
+                vg[tid - half] = fh1;
             }
         }
     } else {
@@ -268,74 +265,152 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         const int nq4 = G * d / 4;
         float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
         if (tid < nq4) qv = q4p[tid];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int e = r * 256 + tid;
-            if (e < nkv4) {
-                kv[r] = k4p[e];
-                vv[r] = v4p[e];
-            }
-        }
+        load_kv();
         if (tid < nq4) q_s[tid / (d / 4)][tid % (d / 4)] = qv;
     }
+    // all 64 rows but a fresh one: the rows past the ones read (past the
+    // position) hold 0, so the output loop needs no bound
+    const int frow = fresh ? static_cast<int>(pos - c0) : -1;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int e = r * 256 + tid;
-        if (e < nkv4) {
+        if (e < kChunk * du4 && e / du4 != frow) {
             k_s[e / du4][e % du4] = kv[r];
             v_s[e / du4][e % du4] = vv[r];
         }
     }
-    __syncthreads();
-    // scores: lane = position, heads wave and wave + 4
-    {
-        const int s = lane;
-        for (int g = wave; g < G; g += 4) {
-            float acc = 0.0f;
-            if (s < valid) {
-#pragma unroll 4
-                for (int c = 0; c < du4; c++) {
-                    const uint4 kk = k_s[s][c];
-                    const float4 qa = q_s[g][2 * c], qb = q_s[g][2 * c + 1];
-                    acc = __builtin_fmaf(qa.x, h2f_bits(static_cast<uint16_t>(kk.x)), acc);
-                    acc = __builtin_fmaf(qa.y, h2f_bits(static_cast<uint16_t>(kk.x >> 16)), acc);
-                    acc = __builtin_fmaf(qa.z, h2f_bits(static_cast<uint16_t>(kk.y)), acc);
-                    acc = __builtin_fmaf(qa.w, h2f_bits(static_cast<uint16_t>(kk.y >> 16)), acc);
-                    acc = __builtin_fmaf(qb.x, h2f_bits(static_cast<uint16_t>(kk.z)), acc);
-                    acc = __builtin_fmaf(qb.y, h2f_bits(static_cast<uint16_t>(kk.z >> 16)), acc);
-                    acc = __builtin_fmaf(qb.z, h2f_bits(static_cast<uint16_t>(kk.w)), acc);
-                    acc = __builtin_fmaf(qb.w, h2f_bits(static_cast<uint16_t>(kk.w >> 16)), acc);
-                }
-            }
-            const float sc = s < valid ? __fmul_rn(acc, scale) : -__builtin_inff();
-            const float m = wave_maxf(sc);
-            const float p = s < valid ? expf(__fsub_rn(sc, m)) : 0.0f;
-            const float l = wave_sum(p);
-            p_s[g][s] = p;
-            if (lane == 0) {
-                float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2);
-                dst[0] = m;
-                dst[1] = l;
-            }
+    if (fresh) {
+        const int row = frow, half = d >> 1;
+        uint16_t* kl = reinterpret_cast<uint16_t*>(&k_s[row][0]);
+        uint16_t* vl = reinterpret_cast<uint16_t*>(&v_s[row][0]);
+        if (tid < half) {
+            kl[tid] = fh1;
+            kl[tid + half] = fh2;
+        } else if (tid < half + d) {
+            vl[tid - half] = fh1;
         }
     }
     __syncthreads();
-    // unnormalised outputs: thread (head, fp16 pair of the row)
-    const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v_s[0][0]);
-    constexpr int kRowW = kRowU4 * 4;
-    const int dp = d >> 1;
-    for (int e = tid; e < G * dp; e += blockDim.x) {
-        const int g = e / dp, i = e - g * dp;
-        float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll 8
-        for (int s = 0; s < valid; s++) {
-            const uint32_t w2 = vw[s * kRowW + i];
-            const float p = p_s[g][s];
-            a0 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(w2)), a0);
-            a1 = __builtin_fmaf(p, h2f_bits(static_cast<uint16_t>(w2 >> 16)), a1);
+    // scores: wave w takes dims [w*d/4, (w+1)*d/4) of every position of the
+    // chunk (lane = position) for all G heads, so each K element is
+    // converted once; the four partial dots are added in wave order below
+    {
+        const int s = lane;
+        const int c_begin = wave * (du4 >> 2), c_end = c_begin + (du4 >> 2);
+        float acc[kMaxG];
+#pragma unroll
+        for (int g = 0; g < kMaxG; g++) acc[g] = 0.0f;
+        for (int c = c_begin; c < c_end; c++) {
+            const uint4 kk = k_s[s][c];
+            const float kf[8] = {h2f_bits(static_cast<uint16_t>(kk.x)), h2f_bits(static_cast<uint16_t>(kk.x >> 16)),
+                                 h2f_bits(static_cast<uint16_t>(kk.y)), h2f_bits(static_cast<uint16_t>(kk.y >> 16)),
+                                 h2f_bits(static_cast<uint16_t>(kk.z)), h2f_bits(static_cast<uint16_t>(kk.z >> 16)),
+                                 h2f_bits(static_cast<uint16_t>(kk.w)), h2f_bits(static_cast<uint16_t>(kk.w >> 16))};
+#pragma unroll
+            for (int g = 0; g < kMaxG; g++) {
+                if (g < G) {                                         // uniform
+                    const float4 qa = q_s[g][2 * c], qb = q_s[g][2 * c + 1];
+                    acc[g] = __builtin_fmaf(qa.x, kf[0], acc[g]);
+                    acc[g] = __builtin_fmaf(qa.y, kf[1], acc[g]);
+                    acc[g] = __builtin_fmaf(qa.z, kf[2], acc[g]);
+                    acc[g] = __builtin_fmaf(qa.w, kf[3], acc[g]);
+                    acc[g] = __builtin_fmaf(qb.x, kf[4], acc[g]);
+                    acc[g] = __builtin_fmaf(qb.y, kf[5], acc[g]);
+                    acc[g] = __builtin_fmaf(qb.z, kf[6], acc[g]);
+                    acc[g] = __builtin_fmaf(qb.w, kf[7], acc[g]);
+                }
+            }
         }
-        float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2) + 2;
-        reinterpret_cast<float2*>(dst)[i] = make_float2(a0, a1);
+#pragma unroll
+        for (int g = 0; g < kMaxG; g++)
+            if (g < G) sc_part[wave][g][s] = acc[g];
+    }
+    __syncthreads();
+    // softmax over the chunk, heads wave and wave + 4 (lane = position)
+    for (int g = wave; g < G; g += 4) {
+        const int s = lane;
+        const float dot = __fadd_rn(__fadd_rn(__fadd_rn(sc_part[0][g][s], sc_part[1][g][s]), sc_part[2][g][s]),
+                                    sc_part[3][g][s]);
+        const float sc = s < valid ? __fmul_rn(dot, scale) : -__builtin_inff();
+        const float m = wave_max(sc);
+        const float p = s < valid ? expf(__fsub_rn(sc, m)) : 0.0f;
+        const float l = wave_sum(p);
+        p_s[g][s] = p;
+        if (lane == 0) {
+            float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2);
+            dst[0] = m;
+            dst[1] = l;
+        }
+    }
+    __syncthreads();
+    // unnormalised outputs: wave w takes positions [16w, 16w + 16), lane =
+    // fp16 pair of the row, all G heads; the K rows are no longer read, so
+    // their space holds the four partial outputs, added in wave order
+    float* out_part = reinterpret_cast<float*>(&k_s[0][0]);          // [4][kMaxG][kMaxD]
+    {
+        const int i = lane, dp = d >> 1;
+        float a0[kMaxG], a1[kMaxG];
+#pragma unroll
+        for (int g = 0; g < kMaxG; g++) a0[g] = a1[g] = 0.0f;
+        if (i < dp) {
+            const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v_s[0][0]);
+            constexpr int kRowW = kRowU4 * 4;
+            // p is 0 and the V row is 0 past the valid positions
+            for (int s0 = 16 * wave; s0 < 16 * wave + 16; s0 += 4) {
+                uint32_t w2[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) w2[j] = vw[(s0 + j) * kRowW + i];
+                float4 pg[kMaxG];
+#pragma unroll
+                for (int g = 0; g < kMaxG; g++)
+                    if (g < G) pg[g] = *reinterpret_cast<const float4*>(&p_s[g][s0]);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float v0 = h2f_bits(static_cast<uint16_t>(w2[j]));
+                    const float v1 = h2f_bits(static_cast<uint16_t>(w2[j] >> 16));
+#pragma unroll
+                    for (int g = 0; g < kMaxG; g++) {
+                        if (g < G) {
+                            const float p = j == 0 ? pg[g].x : j == 1 ? pg[g].y : j == 2 ? pg[g].z : pg[g].w;
+                            a0[g] = __builtin_fmaf(p, v0, a0[g]);
+                            a1[g] = __builtin_fmaf(p, v1, a1[g]);
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < kMaxG; g++)
+                if (g < G) {
+                    float* op = out_part + (wave * kMaxG + g) * kMaxD;
+                    op[2 * i] = a0[g];
+                    op[2 * i + 1] = a1[g];
+                }
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < G * d; e += blockDim.x) {
+        const int g = e / d, j = e - g * d;
+        const float* op = out_part + g * kMaxD + j;
+        const float o = __fadd_rn(__fadd_rn(__fadd_rn(op[0], op[kMaxG * kMaxD]), op[2 * kMaxG * kMaxD]),
+                                  op[3 * kMaxG * kMaxD]);
+        my[(static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2) + 2 + j] = o;
+    }
+}
+
+template <bool ROPE>
+void launch_partial(int G, dim3 grid, hipStream_t st, const float* q, uint16_t* kc, uint16_t* vc, const int64_t* pos,
+                    float* part, int nh, int nkv, int d, int cap, float scale, const float* kraw, const float* vraw,
+                    const float* bias, const float* cos_t, const float* sin_t) {
+    switch (G) {
+#define Q4_ATTN_CASE(g)                                                                                        \
+    case g:                                                                                                    \
+        hipLaunchKernelGGL((attn_partial_kernel<ROPE, g>), grid, dim3(256), 0, st, q, kc, vc, pos, part, nh, nkv, d, \
+                           cap, scale, kraw, vraw, bias, cos_t, sin_t);                                       \
+        break;
+        Q4_ATTN_CASE(1) Q4_ATTN_CASE(2) Q4_ATTN_CASE(3) Q4_ATTN_CASE(4)
+        Q4_ATTN_CASE(5) Q4_ATTN_CASE(6) Q4_ATTN_CASE(7) Q4_ATTN_CASE(8)
+#undef Q4_ATTN_CASE
+        default: break;                        // the callers check 1 <= G <= kMaxG
     }
 }
 
@@ -354,7 +429,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
         w_s[c] = m;
         mloc = fmaxf(mloc, m);
     }
-    mloc = wave_maxf(mloc);
+    mloc = wave_max(mloc);
     if ((tid & 63) == 0) red[tid >> 6] = mloc;
     __syncthreads();
     float M = -__builtin_inff();
@@ -500,15 +575,15 @@ int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_
         return fail(Q4_EARG, "q4_attention_dev: unsupported sizes (heads %d, kv heads %d, head_dim %d, cap %d)",
                     n_heads, n_kv, head_dim, cap);
     const int n_chunks = (cap + kChunk - 1) / kChunk;
-    if (n_chunks > kMaxChunks || head_dim % 8 || 256 % head_dim || (reinterpret_cast<uintptr_t>(q) & 15) ||
+    if (n_chunks > kMaxChunks || head_dim % 32 || 256 % head_dim || (reinterpret_cast<uintptr_t>(q) & 15) ||
         (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
         (reinterpret_cast<uintptr_t>(scratch) & 7))
-        return fail(Q4_EARG, "q4_attention_dev: cap %d over %d, head_dim %d not a multiple of 8 dividing 256, "
+        return fail(Q4_EARG, "q4_attention_dev: cap %d over %d, head_dim %d not 32, 64 or 128, "
                              "or a pointer not 16-byte aligned", cap, kMaxChunks * kChunk, head_dim);
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(attn_partial_kernel<false>, dim3(n_chunks, n_kv), dim3(256), 0, st, q,
-                       const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache), pos, scratch, n_heads, n_kv,
-                       head_dim, cap, scale, nullptr, nullptr, nullptr, nullptr, nullptr);
+    launch_partial<false>(n_heads / n_kv, dim3(n_chunks, n_kv), st, q, const_cast<uint16_t*>(k_cache),
+                          const_cast<uint16_t*>(v_cache), pos, scratch, n_heads, n_kv, head_dim, cap, scale, nullptr,
+                          nullptr, nullptr, nullptr, nullptr);
     if (int rc = check_launch("q4_attention_dev (partial)")) return rc;
     hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(256), 0, st, scratch, out, n_chunks, head_dim);
     return check_launch("q4_attention_dev (combine)");
@@ -519,7 +594,7 @@ int q4_attention_rope_dev(const float* q, const float* k, const float* v, const 
                           float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream) {
     if (!q || !k || !v || !bias || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !out || !scratch)
         return fail(Q4_EARG, "q4_attention_rope_dev: null pointer");
-    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kMaxG || head_dim <= 0 || head_dim % 8 ||
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kMaxG || head_dim <= 0 || head_dim % 32 ||
         256 % head_dim || head_dim > kMaxD || cap <= 0 || (cap + kChunk - 1) / kChunk > kMaxChunks ||
         (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
         (reinterpret_cast<uintptr_t>(scratch) & 7))
@@ -527,8 +602,8 @@ int q4_attention_rope_dev(const float* q, const float* k, const float* v, const 
                              "or a pointer not aligned", n_heads, n_kv, head_dim, cap);
     const int n_chunks = (cap + kChunk - 1) / kChunk;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(attn_partial_kernel<true>, dim3(n_chunks, n_kv), dim3(256), 0, st, q, k_cache, v_cache, pos,
-                       scratch, n_heads, n_kv, head_dim, cap, scale, k, v, bias, cos_t, sin_t);
+    launch_partial<true>(n_heads / n_kv, dim3(n_chunks, n_kv), st, q, k_cache, v_cache, pos, scratch, n_heads,
+                         n_kv, head_dim, cap, scale, k, v, bias, cos_t, sin_t);
     if (int rc = check_launch("q4_attention_rope_dev (partial)")) return rc;
     hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(256), 0, st, scratch, out, n_chunks, head_dim);
     return check_launch("q4_attention_rope_dev (combine)");

@@ -122,12 +122,6 @@ struct Item {
     int unit;                       // wave-uniform
 };
 
-// Raw buffer resource over [p, p + bytes): loads at an offset >= bytes
-// return 0 without a memory access.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, static_cast<int>(bytes), 0x00020000);
-}
-constexpr uint32_t kOutOfRange = 0x80000000u;   // any offset past every resource here
 
 // Issue the loads of item (chunk c, row slot r) of unit `unit`.  The row is
 // wave-uniform: each array gets a resource over that row alone, so lanes

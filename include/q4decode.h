@@ -84,7 +84,8 @@ long q4_attention_scratch_floats(int n_heads, int head_dim, int cap);
  * out [n_heads][d] fp32.  The context is split in chunks of 64 positions
  * (one workgroup per kv head and chunk), whose partial softmax results are
  * combined by a second launch; scratch holds them
- * (q4_attention_scratch_floats). */
+ * (q4_attention_scratch_floats).  head_dim 32, 64 or 128; at most 8 query
+ * heads per kv head; cap <= 65536. */
 int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int64_t* pos,
                      float* out, float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale,
                      void* stream);
