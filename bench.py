@@ -118,6 +118,56 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
             "peak_tflops_bf16_dense": 2500.0, "flops": flops}
 
 
+def small_m_bench(torch, lib, layers, dev, ms=(1, 2, 4, 8), reps=5):
+    """Small-M batched GEMV (M activation rows in flight): the q_proj shape
+    (3584 -> 3584) and the MLP block (fused gate/up + SiLU*mul, then down),
+    over the 28 layers' distinct weights so every call streams its weights
+    from HBM; GB/s counts the weights once per call plus M rows of x and y."""
+    from hetero import q4
+    res = {}
+    stream = torch.cuda.Stream(device=dev)
+    for m in ms:
+        x = torch.randn((m, 3584), device=dev)
+        y = torch.empty((m, 3584), device=dev)
+        h = torch.empty((m, 18944), device=dev)
+        mo = torch.empty((m, 3584), device=dev)
+
+        def step_q():
+            for layer in layers:
+                q4.gemv_dev(*layer[0], x, out=y, stream=stream, lib=lib)
+
+        def step_mlp():
+            for layer in layers:
+                q4.mlp_dev(layer[4], layer[5], layer[6], x, h=h, out=mo, stream=stream, lib=lib)
+
+        row = {}
+        for name, step, nbytes in (
+                ("q_proj", step_q, len(layers) * gemv_bytes(m, 3584, 3584)),
+                ("mlp", step_mlp, len(layers) * (2 * gemv_bytes(m, 18944, 3584) + gemv_bytes(m, 3584, 18944)))):
+            with torch.cuda.stream(stream):
+                step()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                step()
+            with torch.cuda.stream(stream):
+                g.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(reps):
+                    g.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
+            gbs = nbytes / len(layers) / (us * 1e-6) / 1e9
+            row[name] = {"us_per_call": round(us, 2), "GB_s": round(gbs, 1), "frac_peak": round(gbs / HBM_PEAK_GBS, 4)}
+            del g
+        res[f"M={m}"] = row
+    return {"workload": "M rows of x (N(0,1)), q_proj 3584->3584 and the MLP block (gate/up 3584->18944 fused with "
+                        "SiLU*mul, down 18944->3584), 28 layers of distinct weights, HIP graph", "rows": res}
+
+
 def decode_weights(torch, cfg, dev, seed=99):
     """Random-init 4-bit Qwen2 weights (reference tensor names), generated on
     the GPU and copied to host arrays for the NumPy stage."""
@@ -314,6 +364,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-small-m", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--sweep-only", action="store_true",
@@ -492,7 +543,10 @@ def main():
                                     "launches_per_step": LAYERS * len(LAYER_SHAPES) + 1},
     }
     if args.sweep_only:
-        args.no_prefill = args.no_cpu_baseline = args.no_decode = True
+        args.no_prefill = args.no_cpu_baseline = args.no_decode = args.no_small_m = True
+    if not args.no_small_m:
+        log("small-M ...")
+        result["small_m"] = small_m_bench(torch, lib, layers, dev)
     if not args.no_prefill:
         log("prefill ...")
         result["prefill"] = prefill_bench(torch, lib, layers, dev)

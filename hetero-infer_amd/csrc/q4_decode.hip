@@ -479,14 +479,27 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
     const int tid = threadIdx.x, nt = blockDim.x;
     float bv = -__builtin_inff();
     int bi = 0x7FFFFFFF;
+    // eight float4 loads in flight per thread, through a resource over the
+    // whole float4s (past the end: 0, never compared)
     const int n4 = n >> 2;
-    const float4* l4 = reinterpret_cast<const float4*>(logits);
-    for (int i = tid; i < n4; i += nt) {
-        const float4 f = l4[i];
-        better(bv, bi, f.x, 4 * i);
-        better(bv, bi, f.y, 4 * i + 1);
-        better(bv, bi, f.z, 4 * i + 2);
-        better(bv, bi, f.w, 4 * i + 3);
+    const __amdgpu_buffer_rsrc_t lr = buf_rsrc(logits, static_cast<uint32_t>(n4) * 16u);
+    constexpr int kU = 8;
+    for (int base = 0; base < n4; base += kU * nt) {
+        float4 f[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++)
+            f[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  lr, static_cast<uint32_t>(base + u * nt + tid) * 16u, 0, 0));
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int i = base + u * nt + tid;
+            if (i < n4) {
+                better(bv, bi, f[u].x, 4 * i);
+                better(bv, bi, f[u].y, 4 * i + 1);
+                better(bv, bi, f[u].z, 4 * i + 2);
+                better(bv, bi, f[u].w, 4 * i + 3);
+            }
+        }
     }
     for (int i = 4 * n4 + tid; i < n; i += nt) better(bv, bi, logits[i], i);
 #pragma unroll

@@ -46,6 +46,7 @@ struct MatList {
     int n_out[kMaxMats];
     int row_begin[kMaxMats + 1];   // prefix sums of n_out
     int count;
+    int mrows;                     // activation rows present (<= MR): the rest read 0 and are not stored
 };
 
 // The norm prologue (NORM instances): the kernel's input is
@@ -67,9 +68,10 @@ __host__ __device__ inline int term_stride(int G) { return ((G + 3) & ~3) | 4; }
 // the 16-byte reads of one lane per group land on distinct banks.
 constexpr int kStageStride = 68;
 
-inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU) {
+// rw: words of x per thread and row; the staged floats only exist for rw > 1.
+inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU, int rw) {
     const size_t terms = static_cast<size_t>(nwaves) * mr * NU * term_stride(G) * 4;
-    const size_t stage = static_cast<size_t>(mr) * G * kStageStride * 4;
+    const size_t stage = rw > 1 ? static_cast<size_t>(mr) * G * kStageStride * 4 : 0;
     return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
          + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
          + static_cast<size_t>(mr) * 16 * 4 + 16                         // amax per wave, counter
@@ -192,7 +194,12 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // Words of x per thread and activation row that the word pass keeps in
 // registers (RW rounds of blockDim.x words); the host picks the instance.
 template <int MR>
-__host__ __device__ constexpr int stream_max_rounds() { return MR == 1 ? 4 : 2; }
+__host__ __device__ constexpr int stream_max_rounds() { return MR == 1 ? 4 : MR <= 4 ? 2 : 1; }
+
+// Waves per CU the instance runs at: 4 per SIMD (<= 128 VGPRs), 2 for eight
+// rows (<= 256 VGPRs, workgroups of at most 512 threads).
+template <int MR>
+__host__ __device__ constexpr int stream_waves_per_cu() { return MR >= 8 ? 8 : 16; }
 
 // PAIR: matrices 0 and 1 (gate, up) are computed row for row and the output
 // is out[0] = SiLU(gate) * up.
@@ -200,11 +207,14 @@ __host__ __device__ constexpr int stream_max_rounds() { return MR == 1 ? 4 : 2; 
 // of squares taken in the order of add_rmsnorm_kernel (one word per thread,
 // wave sums in wave order), so the input is bit for bit the one that
 // kernel writes.  MR = 1 and RW = 1 only.
+// Rows of x past ml.mrows (an M below MR) read 0 and their outputs are not
+// stored.
 // Host guarantees: MR * (n_in / 64) <= blockDim.x (one thread per group
 // item), chunks * 256 <= RW * blockDim.x, n_in % 64 == 0, x 16-byte aligned.
 template <int MR, int RW, bool PAIR, int RING, bool NORM>
-__global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const float* __restrict__ x,
-                                                          int n_in, int UB, NormArgs na) {
+__global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_kernel(MatList ml,
+                                                                                     const float* __restrict__ x,
+                                                                                     int n_in, int UB, NormArgs na) {
     static_assert(!NORM || (MR == 1 && RW == 1), "the norm prologue takes one row, one word per thread");
     extern __shared__ uint4 lds4[];
     constexpr int lpg = 2;                                        // lanes per group
@@ -229,7 +239,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
     //      each, through a resource over x (words at or past the row end read
     //      0); waves with no word in a round issue nothing.  These are the
     //      first loads of the kernel, so the waits further down stay exact.
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(MR * n_in) * 4u);
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(ml.mrows * n_in) * 4u);
     float4 wv[MR][RW][2];
 #pragma unroll
     for (int m = 0; m < MR; m++)
@@ -476,7 +486,7 @@ __global__ __launch_bounds__(1024) void gemv_stream_kernel(MatList ml, const flo
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         if (lane < MR * UB) {
             const int m = lane / UB, uu = lane - m * UB, gr = unit * UB + uu;
-            if (gr < n_total) {
+            if (gr < n_total && m < ml.mrows) {
                 const float acc = chain_sum(Tw + (m * NU + uu) * Ts, G);
                 if constexpr (PAIR) {
                     const float up = chain_sum(Tw + (m * NU + UB + uu) * Ts, G);

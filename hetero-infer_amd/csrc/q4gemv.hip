@@ -85,6 +85,9 @@ Q4_STREAM_EXTERN(1, 3, false, 5, false) Q4_STREAM_EXTERN(1, 4, false, 5, false)
 Q4_STREAM_RINGS(1, 1, true, false) Q4_STREAM_RINGS(1, 2, true, false)
 Q4_STREAM_RINGS(2, 1, false, false) Q4_STREAM_RINGS(2, 2, false, false)
 Q4_STREAM_RINGS(2, 1, true, false) Q4_STREAM_RINGS(2, 2, true, false)
+Q4_STREAM_RINGS(4, 1, false, false) Q4_STREAM_RINGS(4, 2, false, false)
+Q4_STREAM_RINGS(4, 1, true, false) Q4_STREAM_RINGS(4, 2, true, false)
+Q4_STREAM_RINGS(8, 1, false, false) Q4_STREAM_RINGS(8, 1, true, false)
 Q4_STREAM_RINGS(1, 1, false, true) Q4_STREAM_EXTERN(1, 1, false, 5, true)
 Q4_STREAM_RINGS(1, 1, true, true)
 #undef Q4_STREAM_RINGS
@@ -636,7 +639,7 @@ int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int 
 template <int MR, bool PAIR = false, bool NORM = false>
 int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, const NormArgs& na = NormArgs{}) {
     static_assert(!NORM || MR == 1, "the norm prologue takes one row");
-    constexpr int kWavesPerCu = 16;                     // 4 waves per SIMD at <= 128 VGPRs
+    constexpr int kWavesPerCu = stream_waves_per_cu<MR>();
     constexpr int rmax = NORM ? 1 : stream_max_rounds<MR>();
     const int G = n_in / 64;
     const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
@@ -647,7 +650,7 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, c
     int minw = (MR * G + 63) / 64;
     const int wr = (C * kChunkWords + 64 * rmax - 1) / (64 * rmax);
     if (wr > minw) minw = wr;
-    if (minw > 16) return 0;
+    if (minw > kWavesPerCu) return 0;
     // rows per unit: 1, or more when rows are plentiful and short -- up to 8
     // rows and kUnitItems items, while every wave still gets two units (the
     // end of a unit costs a serial chain, a unit too many per wave a tail)
@@ -662,17 +665,20 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, c
     const int target = n_units < kWavesPerCu * cus ? n_units : kWavesPerCu * cus;
     int nwaves = (target + cus - 1) / cus;
     if (nwaves < minw) nwaves = minw;
-    if (nwaves > 16) nwaves = 16;
-    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB);
-    if (lds > kStreamLdsMax) return 0;
+    if (nwaves > kWavesPerCu) nwaves = kWavesPerCu;
     const int rw = (C * kChunkWords + 64 * nwaves - 1) / (64 * nwaves);
+    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB, rw);
+    if (lds > kStreamLdsMax) return 0;
     const int items = (PAIR ? 2 : 1) * UB * C;
     if constexpr (NORM)
         return rw == 1 ? launch_stream_rw<MR, 1, PAIR, true>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st)
                        : 0;
     switch (rw) {
         case 1: return launch_stream_rw<MR, 1, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
-        case 2: return launch_stream_rw<MR, 2, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+        case 2:
+            if constexpr (rmax >= 2)
+                return launch_stream_rw<MR, 2, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+            return 0;
         // (3 and 4 words per thread: the single-matrix launches of one row)
         case 3:
             if constexpr (rmax >= 3 && !PAIR)
@@ -697,11 +703,17 @@ int try_fused(const MatList& ml, const float* x, int n_in, int gs, hipStream_t s
     return launch_stream<MR>(ml, x, n_in, st);
 }
 
+// m rows run in the instance of the next power of two (3 -> 4, 5..7 -> 8),
+// the missing rows reading 0 and not stored.
 int try_fused_m(const MatList& ml, const float* x, int m, int n_in, int gs, hipStream_t st) {
+    MatList mm = ml;
+    mm.mrows = m;
     switch (m) {
-        case 1: return try_fused<1>(ml, x, n_in, gs, st);
-        case 2: return try_fused<2>(ml, x, n_in, gs, st);
-        default: return 0;      // 3..8 rows: split path (the streaming kernel would spill)
+        case 1: return try_fused<1>(mm, x, n_in, gs, st);
+        case 2: return try_fused<2>(mm, x, n_in, gs, st);
+        case 3: case 4: return try_fused<4>(mm, x, n_in, gs, st);
+        case 5: case 6: case 7: case 8: return try_fused<8>(mm, x, n_in, gs, st);
+        default: return 0;
     }
 }
 
@@ -1099,8 +1111,8 @@ int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const ui
     if ((reinterpret_cast<uintptr_t>(gate_w) | reinterpret_cast<uintptr_t>(up_w)) & 15)
         return fail(Q4_EARG, "w must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    for (int m0 = 0; m0 < m; m0 += 2) {
-        const int mm = m - m0 < 2 ? m - m0 : 2;
+    for (int m0 = 0; m0 < m; m0 += kMaxM) {
+        const int mm = m - m0 < kMaxM ? m - m0 : kMaxM;
         const float* xm = x + static_cast<size_t>(m0) * n_in;
         float* hm = h + static_cast<size_t>(m0) * n_inter;
         MatList ml{};
@@ -1112,11 +1124,14 @@ int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const ui
         ml.row_begin[0] = 0;
         for (int k = 0; k < kMaxMats; k++) ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
         ml.count = 2;
+        ml.mrows = mm;
         int done = 0;
         if (gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
             (n_in / 8 + kChunkWords - 1) / kChunkWords <= 16) {
-            done = mm == 1 ? launch_stream<1, true>(ml, xm, n_in, st)
-                           : launch_stream<2, true>(ml, xm, n_in, st);
+            done = mm == 1   ? launch_stream<1, true>(ml, xm, n_in, st)
+                   : mm == 2 ? launch_stream<2, true>(ml, xm, n_in, st)
+                   : mm <= 4 ? launch_stream<4, true>(ml, xm, n_in, st)
+                             : launch_stream<8, true>(ml, xm, n_in, st);
             if (done < 0) return done;
         }
         if (!done) {        // unfused: gate into h, up into the workspace, then SiLU * mul
@@ -1161,6 +1176,7 @@ int q4_norm_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
         ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
     }
     ml.count = count;
+    ml.mrows = 1;
     if (ml.row_begin[count] == 0) return fail(Q4_EARG, "q4_norm_gemv_multi_dev: no output rows");
     const NormArgs na{delta, norm_w, x_out, eps};
     rc = launch_stream<1, false, true>(ml, x, n_in, static_cast<hipStream_t>(stream), na);
@@ -1189,6 +1205,7 @@ int q4_norm_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, con
     ml.row_begin[0] = 0;
     for (int k = 0; k < kMaxMats; k++) ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
     ml.count = 2;
+    ml.mrows = 1;
     const NormArgs na{delta, norm_w, x_out, eps};
     rc = launch_stream<1, true, true>(ml, x, n_in, static_cast<hipStream_t>(stream), na);
     if (rc == 0) return fail(Q4_EARG, "q4_norm_gate_up_silu_dev: n_in = %d does not fit the norm prologue", n_in);

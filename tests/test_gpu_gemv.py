@@ -200,7 +200,8 @@ def test_multi_dev_grouped(lib):
     o = oracle.Oracle()
     for m, shapes in ((1, [(3584, 3584), (3584, 512), (3584, 512)]),
                       (2, [(1024, 1536), (1024, 2560)]),
-                      (4, [(2048, 96), (2048, 64), (2048, 8), (2048, 40)])):
+                      (4, [(2048, 96), (2048, 64), (2048, 8), (2048, 40)]),
+                      (3, [(3584, 512), (3584, 128)]), (6, [(1024, 200)]), (8, [(3584, 512), (3584, 256)])):
         k_in = shapes[0][0]
         print(f"multi m={m} shapes={shapes}", flush=True)
         mats_np = [synth.qlinear(300 + i, n, k_in, 64) for i, (_, n) in enumerate(shapes)]

@@ -34,8 +34,9 @@ def mats(seed, n_out, n_in):
     return (w, s, b), tuple(tensors(w, s.view(np.int16), b.view(np.int16)))
 
 
-@pytest.mark.parametrize("hidden,inter,m", [(1024, 2816, 1), (1024, 2816, 2), (1024, 2816, 3),
-                                            (3584, 18944, 1), (3584, 18944, 2)])
+@pytest.mark.parametrize("hidden,inter,m", [(1024, 2816, 1), (1024, 2816, 2), (1024, 2816, 3), (1024, 2816, 5),
+                                            (1024, 2816, 8), (3584, 18944, 1), (3584, 18944, 2),
+                                            (3584, 18944, 4), (3584, 18944, 8)])
 def test_gate_up_silu_and_mlp(hidden, inter, m):
     import torch
     print(f"mlp hidden={hidden} inter={inter} m={m}", flush=True)
