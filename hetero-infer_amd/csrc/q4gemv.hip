@@ -34,6 +34,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <type_traits>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -389,73 +390,111 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
 }
 
-template <int BM, int BN>
+// x rounded to bf16 (RNE) once per call, 8 values per thread.
+__global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict__ x, uint4* __restrict__ xb,
+                                                        long n8) {
+    const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n8) {
+        const float4 a = reinterpret_cast<const float4*>(x)[2 * i], b = reinterpret_cast<const float4*>(x)[2 * i + 1];
+        uint4 o;
+        o.x = pack_bf16x2(a.x, a.y);
+        o.y = pack_bf16x2(a.z, a.w);
+        o.z = pack_bf16x2(b.x, b.y);
+        o.w = pack_bf16x2(b.z, b.w);
+        xb[i] = o;
+    }
+}
+
+// Prefill GEMM: out[M][N] = bf16(x)[M][K] . bf16(dequant W)[N][K]^T, fp32
+// accumulation on v_mfma_f32_32x32x16_bf16.  Tile BM x BN x 64 (one group
+// of K per step, so each B row has one scale/bias pair per step); 4 waves
+// (2 x 2), each (BM/2) x (BN/2).  A is the bf16 copy of x; B is dequantised
+// while it is stored to LDS (v_cvt_f32_ubyte -> fma with the fp16
+// scale/bias -> RNE to bf16: the value of q4_dequant_bf16_dev).
+// Pipeline: D register slots of loads in flight (step k + D is issued while
+// step k is multiplied), LDS double-buffered; every load goes through a
+// buffer resource bounded to the tile's rows, so rows past M or N and steps
+// past the workgroup's K range read 0 and cost no access.  Split-K:
+// blockIdx.z takes steps [z*kt_split, (z+1)*kt_split) and writes its
+// partial sums to out + z*M*N.
+template <int BM, int BN, int D>
 __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
-    const float* __restrict__ x, const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
-    const uint16_t* __restrict__ bi, float* __restrict__ out, int M, int N, int K) {
+    const uint16_t* __restrict__ xb, const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
+    const uint16_t* __restrict__ bi, float* __restrict__ out, int M, int N, int K, int kt_split) {
+    static_assert(D % 2 == 0, "the LDS buffer of a step is its slot parity");
     extern __shared__ uint4 gemm_lds[];
     uint16_t* As = reinterpret_cast<uint16_t*>(gemm_lds);          // [2][BM][72]
     uint16_t* Bs = As + 2 * BM * kGemmLdsK;                        // [2][BN][72]
     constexpr int TM = BM / 64, TN = BN / 64;                      // 32x32 tiles per wave
-    constexpr int A_PER = BM * 16 / 256;                           // float4 of x per thread
-    constexpr int B_PER = BN * 2 / 256;                            // uint4 of w per thread (may be < 1)
+    constexpr int A_PER = BM * 8 / 256;                            // uint4 (8 bf16) of x per thread and step
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int G = K >> 6, wpr = K >> 3;
+    const int kt0 = blockIdx.z * kt_split;
+    const int nk = G - kt0 < kt_split ? G - kt0 : kt_split;
+    const int mrows = M - m0 < BM ? M - m0 : BM, nrows = N - n0 < BN ? N - n0 : BN;
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(xb + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows * K) * 2u);
+    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(w + static_cast<size_t>(n0) * wpr, static_cast<uint32_t>(nrows * wpr) * 4u);
+    const __amdgpu_buffer_rsrc_t sr = buf_rsrc(sc + static_cast<size_t>(n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
+    const __amdgpu_buffer_rsrc_t br = buf_rsrc(bi + static_cast<size_t>(n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
+    // B: 256 / BN threads per row, WPT words (8 nibbles each) per thread
+    constexpr int QPR = 256 / BN, WPT = 8 / QPR;
+    static_assert(WPT == 4 || WPT == 2, "BN is 64 or 128");
+    const int brow = tid / QPR, bq = tid % QPR;
+    using BVec = typename std::conditional<WPT == 4, uint4, uint2>::type;
 
-    float4 ra[A_PER];
-    uint4 rb[B_PER > 0 ? B_PER : 1];
-    uint16_t rs[B_PER > 0 ? B_PER : 1], rbb[B_PER > 0 ? B_PER : 1];
-    auto gload = [&](int kt) {
+    uint4 ra[D][A_PER];
+    BVec rb[D];
+    uint16_t rs[D], rbb[D];
+    // issue the loads of step `it` (relative to kt0) into slot j
+    auto load = [&](uint4 (&a)[A_PER], BVec& bw, uint16_t& s16, uint16_t& b16, int it) {
+        const bool live = it < nk;
+        const int kt = kt0 + it;
 #pragma unroll
         for (int i = 0; i < A_PER; i++) {
-            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
-            const int gm = m0 + row < M ? m0 + row : M - 1;
-            ra[i] = reinterpret_cast<const float4*>(x + static_cast<size_t>(gm) * K + 64 * kt)[c4];
+            const int idx = tid + 256 * i, row = idx >> 3, c = idx & 7;
+            const uint32_t off = live ? static_cast<uint32_t>(row * K + kt * 64 + c * 8) * 2u : kOutOfRange;
+            a[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
         }
-#pragma unroll
-        for (int i = 0; i < (B_PER > 0 ? B_PER : 1); i++) {
-            const int idx = tid + 256 * i, row = idx >> 1, half = idx & 1;
-            if (B_PER > 0 || row < BN) {
-                const int gn = n0 + row < N ? n0 + row : N - 1;
-                rb[i] = *reinterpret_cast<const uint4*>(w + static_cast<size_t>(gn) * wpr + 8 * kt + 4 * half);
-                rs[i] = sc[static_cast<size_t>(gn) * G + kt];
-                rbb[i] = bi[static_cast<size_t>(gn) * G + kt];
-            }
-        }
+        const uint32_t wo = live ? static_cast<uint32_t>(brow * wpr + kt * 8 + bq * WPT) * 4u : kOutOfRange;
+        const uint32_t go = live ? static_cast<uint32_t>(brow * G + kt) * 2u : kOutOfRange;
+        if constexpr (WPT == 4)
+            bw = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2));
+        else
+            bw = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
+        s16 = __builtin_amdgcn_raw_buffer_load_b16(sr, go, 0, 0);
+        b16 = __builtin_amdgcn_raw_buffer_load_b16(br, go, 0, 0);
     };
-    auto lstore = [&](int buf) {
+    auto store = [&](const uint4 (&a)[A_PER], const BVec& bw, uint16_t s16, uint16_t b16, int buf) {
 #pragma unroll
         for (int i = 0; i < A_PER; i++) {
-            const int idx = tid + 256 * i, row = idx >> 4, c4 = idx & 15;
-            uint2 v;
-            v.x = pack_bf16x2(ra[i].x, ra[i].y);
-            v.y = pack_bf16x2(ra[i].z, ra[i].w);
-            *reinterpret_cast<uint2*>(As + (buf * BM + row) * kGemmLdsK + 4 * c4) = v;
+            const int idx = tid + 256 * i, row = idx >> 3, c = idx & 7;
+            *reinterpret_cast<uint4*>(As + (buf * BM + row) * kGemmLdsK + 8 * c) = a[i];
         }
+        {
+            const float sf = h2f(s16), bf = h2f(b16);
+            uint32_t wd[WPT];
+            if constexpr (WPT == 4) {
+                wd[0] = bw.x; wd[1] = bw.y; wd[2] = bw.z; wd[3] = bw.w;
+            } else {
+                wd[0] = bw.x; wd[1] = bw.y;
+            }
 #pragma unroll
-        for (int i = 0; i < (B_PER > 0 ? B_PER : 1); i++) {
-            const int idx = tid + 256 * i, row = idx >> 1, half = idx & 1;
-            if (B_PER > 0 || row < BN) {
-                const float s = h2f(rs[i]), b = h2f(rbb[i]);
-                const uint32_t wd[4] = {rb[i].x, rb[i].y, rb[i].z, rb[i].w};
+            for (int t = 0; t < WPT; t++) {
+                // even values in the bytes of lo, odd ones in hi; v_cvt_f32_ubyteN
+                // turns each byte into a float in one instruction
+                const uint32_t lo = wd[t] & 0x0F0F0F0Fu, hi = (wd[t] >> 4) & 0x0F0F0F0Fu;
+                float v[8];
 #pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    // even values in the bytes of lo, odd ones in hi; v_cvt_f32_ubyteN
-                    // turns each byte into a float in one instruction
-                    const uint32_t lo = wd[t] & 0x0F0F0F0Fu, hi = (wd[t] >> 4) & 0x0F0F0F0Fu;
-                    float v[8];
-#pragma unroll
-                    for (int n = 0; n < 4; n++) {
-                        v[2 * n] = __builtin_fmaf(static_cast<float>((lo >> (8 * n)) & 0xFFu), s, b);
-                        v[2 * n + 1] = __builtin_fmaf(static_cast<float>((hi >> (8 * n)) & 0xFFu), s, b);
-                    }
-                    uint4 pk;
-                    pk.x = pack_bf16x2(v[0], v[1]); pk.y = pack_bf16x2(v[2], v[3]);
-                    pk.z = pack_bf16x2(v[4], v[5]); pk.w = pack_bf16x2(v[6], v[7]);
-                    *reinterpret_cast<uint4*>(Bs + (buf * BN + row) * kGemmLdsK + 32 * half + 8 * t) = pk;
+                for (int n = 0; n < 4; n++) {
+                    v[2 * n] = __builtin_fmaf(static_cast<float>((lo >> (8 * n)) & 0xFFu), sf, bf);
+                    v[2 * n + 1] = __builtin_fmaf(static_cast<float>((hi >> (8 * n)) & 0xFFu), sf, bf);
                 }
+                uint4 pk;
+                pk.x = pack_bf16x2(v[0], v[1]); pk.y = pack_bf16x2(v[2], v[3]);
+                pk.z = pack_bf16x2(v[4], v[5]); pk.w = pack_bf16x2(v[6], v[7]);
+                *reinterpret_cast<uint4*>(Bs + (buf * BN + brow) * kGemmLdsK + 8 * WPT * bq + 8 * t) = pk;
             }
         }
     };
@@ -468,35 +507,50 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
 
-    gload(0);
-    lstore(0);
+#pragma unroll
+    for (int j = 0; j < D; j++) load(ra[j], rb[j], rs[j], rbb[j], j);
+    store(ra[0], rb[0], rs[0], rbb[0], 0);
     __syncthreads();
-    for (int kt = 0; kt < G; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < G) gload(kt + 1);
+    const int ngroups = (nk + D - 1) / D;
+    for (int g = 0; g < ngroups; g++) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            bf16x8 a[TM], bv[TN];
+        for (int j = 0; j < D; j++) {
+            const int it = g * D + j;
+            const int cur = j & 1;
+            // slot j held step `it` (already in LDS): refill it with step it + D.
+            // Steps past the K range multiply zeros (their loads read 0), so
+            // the multiply needs no branch.
+            load(ra[j], rb[j], rs[j], rbb[j], it + D);
+            {
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int row = wm * (BM / 2) + i * 32 + (lane & 31);
-                a[i] = *reinterpret_cast<const bf16x8*>(As + (cur * BM + row) * kGemmLdsK + 16 * ks + 8 * (lane >> 5));
+                for (int ks = 0; ks < 4; ks++) {
+                    bf16x8 av[TM], bv[TN];
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        const int row = wm * (BM / 2) + i * 32 + (lane & 31);
+                        av[i] = *reinterpret_cast<const bf16x8*>(As + (cur * BM + row) * kGemmLdsK + 16 * ks +
+                                                                 8 * (lane >> 5));
+                    }
+#pragma unroll
+                    for (int jj = 0; jj < TN; jj++) {
+                        const int row = wn * (BN / 2) + jj * 32 + (lane & 31);
+                        bv[jj] = *reinterpret_cast<const bf16x8*>(Bs + (cur * BN + row) * kGemmLdsK + 16 * ks +
+                                                                  8 * (lane >> 5));
+                    }
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int jj = 0; jj < TN; jj++)
+                            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[jj], acc[i][jj], 0, 0, 0);
+                }
             }
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int row = wn * (BN / 2) + j * 32 + (lane & 31);
-                bv[j] = *reinterpret_cast<const bf16x8*>(Bs + (cur * BN + row) * kGemmLdsK + 16 * ks + 8 * (lane >> 5));
-            }
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bv[j], acc[i][j], 0, 0, 0);
+            // the next step, loaded D - 1 steps ago, into the other buffer
+            store(ra[(j + 1) % D], rb[(j + 1) % D], rs[(j + 1) % D], rbb[(j + 1) % D], cur ^ 1);
+            __syncthreads();
         }
-        if (kt + 1 < G) lstore(cur ^ 1);
-        __syncthreads();
     }
     // C tile layout: lane l, register v holds row 8*(v/4) + 4*(l/32) + v%4, column l%32
+    float* o = out + static_cast<size_t>(blockIdx.z) * M * N;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -505,8 +559,19 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
             for (int v = 0; v < 16; v++) {
                 const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
-                if (row < M && col < N) out[static_cast<size_t>(row) * N + col] = acc[i][j][v];
+                if (row < M && col < N) o[static_cast<size_t>(row) * N + col] = acc[i][j][v];
             }
+}
+
+// out = sum over the S split-K partials, in split order.
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                         long n, int S) {
+    const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) {
+        float a = part[i];
+        for (int s = 1; s < S; s++) a = __fadd_rn(a, part[static_cast<long>(s) * n + i]);
+        out[i] = a;
+    }
 }
 
 // ============================================================ host side ===
@@ -531,7 +596,28 @@ struct Workspace {
     size_t cap_words = 0, cap_groups = 0;
     float* tmp = nullptr;                       // up-projection rows of the unfused MLP
     size_t cap_tmp = 0;
+    void* xbf = nullptr;                        // prefill: bf16 copy of x
+    size_t cap_xbf = 0;
+    void* part = nullptr;                       // prefill: split-K partial sums
+    size_t cap_part = 0;
 };
+
+// Grow one raw workspace buffer (bytes), outside graph capture.
+int ensure_raw(void*& p, size_t& cap, size_t bytes, hipStream_t st, const char* what) {
+    if (bytes <= cap && p) return 0;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(Q4_EARG, "%s workspace of this stream must grow during graph capture: "
+                             "run the largest call once on the stream before capturing", what);
+    HIP_TRY(hipStreamSynchronize(st));
+    (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    HIP_TRY(hipMalloc(&p, bytes));
+    cap = bytes;
+    return 0;
+}
 
 int ensure_tmp(Workspace& ws, hipStream_t st, size_t n) {
     if (n <= ws.cap_tmp && ws.tmp) return 0;
@@ -916,9 +1002,10 @@ int dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, void
 
 
 template <int BM, int BN>
-int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x, float* out,
-                int M, int N, int K, hipStream_t st) {
-    auto kern = gemm_q4_bf16_kernel<BM, BN>;
+int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* xb, float* out,
+                int M, int N, int K, int S, int kt_split, hipStream_t st) {
+    constexpr int D = 4;                 // steps in flight
+    auto kern = gemm_q4_bf16_kernel<BM, BN, D>;
     const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
     static bool attr_set = false;
     if (!attr_set) {
@@ -927,8 +1014,8 @@ int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const f
         if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
         attr_set = true;
     }
-    dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN);
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, x, w, s, b, out, M, N, K);
+    dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN, S);
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, xb, w, s, b, out, M, N, K, kt_split);
     HIP_TRY(hipGetLastError());
     return 0;
 }
@@ -1243,10 +1330,41 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
         HIP_TRY(hipGetLastError());
         return 0;
     }
-    // 128 x 128 tiles once there are enough of them for the CUs, else 128 x 64
+    Workspace* ws;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        int dev;
+        if ((rc = current_device(&dev))) return rc;
+        ws = &g_dev[dev].ws[st];
+    }
+    // tiles: 128 x 128 once they fill the CUs, else 128 x 64; split K in
+    // two while the workgroups do not fill the CUs twice and every split
+    // keeps at least 8 groups of K
+    const int cus = num_cus();
     const long tiles128 = static_cast<long>((m + 127) / 128) * ((n_out + 127) / 128);
-    if (tiles128 >= 2L * num_cus()) return launch_gemm<128, 128>(w, scales, biases, x, out, m, n_out, n_in, st);
-    return launch_gemm<128, 64>(w, scales, biases, x, out, m, n_out, n_in, st);
+    const int BN = tiles128 >= cus ? 128 : 64;
+    const long tiles = static_cast<long>((m + 127) / 128) * ((n_out + BN - 1) / BN);
+    const int G = n_in / 64;
+    int S = 1;
+    while (S < 8 && tiles * S < 2L * cus && G / (2 * S) >= 8) S *= 2;
+    const int kt_split = (G + S - 1) / S;
+    S = (G + kt_split - 1) / kt_split;
+    const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * n_out;
+    if ((rc = ensure_raw(ws->xbf, ws->cap_xbf, mk * 2, st, "prefill"))) return rc;
+    if (S > 1 && (rc = ensure_raw(ws->part, ws->cap_part, S * mn * 4, st, "prefill"))) return rc;
+    const long n8 = static_cast<long>(mk / 8);
+    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, st, x,
+                       static_cast<uint4*>(ws->xbf), n8);
+    HIP_TRY(hipGetLastError());
+    const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
+    float* dst = S > 1 ? static_cast<float*>(ws->part) : out;
+    rc = BN == 128 ? launch_gemm<128, 128>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st)
+                   : launch_gemm<128, 64>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st);
+    if (rc || S == 1) return rc;
+    hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const float*>(ws->part), out, static_cast<long>(mn), S);
+    HIP_TRY(hipGetLastError());
+    return 0;
 }
 
 int q4_dequant_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,

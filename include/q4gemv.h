@@ -120,7 +120,10 @@ int q4_mlp_dev(const uint32_t *gate_w, const uint16_t *gate_s, const uint16_t *g
  * cores (v_mfma_f32_32x32x16_bf16).  Replaces QLinear._gemm,
  * hetero/cpu_model.py:119-136 (512-row q4_dequant blocks + an fp32 BLAS
  * sgemm); the result differs from it by bf16 rounding of both operands.
- * gs must be 64; w and x 16-byte aligned. */
+ * gs must be 64; w and x 16-byte aligned.  Uses a per-stream workspace (the
+ * bf16 copy of x and, when K is split over workgroups, the partial sums)
+ * that grows on first use: run the largest call once on a stream before
+ * capturing it in a graph. */
 int q4_gemm_bf16_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
                      const float *x, float *out, int m, int n_out, int n_in, int gs,
                      void *stream);
