@@ -112,10 +112,25 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
         torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
     tf = flops / (ms * 1e-3) / 1e12
+    # error vs the reference contraction, fp32 dequant-matmul (hetero/cpu_model.py:119-136), on
+    # each projection shape of layer 0: max |err| / max |ref| and norm-wise
+    errs = {}
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for (name, n_in, n_out), (w, s, b) in zip(LAYER_SHAPES, layers[0]):
+        got = q4.gemm_bf16_dev(w, s, b, xs[n_in], lib=lib)
+        ref = xs[n_in] @ q4.dequant_dev(w, s, b, lib=lib).t()
+        d = (got - ref).double()
+        errs[name] = {"max_rel": float(d.abs().max() / ref.double().abs().max()),
+                      "normwise_rel": float(d.norm() / ref.double().norm())}
+    torch.backends.cuda.matmul.allow_tf32 = prev
+    worst = max(v["max_rel"] for v in errs.values())
     return {"workload": "M=512 prompt, 28 layers x 7 projections (K/N of the decode sweep), "
                         "group-64 dequant to bf16 fused into the weight-tile load, MFMA GEMM",
             "ms": round(ms, 3), "tflops": round(tf, 1), "frac_mfma_peak": round(tf / 2500.0, 4),
-            "peak_tflops_bf16_dense": 2500.0, "flops": flops}
+            "peak_tflops_bf16_dense": 2500.0, "flops": flops,
+            "max_rel_err_vs_fp32_dequant_matmul": round(worst, 6),
+            "err_per_shape": {k: {kk: round(vv, 7) for kk, vv in v.items()} for k, v in errs.items()}}
 
 
 def small_m_bench(torch, lib, layers, dev, ms=(1, 2, 4, 8), reps=5):
@@ -369,6 +384,8 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--sweep-only", action="store_true",
                     help="only the grouped decode sweep (for rocprof runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the M=512 prefill leg (for counter runs)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode step (for rocprof runs)")
     ap.add_argument("--no-decode-check", action="store_true",
@@ -395,6 +412,9 @@ def main():
     t_setup = time.perf_counter()
     layers = [[make_weights(torch, gen, n_out, n_in, dev) for _, n_in, n_out in LAYER_SHAPES]
               for _ in range(LAYERS)]
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_bench(torch, lib, layers, dev)}), flush=True)
+        return
     head = make_weights(torch, gen, HEAD_SHAPE[2], HEAD_SHAPE[1], dev)
     xs = {k: torch.randn((1, k), device=dev, generator=gen) for k in (3584, 18944)}
     outs = {n: torch.empty((1, n), device=dev) for n in (512, 3584, 18944, 152064)}
