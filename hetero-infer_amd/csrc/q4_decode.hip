@@ -415,46 +415,68 @@ void launch_partial(int G, dim3 grid, hipStream_t st, const float* q, uint16_t* 
 }
 
 // one workgroup per query head: M = max_c m_c, w_c = e^(m_c - M),
-// o = sum_c w_c o_c / sum_c w_c l_c
+// o = sum_c w_c o_c / sum_c w_c l_c.  Every load is issued before the
+// first reduction: m and l of chunk c by thread c (c + 256, ...), and thread
+// (part k, dim i) prefetches o[i] of its chunks k, k + nparts, ... (nparts =
+// 256 / d) -- one round of memory latency instead of three.
 __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            int n_chunks, int d) {
     __shared__ float w_s[kMaxChunks];
     __shared__ float red[8];
     const int h = blockIdx.x, tid = threadIdx.x, nt = blockDim.x;
     const int stride = d + 2;
-    const float* base = part + static_cast<size_t>(h) * n_chunks * stride;
-    float mloc = -__builtin_inff();
-    for (int c = tid; c < n_chunks; c += nt) {
-        const float m = base[static_cast<size_t>(c) * stride];
-        w_s[c] = m;
-        mloc = fmaxf(mloc, m);
+    const int i = tid % d, part_k = tid / d;
+    const int nparts = nt / d;
+    const __amdgpu_buffer_rsrc_t pr = buf_rsrc(part + static_cast<size_t>(h) * n_chunks * stride,
+                                               static_cast<uint32_t>(n_chunks * stride) * 4u);
+    auto ld = [&](int c, int k) {                 // element k of chunk c (0 past the last chunk)
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             pr, static_cast<uint32_t>(c * stride + k) * 4u, 0, 0));
+    };
+    constexpr int kPre = 32;                      // o values prefetched per thread
+    float ob[kPre];
+#pragma unroll
+    for (int j = 0; j < kPre; j++) ob[j] = ld(part_k + j * nparts, 2 + i);
+    constexpr int kMl = kMaxChunks / 256;         // chunks per thread for m and l
+    float mv[kMl], lv[kMl];
+#pragma unroll
+    for (int r = 0; r < kMl; r++) {
+        mv[r] = ld(tid + 256 * r, 0);
+        lv[r] = ld(tid + 256 * r, 1);
     }
+    float mloc = -__builtin_inff();
+#pragma unroll
+    for (int r = 0; r < kMl; r++)
+        if (tid + 256 * r < n_chunks) mloc = fmaxf(mloc, mv[r]);
     mloc = wave_max(mloc);
     if ((tid & 63) == 0) red[tid >> 6] = mloc;
     __syncthreads();
     float M = -__builtin_inff();
-    for (int i = 0; i < (nt >> 6); i++) M = fmaxf(M, red[i]);
+    for (int k = 0; k < (nt >> 6); k++) M = fmaxf(M, red[k]);
     __syncthreads();
     float lloc = 0.0f;
-    for (int c = tid; c < n_chunks; c += nt) {
-        const float m = w_s[c];
-        const float wgt = m == -__builtin_inff() ? 0.0f : expf(__fsub_rn(m, M));
-        w_s[c] = wgt;
-        lloc = __builtin_fmaf(base[static_cast<size_t>(c) * stride + 1], wgt, lloc);
+#pragma unroll
+    for (int r = 0; r < kMl; r++) {
+        const int c = tid + 256 * r;
+        if (c < n_chunks) {
+            const float wgt = mv[r] == -__builtin_inff() ? 0.0f : expf(__fsub_rn(mv[r], M));
+            w_s[c] = wgt;
+            lloc = __builtin_fmaf(lv[r], wgt, lloc);
+        }
     }
     lloc = wave_sum(lloc);
     if ((tid & 63) == 0) red[tid >> 6] = lloc;
     __syncthreads();
     float L = 0.0f;
-    for (int i = 0; i < (nt >> 6); i++) L = __fadd_rn(L, red[i]);
-    // threads (part, dim): part k of nparts takes chunks k, k + nparts, ...;
-    // the parts are then added in order (d divides the 256 threads)
-    const int i = tid % d, part_k = tid / d;
-    const int nparts = nt / d;
+    for (int k = 0; k < (nt >> 6); k++) L = __fadd_rn(L, red[k]);
+    // the part's chunks in order: the prefetched ones, then any past them
     float O = 0.0f;
-#pragma unroll 16
-    for (int c = part_k; c < n_chunks; c += nparts)
-        O = __builtin_fmaf(base[static_cast<size_t>(c) * stride + 2 + i], w_s[c], O);
+#pragma unroll
+    for (int j = 0; j < kPre; j++) {
+        const int c = part_k + j * nparts;
+        if (c < n_chunks) O = __builtin_fmaf(ob[j], w_s[c], O);
+    }
+    for (int c = part_k + kPre * nparts; c < n_chunks; c += nparts) O = __builtin_fmaf(ld(c, 2 + i), w_s[c], O);
     __syncthreads();
     float* o_s = w_s;                                        // the weights are no longer read
     o_s[part_k * d + i] = O;
