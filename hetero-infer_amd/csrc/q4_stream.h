@@ -101,6 +101,12 @@ __device__ __forceinline__ uint64_t sel4(int p, uint64_t a0, uint64_t a1, uint64
     return r;
 }
 __device__ __forceinline__ int sel4(int p, int a0, int a1, int a2, int a3) {
+    // the operands are uniform; readfirstlane keeps them in SGPRs where the
+    // compiler would otherwise hold a loop-invariant copy in a VGPR
+    a0 = __builtin_amdgcn_readfirstlane(a0);
+    a1 = __builtin_amdgcn_readfirstlane(a1);
+    a2 = __builtin_amdgcn_readfirstlane(a2);
+    a3 = __builtin_amdgcn_readfirstlane(a3);
     int r;
     asm volatile(
         "s_cmp_eq_u32 %1, 1\n\t"
@@ -125,30 +131,61 @@ struct Item {
 };
 
 
-// Issue the loads of item (chunk c, row slot r) of unit `unit`.  The row is
-// wave-uniform: each array gets a resource over that row alone, so lanes
-// past the row end read 0 and cost no memory access, and `live` false (a
-// prefetch past the wave's last item) gives an empty resource: every lane
-// reads 0.  No branch, so the waits on earlier loads stay exact.
+// The rows of the unit the prefetch cursor is in: its matrix's w/s/b
+// advanced to the unit's first row (PAIR: index 1 holds the same rows of
+// matrix 1).  Resolved once per unit -- the host picks UB dividing every
+// n_out, so a unit never straddles two matrices -- and wave-uniform, so an
+// item's loads only add the row slot to scalar pointers.
+struct UnitRows {
+    const uint32_t* w[2];
+    const uint16_t* s[2];
+    const uint16_t* b[2];
+};
+
 template <bool PAIR>
-__device__ __forceinline__ void load_item(Item& it, const MatList& ml, int unit, int c, int r, int UB,
-                                          int n_total, int wpr, int G, int lane, bool live) {
+__device__ __forceinline__ void unit_rows(UnitRows& ur, const MatList& ml, int unit, int UB, int wpr, int G) {
+    const int gr = unit * UB;
+    if constexpr (PAIR) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            ur.w[k] = ml.w[k] + static_cast<size_t>(gr) * wpr;
+            ur.s[k] = ml.s[k] + static_cast<size_t>(gr) * G;
+            ur.b[k] = ml.b[k] + static_cast<size_t>(gr) * G;
+        }
+    } else {
+        // p is wave-uniform; readfirstlane makes that explicit, so the
+        // kernel-argument reads are scalar loads
+        const int p = __builtin_amdgcn_readfirstlane(mat_of_row(ml, gr));
+        const int o = __builtin_amdgcn_readfirstlane(
+            gr - sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2], ml.row_begin[3]));
+        ur.w[0] = pick(ml.w, p) + static_cast<size_t>(o) * wpr;
+        ur.s[0] = pick(ml.s, p) + static_cast<size_t>(o) * G;
+        ur.b[0] = pick(ml.b, p) + static_cast<size_t>(o) * G;
+    }
+}
+
+// Issue the loads of item (chunk c, row slot r) of the unit whose rows `ur`
+// holds.  The row is wave-uniform: each array gets a resource over that row
+// alone, so lanes past the row end read 0 and cost no memory access, and
+// `live` false (a prefetch past the wave's last item) gives an empty
+// resource: every lane reads 0.  No branch, so the waits on earlier loads
+// stay exact.
+template <bool PAIR>
+__device__ __forceinline__ void load_item(Item& it, const UnitRows& ur, int unit, int c, int r, int UB,
+                                          int wpr, int G, int lane, bool live) {
     it.unit = unit;
-    const int u = PAIR ? (r < UB ? r : r - UB) : r;
-    int gr = unit * UB + u;
-    gr = gr < n_total ? gr : n_total - 1;
-    // p is wave-uniform; readfirstlane makes that explicit, so the
-    // kernel-argument reads below are scalar loads
-    const int p = __builtin_amdgcn_readfirstlane(PAIR ? (r < UB ? 0 : 1) : mat_of_row(ml, gr));
-    const int o = __builtin_amdgcn_readfirstlane(
-        PAIR ? gr : gr - sel4(p, ml.row_begin[0], ml.row_begin[1], ml.row_begin[2], ml.row_begin[3]));
+    const bool second = PAIR && r >= UB;
+    const int u = second ? r - UB : r;
+    const uint32_t* wp = second ? ur.w[1] : ur.w[0];
+    const uint16_t* sp = second ? ur.s[1] : ur.s[0];
+    const uint16_t* bp = second ? ur.b[1] : ur.b[0];
     const uint32_t wbytes = live ? static_cast<uint32_t>(wpr) * 4u : 0u;
     const uint32_t gbytes = live ? static_cast<uint32_t>(G) * 2u : 0u;
     const int word0 = c * kChunkWords + lane * 4;
     const int go = (word0 >> 3) * 2;
-    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(pick(ml.w, p) + static_cast<size_t>(o) * wpr, wbytes);
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(pick(ml.s, p) + static_cast<size_t>(o) * G, gbytes);
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(pick(ml.b, p) + static_cast<size_t>(o) * G, gbytes);
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wp + static_cast<size_t>(u) * wpr, wbytes);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(sp + static_cast<size_t>(u) * G, gbytes);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(bp + static_cast<size_t>(u) * G, gbytes);
     // the three loads in a fixed order wherever an item is loaded: the
     // partial waits on the ring are computed from the issue order, which
     // must then be the same on entry to the main loop as around it.  The
@@ -282,9 +319,11 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     constexpr int kE = RING < kEarly ? RING : kEarly;
     Item ring[RING];
     int pf_unit = first_unit, pf_c = 0, pf_r = 0;                 // prefetch cursor (uniform)
+    UnitRows pf_rows;
+    unit_rows<PAIR>(pf_rows, ml, pf_unit, UB, wpr, G);
 #pragma unroll
     for (int d = 0; d < kE; d++) {
-        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, has_work);
+        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, lane, has_work);
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
 
@@ -372,7 +411,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     }
 #pragma unroll
     for (int d = kE; d < RING; d++) {
-        load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, has_work);
+        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, lane, has_work);
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
     if (tid == 0) *claim_ctr = 0;
@@ -523,6 +562,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
             const int u = blockIdx.x + __builtin_amdgcn_readfirstlane(claimed) * grid;
             if (u >= n_units) return false;
             pf_unit = u;
+            unit_rows<PAIR>(pf_rows, ml, pf_unit, UB, wpr, G);
             pf_c = 0;
             pf_r = 0;
             cyc_pf = 0;
@@ -539,7 +579,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
                 // the refill may not be scheduled above the consume of its
                 // slot, so that the slot keeps its registers
                 __builtin_amdgcn_sched_barrier(0);
-                load_item<PAIR>(ring[d], ml, pf_unit, pf_c, pf_r, UB, n_total, wpr, G, lane, true);
+                load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, lane, true);
                 if (++pf_r == NU) { pf_r = 0; ++pf_c; }
             }
             ++cyc_pf;
