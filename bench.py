@@ -183,6 +183,88 @@ def small_m_bench(torch, lib, layers, dev, ms=(1, 2, 4, 8), reps=5):
                         "SiLU*mul, down 18944->3584), 28 layers of distinct weights, HIP graph", "rows": res}
 
 
+def wire_bench(torch, lib, dev, rows_list=(1, 256, 2048), hidden=3584, reps=5):
+    """Activation wire codec (include/q4wire.h): encode and decode of an fp32
+    [rows][hidden] hidden state, both codecs.  Distinct input buffers (about
+    600 MB in all, at most 64) are visited in turn inside one HIP graph, so
+    the larger cases stream from HBM.  GB/s counts the fp32 side and the
+    payload once per call."""
+    from hetero import q4
+    res = {}
+    stream = torch.cuda.Stream(device=dev)
+    for rows in rows_list:
+        n = rows * hidden
+        nb = int(min(64, max(2, -(-600_000_000 // (4 * n)))))
+        xs = [torch.randn((rows, hidden), device=dev) for _ in range(nb)]
+        outs = [torch.empty((rows, hidden), device=dev) for _ in range(nb)]
+        row = {}
+        for codec, cid in (("fp16", 0), ("int8", 1)):
+            pb = int(lib.q4_wire_payload_bytes(cid, rows, hidden))
+            pays = [torch.empty(pb, dtype=torch.uint8, device=dev) for _ in range(nb)]
+            st = stream.cuda_stream
+
+            def enc():
+                for x, p in zip(xs, pays):
+                    q4.check(lib, lib.q4_wire_encode_dev(x.data_ptr(), rows, hidden, cid, p.data_ptr(), st), "encode")
+
+            def dec():
+                for p, o in zip(pays, outs):
+                    q4.check(lib, lib.q4_wire_decode_dev(p.data_ptr(), rows, hidden, cid, o.data_ptr(), st), "decode")
+
+            for name, fn in (("encode", enc), ("decode", dec)):
+                with torch.cuda.stream(stream):
+                    fn()
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, stream=stream):
+                    fn()
+                with torch.cuda.stream(stream):
+                    g.replay()
+                    torch.cuda.synchronize()
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    for _ in range(reps):
+                        g.replay()
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / (reps * nb)
+                gbs = (4 * n + pb) / (us * 1e-6) / 1e9
+                row[f"{codec}_{name}"] = {"us_per_call": round(us, 3), "GB_s": round(gbs, 1),
+                                          "frac_peak": round(gbs / HBM_PEAK_GBS, 4), "payload_bytes": pb}
+                del g
+            del pays
+        res[f"rows={rows}"] = row
+        del xs, outs
+    return {"workload": f"fp32 hidden state [rows][{hidden}] ~ N(0,1) -> wire payload and back "
+                        "(hetero/transport.py:198-225 with the NumPy backend's fp16 to_wire/from_wire), "
+                        "distinct buffers per call, HIP graph", "rows": res}
+
+
+def wire_cpu_baseline(rows_list=(1, 256, 2048), hidden=3584, budget_s=2.0):
+    """The oracle's NumPy codec (a restatement of the reference's host
+    encode/decode) on this host, per call, for the rows of wire_bench."""
+    import numpy as np
+    from oracle import wire
+    res = {}
+    rng = np.random.default_rng(0)
+    for rows in rows_list:
+        x = rng.standard_normal((rows, hidden)).astype(np.float32)
+        row = {}
+        for codec in ("fp16", "int8"):
+            h, p = wire.stage_encode(x, codec)
+            for name, fn in (("encode", lambda: wire.stage_encode(x, codec)),
+                             ("decode", lambda: wire.stage_decode(h, p))):
+                fn()
+                k, t0 = 0, time.perf_counter()
+                while time.perf_counter() - t0 < budget_s / (2 * len(rows_list) * 2) or k < 3:
+                    fn()
+                    k += 1
+                row[f"{codec}_{name}"] = {"us_per_call": round((time.perf_counter() - t0) / k * 1e6, 1)}
+        res[f"rows={rows}"] = row
+    return {"kind": "port", "cores": 1, "sample": "oracle/wire.py (NumPy, one thread) on the same shapes",
+            "rows": res}
+
+
 def decode_weights(torch, cfg, dev, seed=99):
     """Random-init 4-bit Qwen2 weights (reference tensor names), generated on
     the GPU and copied to host arrays for the NumPy stage."""
@@ -380,6 +462,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-small-m", action="store_true")
+    ap.add_argument("--no-wire", action="store_true")
+    ap.add_argument("--wire-only", action="store_true", help="only the activation codec section")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--sweep-only", action="store_true",
@@ -403,6 +487,12 @@ def main():
     from hetero import q4
     lib = q4.load()
     dev = torch.device("cuda:0")
+    if args.wire_only:
+        res = wire_bench(torch, lib, dev)
+        if not args.no_cpu_baseline:
+            res["cpu_baseline"] = wire_cpu_baseline()
+        print(json.dumps({"wire": res}), flush=True)
+        return
     if args.decode_only:
         res = decode_bench(torch, dev, steps=args.decode_steps, check=not args.no_decode_check)
         print(json.dumps({"decode": res}), flush=True)
@@ -563,13 +653,18 @@ def main():
                                     "launches_per_step": LAYERS * len(LAYER_SHAPES) + 1},
     }
     if args.sweep_only:
-        args.no_prefill = args.no_cpu_baseline = args.no_decode = args.no_small_m = True
+        args.no_prefill = args.no_cpu_baseline = args.no_decode = args.no_small_m = args.no_wire = True
     if not args.no_small_m:
         log("small-M ...")
         result["small_m"] = small_m_bench(torch, lib, layers, dev)
     if not args.no_prefill:
         log("prefill ...")
         result["prefill"] = prefill_bench(torch, lib, layers, dev)
+    if not args.no_wire:
+        log("wire codec ...")
+        result["wire"] = wire_bench(torch, lib, dev)
+        if not args.no_cpu_baseline:
+            result["wire"]["cpu_baseline"] = wire_cpu_baseline()
     rows, threads = 1, 16
     if not args.no_cpu_baseline:
         log("cpu baseline ...")

@@ -24,6 +24,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 SRC = os.path.join(CSRC, "q4gemv.hip")
 DECODE = os.path.join(CSRC, "q4_decode.hip")
+WIRE = os.path.join(CSRC, "q4_wire.hip")
 INST = os.path.join(CSRC, "q4_stream_inst.hip")
 OUT = os.path.join(HERE, "kernel", "libq4gemv.so")
 
@@ -60,7 +61,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
     jobs = jobs or min(16, os.cpu_count() or 4)
     with tempfile.TemporaryDirectory(prefix="q4build") as tmpd:
-        units = [(SRC, os.path.join(tmpd, "q4gemv.o"), []), (DECODE, os.path.join(tmpd, "q4_decode.o"), [])]
+        units = [(SRC, os.path.join(tmpd, "q4gemv.o"), []), (DECODE, os.path.join(tmpd, "q4_decode.o"), []),
+                 (WIRE, os.path.join(tmpd, "q4_wire.o"), [])]
         for mr, pair, ring in STREAM_INSTANCES:
             obj = os.path.join(tmpd, f"stream_m{mr}_p{pair}_r{ring}.o")
             units.append((INST, obj, [f"-DQ4_MR={mr}", f"-DQ4_PAIR={pair}", f"-DQ4_RING={ring}"]))

@@ -25,7 +25,9 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            # decode-step kernels (include/q4decode.h)
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
            "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev",
-           "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev")
+           "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev",
+           # activation wire codec (include/q4wire.h)
+           "q4_wire_payload_bytes", "q4_wire_encode_dev", "q4_wire_decode_dev")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
@@ -80,6 +82,12 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_norm_gate_up_silu_dev.restype = _I
         lib.q4_argmax_dev.argtypes = [_VP, _I, _VP, _VP, _VP, ctypes.c_int64, _I, _VP]
         lib.q4_argmax_dev.restype = _I
+        lib.q4_wire_payload_bytes.argtypes = [_I] * 3
+        lib.q4_wire_payload_bytes.restype = ctypes.c_longlong
+        lib.q4_wire_encode_dev.argtypes = [_VP, _I, _I, _I, _VP, _VP]
+        lib.q4_wire_encode_dev.restype = _I
+        lib.q4_wire_decode_dev.argtypes = [_VP, _I, _I, _I, _VP, _VP]
+        lib.q4_wire_decode_dev.restype = _I
     return lib
 
 

@@ -18,7 +18,7 @@ import pytest
 from hetero import q4
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("q4gemv.h", "q4decode.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("q4gemv.h", "q4decode.h", "q4wire.h")]
 
 
 def header_functions():
@@ -124,3 +124,25 @@ def test_decode_kernel_argument_errors(lib):
     assert lib.q4_norm_gate_up_silu_dev(*([p] * 6), p, None, p, 1e-6, None, p, 64, 256, 128, None) == q4.Q4_EARG
     assert lib.q4_attention_scratch_floats(28, 128, 2048) == 28 * 32 * 130
     assert lib.q4_attention_scratch_floats(28, 128, 2049) == 28 * 33 * 130
+
+
+def test_wire_codec_argument_errors(lib):
+    """Payload sizes (host arithmetic) and the codec's checks before any launch."""
+    assert lib.q4_wire_payload_bytes(0, 3, 3584) == 2 * 3 * 3584
+    assert lib.q4_wire_payload_bytes(1, 3, 3584) == 3 * 4 + 3 * 3584
+    assert lib.q4_wire_payload_bytes(1, 0, 3584) == 0
+    assert lib.q4_wire_payload_bytes(2, 3, 3584) == -1
+    assert lib.q4_wire_payload_bytes(0, -1, 3584) == -1
+    assert lib.q4_wire_payload_bytes(0, 1, 0) == -1
+    x = np.zeros(16, np.float32)
+    p = x.ctypes.data
+    assert lib.q4_wire_encode_dev(p, 1, 16, 7, p, None) == q4.Q4_EARG                 # unknown codec
+    assert lib.q4_wire_encode_dev(p, -1, 16, 0, p, None) == q4.Q4_EARG
+    assert lib.q4_wire_encode_dev(None, 1, 16, 1, p, None) == q4.Q4_EARG
+    assert lib.q4_wire_encode_dev(p, 1, 40000, 1, p, None) == q4.Q4_EARG             # int8 row past 32768
+    assert lib.q4_wire_encode_dev(p, 1, 16, 1, p + 2, None) == q4.Q4_EARG            # payload not 4-aligned
+    assert lib.q4_wire_decode_dev(p, 1, 16, 3, p, None) == q4.Q4_EARG
+    assert lib.q4_wire_decode_dev(None, 1, 16, 0, p, None) == q4.Q4_EARG
+    assert lib.q4_wire_decode_dev(p + 2, 1, 16, 1, p, None) == q4.Q4_EARG
+    assert lib.q4_wire_encode_dev(None, 0, 16, 1, None, None) == 0                    # no rows: no-op
+    assert lib.q4_wire_decode_dev(None, 0, 16, 1, None, None) == 0
