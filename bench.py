@@ -265,6 +265,95 @@ def wire_cpu_baseline(rows_list=(1, 256, 2048), hidden=3584, budget_s=2.0):
             "rows": res}
 
 
+def load_bench(torch, dev, layers=4, reps=2):
+    """Checkpoint shard -> HBM (hetero/shard.py).  A synthetic MLX-layout
+    checkpoint of `layers` Qwen2.5-7B decoder layers (131 MB each: U32
+    weights, F16 scales/biases, F32 biases and norms, two layers per file)
+    is written to a temporary directory.  It is then loaded three ways:
+      * load_shard(framework="hip"): owned byte ranges through two pinned
+        staging buffers, with async copies on a copy stream;
+      * the reference's path, load_shard(framework="numpy") through the
+        safetensors package (hetero/shard.py:131-153), then one device copy
+        per tensor;
+      * the same package read alone (no device), for scale.
+    The files were just written, so they come from the page cache:
+    host-memory -> HBM throughput, not disk."""
+    import shutil
+    import tempfile
+    import numpy as np
+    from safetensors import safe_open
+    from safetensors.numpy import save_file
+    from hetero import cpu_model
+    from hetero.shard import ShardSpec, WeightIndex
+    cfg = cpu_model.qwen2_7b_config(layers)
+    h, inter = cfg["hidden_size"], cfg["intermediate_size"]
+    kvd = h // cfg["num_attention_heads"] * cfg["num_key_value_heads"]
+    rng = np.random.default_rng(0)
+    d = tempfile.mkdtemp(prefix="q4ckpt", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        for f0 in range(0, layers, 2):
+            t = {}
+            for i in range(f0, min(layers, f0 + 2)):
+                p = f"model.layers.{i}"
+                for name, n_out, n_in, bias in (("self_attn.q_proj", h, h, True), ("self_attn.k_proj", kvd, h, True),
+                                                ("self_attn.v_proj", kvd, h, True), ("self_attn.o_proj", h, h, False),
+                                                ("mlp.gate_proj", inter, h, False), ("mlp.up_proj", inter, h, False),
+                                                ("mlp.down_proj", h, inter, False)):
+                    q = f"{p}.{name}"
+                    t[f"{q}.weight"] = rng.integers(0, 2 ** 32, (n_out, n_in // 8), dtype=np.uint32)
+                    t[f"{q}.scales"] = (rng.random((n_out, n_in // 64), dtype=np.float32) * 0.02).astype(np.float16)
+                    t[f"{q}.biases"] = (rng.random((n_out, n_in // 64), dtype=np.float32) * -0.1).astype(np.float16)
+                    if bias:
+                        t[f"{q}.bias"] = rng.standard_normal(n_out, dtype=np.float32) * 0.02
+                for nrm in ("input_layernorm", "post_attention_layernorm"):
+                    t[f"{p}.{nrm}.weight"] = np.ones(h, np.float32)
+            save_file(t, os.path.join(d, f"model-{f0 // 2:05d}.safetensors"), metadata={"format": "mlx"})
+            del t
+        with open(os.path.join(d, "config.json"), "w") as f:
+            json.dump(cfg, f)
+        idx = WeightIndex(d)
+        spec = ShardSpec(0, layers, False, False)
+        nbytes = idx.shard_bytes(spec)
+
+        def ours():
+            return idx.load_shard(spec, framework="hip", device=dev)
+
+        def reference_path():
+            out = {}
+            for path in sorted({idx.entries[n][0] for n in idx.owned(spec)}):
+                with safe_open(path, framework="numpy") as f:
+                    for n in f.keys():
+                        out[n] = torch.from_numpy(f.get_tensor(n)).to(dev)
+            return out
+
+        def host_only():
+            out = {}
+            for path in sorted({idx.entries[n][0] for n in idx.owned(spec)}):
+                with safe_open(path, framework="numpy") as f:
+                    for n in f.keys():
+                        out[n] = f.get_tensor(n)
+            return out
+
+        res = {}
+        for name, fn in (("load_shard_hip", ours), ("reference_numpy_then_copy", reference_path),
+                         ("reference_numpy_host_only", host_only)):
+            best = None
+            for _ in range(reps):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                w = fn()
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                del w
+                best = dt if best is None else min(best, dt)
+            res[name] = {"s": round(best, 4), "GB_s": round(nbytes / best / 1e9, 2)}
+        return {"workload": f"{layers} Qwen2.5-7B decoder layers in MLX 4-bit layout, {nbytes} bytes in "
+                            f"{len(os.listdir(d)) - 1} safetensors files (page cache) -> HBM", "bytes": nbytes,
+                **res}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def decode_weights(torch, cfg, dev, seed=99):
     """Random-init 4-bit Qwen2 weights (reference tensor names), generated on
     the GPU and copied to host arrays for the NumPy stage."""
@@ -464,6 +553,8 @@ def main():
     ap.add_argument("--no-small-m", action="store_true")
     ap.add_argument("--no-wire", action="store_true")
     ap.add_argument("--wire-only", action="store_true", help="only the activation codec section")
+    ap.add_argument("--no-load", action="store_true")
+    ap.add_argument("--load-only", action="store_true", help="only the checkpoint-to-HBM section")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--sweep-only", action="store_true",
@@ -487,6 +578,9 @@ def main():
     from hetero import q4
     lib = q4.load()
     dev = torch.device("cuda:0")
+    if args.load_only:
+        print(json.dumps({"load": load_bench(torch, dev)}), flush=True)
+        return
     if args.wire_only:
         res = wire_bench(torch, lib, dev)
         if not args.no_cpu_baseline:
@@ -654,6 +748,7 @@ def main():
     }
     if args.sweep_only:
         args.no_prefill = args.no_cpu_baseline = args.no_decode = args.no_small_m = args.no_wire = True
+        args.no_load = True
     if not args.no_small_m:
         log("small-M ...")
         result["small_m"] = small_m_bench(torch, lib, layers, dev)
@@ -665,6 +760,9 @@ def main():
         result["wire"] = wire_bench(torch, lib, dev)
         if not args.no_cpu_baseline:
             result["wire"]["cpu_baseline"] = wire_cpu_baseline()
+    if not args.no_load:
+        log("checkpoint load ...")
+        result["load"] = load_bench(torch, dev)
     rows, threads = 1, 16
     if not args.no_cpu_baseline:
         log("cpu baseline ...")

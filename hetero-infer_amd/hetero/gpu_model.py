@@ -31,7 +31,8 @@ from . import q4
 class GpuStage:
     def __init__(self, cfg: dict, w: Dict[str, np.ndarray], kv_k: List[np.ndarray],
                  kv_v: List[np.ndarray], max_new: int, device="cuda", lib=None):
-        """w: reference-named numpy weights (cpu_model.synthetic_weights);
+        """w: reference-named weights, NumPy arrays (cpu_model.synthetic_weights)
+        or device tensors (shard.WeightIndex.load_shard(..., framework="hip"));
         kv_k / kv_v: per layer [KH, S0, D] context already in the cache
         (fp16 as stored); max_new: decode steps the cache must hold."""
         import torch
@@ -50,12 +51,29 @@ class GpuStage:
         dev = self.dev
 
         def t(a, dtype=None):
+            if isinstance(a, torch.Tensor):           # already loaded (hetero/shard.py)
+                return a.to(dev) if dtype is None else a.to(dev, dtype)
             a = np.ascontiguousarray(a)
             tt = torch.from_numpy(a.view(np.int16) if a.dtype == np.float16 else a)
             return tt.to(dev) if dtype is None else tt.to(dev, dtype)
 
+        def f16_bits(a):
+            """scales/biases as fp16 bit patterns (cpu_model.py:102-103 takes
+            them as float16; a bf16 or fp32 checkpoint is rounded to nearest
+            fp16 once, here)."""
+            if isinstance(a, torch.Tensor):
+                a = a.to(dev)
+                return (a if a.dtype == torch.float16 else a.to(torch.float32).to(torch.float16)).view(torch.int16)
+            return t(np.asarray(a, dtype=np.float16))
+
+        def f32(a):
+            """.astype(np.float32) of a host array or a device tensor"""
+            if isinstance(a, torch.Tensor):
+                return a.to(dev, torch.float32)
+            return t(np.asarray(a).astype(np.float32))
+
         def mat(name):
-            return (t(w[f"{name}.weight"]), t(w[f"{name}.scales"]), t(w[f"{name}.biases"]))
+            return (t(w[f"{name}.weight"]), f16_bits(w[f"{name}.scales"]), f16_bits(w[f"{name}.biases"]))
 
         self.embed = mat("model.embed_tokens")
         self.layers = []
@@ -63,13 +81,13 @@ class GpuStage:
             p = f"model.layers.{i}"
             L = {
                 "qkv": [mat(f"{p}.self_attn.{x}_proj") for x in ("q", "k", "v")],
-                "qkv_bias": t(np.concatenate([w[f"{p}.self_attn.{x}_proj.bias"] for x in ("q", "k", "v")])
-                              .astype(np.float32)),
+                "qkv_bias": torch.cat([f32(w[f"{p}.self_attn.{x}_proj.bias"]).reshape(-1)
+                                       for x in ("q", "k", "v")]),
                 "o": mat(f"{p}.self_attn.o_proj"),
                 "gate": mat(f"{p}.mlp.gate_proj"), "up": mat(f"{p}.mlp.up_proj"),
                 "down": mat(f"{p}.mlp.down_proj"),
-                "in_w": t(w[f"{p}.input_layernorm.weight"].astype(np.float32)),      # cpu_model.py:298-299
-                "post_w": t(w[f"{p}.post_attention_layernorm.weight"].astype(np.float32)),
+                "in_w": f32(w[f"{p}.input_layernorm.weight"]),                      # cpu_model.py:298-299
+                "post_w": f32(w[f"{p}.post_attention_layernorm.weight"]),
             }
             kc = torch.zeros((self.nkv, self.cap, self.hd), dtype=torch.float16, device=dev)
             vc = torch.zeros_like(kc)
@@ -77,8 +95,9 @@ class GpuStage:
             vc[:, :self.s0] = t(kv_v[i].astype(np.float16)).view(torch.float16)
             L["k_cache"], L["v_cache"] = kc, vc
             self.layers.append(L)
-        self.norm_w = t(w["model.norm.weight"].astype(np.float32))
-        self.lm_head = mat("lm_head")
+        self.norm_w = f32(w["model.norm.weight"])
+        tied = bool(cfg.get("tie_word_embeddings", False))
+        self.lm_head = self.embed if tied else mat("lm_head")                # cpu_model.py:324-329
         # RoPE table exactly as the reference builds it (cpu_model.py:180-193)
         half = self.hd // 2
         inv = cfg["rope_theta"] ** (-np.arange(0, half, dtype=np.float32) * 2.0 / self.hd)
