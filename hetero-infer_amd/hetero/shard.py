@@ -7,10 +7,10 @@ and loads those alone.  What this module adds is a device target:
 
   * load_shard(spec, framework="hip") streams the owned tensors straight into
     HBM.  It reads their byte ranges from the files into two pinned staging
-    buffers, and each filled buffer is copied to the device asynchronously on
-    a copy stream while the next range is read.  No host copy of the shard is
-    ever whole, and the tensors come back as device tensors in the file's
-    dtype.
+    buffers, several threads per buffer.  Each filled buffer is copied to the
+    device asynchronously on a copy stream while the next range is read.  No
+    host copy of the shard is ever whole, and the tensors come back as device
+    tensors in the file's dtype.
   * Residency tracks what a device holds (name -> tensor, bytes per layer)
     and refuses a shard that does not fit in the free HBM, before reading
     anything.
@@ -168,7 +168,8 @@ class WeightIndex:
     # ---- loading ----
 
     def load_shard(self, spec: ShardSpec, framework: str = "numpy", device="cuda",
-                   residency: Optional["Residency"] = None, staging_bytes: int = 64 << 20):
+                   residency: Optional["Residency"] = None, staging_bytes: int = 64 << 20,
+                   readers: int = 4):
         """Read only this stage's tensors (hetero/shard.py:131-159).
 
         framework="numpy": {name: ndarray} (BF16 has no NumPy dtype and
@@ -182,7 +183,7 @@ class WeightIndex:
             raise ValueError(f"unknown framework {framework}")
         if residency is not None:
             residency.reserve(sum(self.nbytes(n) for n in names))
-        out = self._to_device(names, device, staging_bytes)
+        out = self._to_device(names, device, staging_bytes, readers)
         if residency is not None:
             residency.add(out)
         return out
@@ -195,8 +196,9 @@ class WeightIndex:
         mm = np.memmap(path, dtype=np.uint8, mode="r", offset=b0, shape=(nb,)) if nb else np.zeros(0, np.uint8)
         return np.array(mm).view(_NUMPY[dt]).reshape(shape)
 
-    def _to_device(self, names: List[str], device, staging_bytes: int):
+    def _to_device(self, names: List[str], device, staging_bytes: int, readers: int):
         import torch
+        from concurrent.futures import ThreadPoolExecutor
         dev = torch.device(device)
         out = {}
         # one device buffer per tensor, in the file's dtype; reads go file by
@@ -229,7 +231,18 @@ class WeightIndex:
         views = [memoryview(s.numpy()) for s in stage]
         done = [None, None]
         copy_stream = torch.cuda.Stream(device=dev)
+        pool = ThreadPoolExecutor(max(1, readers))
         k = 0
+
+        def read(fd, mv, at):               # one reader's part of a chunk (preadv drops the GIL)
+            got = 0
+            while got < len(mv):
+                r = os.preadv(fd, [mv[got:]], at + got)
+                if r <= 0:
+                    break
+                got += r
+            return got
+
         for path, off, total, dsts in spans:
             with open(path, "rb", buffering=0) as f:
                 di, dpos = 0, 0             # destination tensor and the bytes of it written
@@ -239,8 +252,13 @@ class WeightIndex:
                     slot = k % 2
                     if done[slot] is not None:
                         done[slot].synchronize()          # the copy out of this buffer has finished
-                    got = os.preadv(f.fileno(), [views[slot][:n]], off + pos)
+                    # the chunk in `readers` page-aligned parts, read in parallel
+                    step = max(4096, -(-n // max(1, readers)) + 4095 & ~4095)
+                    parts = [(a, min(n, a + step)) for a in range(0, n, step)]
+                    got = sum(fu.result() for fu in [pool.submit(read, f.fileno(), views[slot][a:b], off + pos + a)
+                                                     for a, b in parts])
                     if got != n:
+                        pool.shutdown()
                         raise IOError(f"{path}: short read at {off + pos} ({got} of {n} bytes)")
                     with torch.cuda.stream(copy_stream):
                         s = 0
@@ -257,6 +275,7 @@ class WeightIndex:
                     done[slot] = ev
                     pos += n
                     k += 1
+        pool.shutdown()
         copy_stream.synchronize()
         torch.cuda.current_stream(dev).wait_stream(copy_stream)
         return out
