@@ -14,10 +14,11 @@ namespace q4k {
 //   * The x prologue runs once per workgroup.  Every x load is issued before
 //     the first weight load and x is read once: vector-memory results return
 //     in issue order, so an x load issued behind the weight stream would wait
-//     for it.  Each thread loads whole packed words (8 values), stages them
-//     in LDS and takes amax; after one barrier one thread per group chains
-//     the group sum in ascending order from LDS while every thread writes
-//     the int8/uint8 planes of its words of the int16 x into LDS.
+//     for it.  Each thread loads whole packed words (8 values), one per
+//     round of blockDim.x words, and takes amax; the 8 lanes of a group
+//     chain its sum in ascending order, lane after lane, one chain per
+//     round; after one barrier every thread writes the int8/uint8 planes of
+//     its words of the int16 x into LDS.
 //   * Then every wave works alone on a flat stream of 1 KiB items: the items
 //     of its units (UB consecutive rows; PAIR: UB rows of matrix 0 and the
 //     same UB rows of matrix 1), chunk-major within a unit so consecutive
@@ -64,18 +65,14 @@ struct NormArgs {
 // the banks.
 __host__ __device__ inline int term_stride(int G) { return ((G + 3) & ~3) | 4; }
 
-// Staged x floats: group g of row m at (m*G + g) * kStageStride floats, so
-// the 16-byte reads of one lane per group land on distinct banks.
-constexpr int kStageStride = 68;
-
-// rw: words of x per thread and row; the staged floats only exist for rw > 1.
+// rw: words of x per thread and row (the register rounds of the x prologue).
 inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU, int rw) {
+    (void)rw;
     const size_t terms = static_cast<size_t>(nwaves) * mr * NU * term_stride(G) * 4;
-    const size_t stage = rw > 1 ? static_cast<size_t>(mr) * G * kStageStride * 4 : 0;
     return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
          + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
          + static_cast<size_t>(mr) * 16 * 4 + 16                         // amax per wave, counter
-         + (terms > stage ? terms : stage);                              // term tables | staged x
+         + terms;                                                        // term tables
 }
 
 __device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
@@ -246,8 +243,8 @@ __host__ __device__ constexpr int stream_waves_per_cu() { return MR >= 8 ? 8 : 1
 // kernel writes.  MR = 1 and RW = 1 only.
 // Rows of x past ml.mrows (an M below MR) read 0 and their outputs are not
 // stored.
-// Host guarantees: MR * (n_in / 64) <= blockDim.x (one thread per group
-// item), chunks * 256 <= RW * blockDim.x, n_in % 64 == 0, x 16-byte aligned.
+// Host guarantees: chunks * 256 <= RW * blockDim.x, n_in % 64 == 0, x
+// 16-byte aligned.
 template <int MR, int RW, bool PAIR, int RING, bool NORM>
 __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_kernel(MatList ml,
                                                                                      const float* __restrict__ x,
@@ -268,26 +265,31 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
     int* claim_ctr = reinterpret_cast<int*>(red + MR * 16);       // units handed out past the first
     float* Tw = red + MR * 16 + 4 + wave * (MR * NU * Ts);        // this wave: [MR][NU][Ts]
-    const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
-    const int n_units = (n_total + UB - 1) / UB;
-    const int items = NU * C;
 
     // ---- x loads: thread t owns words t, t + nt, ... of every row, 8 values
     //      each, through a resource over x (words at or past the row end read
-    //      0); waves with no word in a round issue nothing.  These are the
-    //      first loads of the kernel, so the waits further down stay exact.
+    //      0).  These are the first loads of the kernel, so the waits further
+    //      down stay exact.
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(ml.mrows * n_in) * 4u);
+    // unconditional (a wave with no word in a round reads past the range: 0,
+    // no access), so the loads depend on nothing but x, n_in and mrows and
+    // go out after the first round of kernel-argument reads
     float4 wv[MR][RW][2];
 #pragma unroll
     for (int m = 0; m < MR; m++)
 #pragma unroll
-        for (int r = 0; r < RW; r++)
-            if (r * nt + wave * 64 < wpr) {                       // uniform
-                const int j = r * nt + tid;
-                const uint32_t off = j < wpr ? static_cast<uint32_t>(m * n_in + 8 * j) * 4u : kOutOfRange;
-                wv[m][r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
-                wv[m][r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
-            }
+        for (int r = 0; r < RW; r++) {
+            const int j = r * nt + tid;
+            const uint32_t off = j < wpr ? static_cast<uint32_t>(m * n_in + 8 * j) * 4u : kOutOfRange;
+            wv[m][r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            wv[m][r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+        }
+    // nothing below (the indexed row_begin read in particular) may be
+    // scheduled ahead of these loads
+    __builtin_amdgcn_sched_barrier(0);
+    const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
+    const int n_units = (n_total + UB - 1) / UB;
+    const int items = NU * C;
     // NORM: the thread's word of delta and of the norm weights (a NULL
     // delta reads through an empty range: no access)
     float4 nd[2], nw[2];
@@ -330,17 +332,14 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     // ---- group sums (kernel/q4gemv.c:244-248: the group's 64 values added
     //      in ascending order) and the running max |x| (:258-259,
     //      NaN-skipping) per row.  A group is 8 consecutive words, so it
-    //      lies in 8 consecutive lanes of one wave.  With one word per
-    //      thread the wave chains its groups itself, lane after lane
-    //      (row_shr:1), while it waits for the other waves' x; otherwise
-    //      the floats are staged in LDS (the term tables' space, free until
-    //      the main loop) and one thread per group chains them after the
-    //      barrier.
-    float* stage = red + MR * 16 + 4;
+    //      lies in 8 consecutive lanes of one wave: the wave chains its
+    //      groups itself, lane after lane (row_shr:1), while it waits for
+    //      the other waves' x -- every round's chain at once.
+    float* stage = red + MR * 16 + 4;                              // NORM: the wave sums
     if constexpr (NORM) {
         // hetero/cpu_model.py:304-306 (x + delta) and :164-166 (RMSNorm); the
-        // sum of squares goes through the staging space (free until the
-        // main loop), the amax slots stay untouched
+        // wave sums of squares go through the term tables' space (free until
+        // the main loop), the amax slots stay untouched
         float ss = 0.0f;
         float v[8] = {wv[0][0][0].x, wv[0][0][0].y, wv[0][0][0].z, wv[0][0][0].w,
                       wv[0][0][1].x, wv[0][0][1].y, wv[0][0][1].z, wv[0][0][1].w};
@@ -376,36 +375,40 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     }
 #pragma unroll
     for (int m = 0; m < MR; m++) {
+        // one chain per round, the rounds' chains independent (interleaved
+        // by the scheduler); words past the row end are 0 and store nothing
+        float v8[RW][8], acc[RW];
         float amax = 0.0f;
 #pragma unroll
-        for (int r = 0; r < RW; r++)
-            if (r * nt + wave * 64 < wpr) {                       // uniform
-                const int j = r * nt + tid;
-                if constexpr (RW == 1) {
-                    const float v8[8] = {wv[m][r][0].x, wv[m][r][0].y, wv[m][r][0].z, wv[m][r][0].w,
-                                         wv[m][r][1].x, wv[m][r][1].y, wv[m][r][1].z, wv[m][r][1].w};
-                    const int sub = lane & 7;
-                    float acc = 0.0f;
+        for (int r = 0; r < RW; r++) {
+            const float4 a = wv[m][r][0], b = wv[m][r][1];
+            v8[r][0] = a.x; v8[r][1] = a.y; v8[r][2] = a.z; v8[r][3] = a.w;
+            v8[r][4] = b.x; v8[r][5] = b.y; v8[r][6] = b.z; v8[r][7] = b.w;
+            acc[r] = 0.0f;
+            amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                     fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+        }
+        const int sub = lane & 7;
+        if (wave * 64 < wpr) {                                    // uniform: the wave has words
 #pragma unroll
-                    for (int step = 0; step < 8; step++) {
-                        // lane 8k+step continues the chain of lane 8k+step-1
-                        float a = step == 0 ? 0.0f
-                                            : __int_as_float(__builtin_amdgcn_update_dpp(
-                                                  0, __float_as_int(acc), 0x111, 0xF, 0xF, false));
+            for (int step = 0; step < 8; step++) {
 #pragma unroll
-                        for (int i = 0; i < 8; i++) a = __fadd_rn(a, v8[i]);
-                        acc = sub == step ? a : acc;
-                    }
-                    if (sub == 7 && j < wpr) xsum_lds[m * Gr + (j >> 3)] = acc;
-                } else if (j < wpr) {
-                    float4* dst = reinterpret_cast<float4*>(stage + (m * G + (j >> 3)) * kStageStride + 8 * (j & 7));
-                    dst[0] = wv[m][r][0];
-                    dst[1] = wv[m][r][1];
+                for (int r = 0; r < RW; r++) {
+                    // lane 8k+step continues the chain of lane 8k+step-1
+                    float a = step == 0 ? 0.0f
+                                        : __int_as_float(__builtin_amdgcn_update_dpp(
+                                              0, __float_as_int(acc[r]), 0x111, 0xF, 0xF, false));
+#pragma unroll
+                    for (int i = 0; i < 8; i++) a = __fadd_rn(a, v8[r][i]);
+                    acc[r] = sub == step ? a : acc[r];
                 }
-                const float4 a = wv[m][r][0], b = wv[m][r][1];  // 0 past the row end
-                amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
             }
+#pragma unroll
+            for (int r = 0; r < RW; r++) {
+                const int j = r * nt + tid;
+                if (sub == 7 && j < wpr) xsum_lds[m * Gr + (j >> 3)] = acc[r];
+            }
+        }
         amax = wave_max(amax);
         if (lane == 0) red[m * 16 + wave] = amax;
     }
@@ -424,23 +427,6 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
         return v + nwaves;                                        // lane 0's value counts
     };
     int claimed = claim();
-
-    // ---- group sums from the staged floats: one thread per (row, group)
-    //      chains its 64 values in ascending order
-    if (RW > 1 && tid < MR * G) {
-        const float4* gp = reinterpret_cast<const float4*>(stage + tid * kStageStride);
-        float sum = 0.0f;
-#pragma unroll
-        for (int i0 = 0; i0 < 16; i0 += 4) {
-            const float4 v0 = gp[i0], v1 = gp[i0 + 1], v2 = gp[i0 + 2], v3 = gp[i0 + 3];
-            const float vals[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
-                                    v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
-#pragma unroll
-            for (int i = 0; i < 16; i++) sum = __fadd_rn(sum, vals[i]);
-        }
-        const int m = tid / G;
-        xsum_lds[m * Gr + (tid - m * G)] = sum;
-    }
 
     // ---- int16 x (kernel/q4gemv.c:260-270) as byte planes in LDS
     float xsc[MR];

@@ -731,11 +731,9 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, c
     const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
     const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
     const int cus = num_cus();
-    // smallest workgroup the prologue accepts: one thread per (row, group)
-    // item, and at most rmax words of x per thread and row
-    int minw = (MR * G + 63) / 64;
-    const int wr = (C * kChunkWords + 64 * rmax - 1) / (64 * rmax);
-    if (wr > minw) minw = wr;
+    // smallest workgroup the prologue accepts: at most rmax words of x per
+    // thread and row
+    const int minw = (C * kChunkWords + 64 * rmax - 1) / (64 * rmax);
     if (minw > kWavesPerCu) return 0;
     // rows per unit: 1, or more when rows are plentiful and short -- up to 8
     // rows and kUnitItems items, while every wave still gets two units (the

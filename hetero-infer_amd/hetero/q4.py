@@ -82,6 +82,7 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_norm_gate_up_silu_dev.restype = _I
         lib.q4_argmax_dev.argtypes = [_VP, _I, _VP, _VP, _VP, ctypes.c_int64, _I, _VP]
         lib.q4_argmax_dev.restype = _I
+    if hasattr(lib, "q4_wire_encode_dev"):
         lib.q4_wire_payload_bytes.argtypes = [_I] * 3
         lib.q4_wire_payload_bytes.restype = ctypes.c_longlong
         lib.q4_wire_encode_dev.argtypes = [_VP, _I, _I, _I, _VP, _VP]
