@@ -162,27 +162,32 @@ __device__ __forceinline__ void unit_rows(UnitRows& ur, const MatList& ml, int u
 }
 
 // Issue the loads of item (chunk c, row slot r) of the unit whose rows `ur`
-// holds.  The row is wave-uniform: each array gets a resource over that row
-// alone, so lanes past the row end read 0 and cost no memory access, and
-// `live` false (a prefetch past the wave's last item) gives an empty
-// resource: every lane reads 0.  No branch, so the waits on earlier loads
-// stay exact.
+// holds.  The row is wave-uniform: each array gets a resource that starts at
+// the chunk and ends with the row, so lanes past the row end read 0 and cost
+// no memory access, and `live` false (a prefetch past the wave's last item)
+// gives an empty resource: every lane reads 0.  The chunk moves the
+// resource's base (scalar work); the lanes' offsets are the same for every
+// item.  No branch, so the waits on earlier loads stay exact.
 template <bool PAIR>
 __device__ __forceinline__ void load_item(Item& it, const UnitRows& ur, int unit, int c, int r, int UB,
-                                          int wpr, int G, int lane, bool live) {
+                                          int wpr, int G, uint32_t vo_w, uint32_t vo_g, bool live) {
     it.unit = unit;
     const bool second = PAIR && r >= UB;
     const int u = second ? r - UB : r;
     const uint32_t* wp = second ? ur.w[1] : ur.w[0];
     const uint16_t* sp = second ? ur.s[1] : ur.s[0];
     const uint16_t* bp = second ? ur.b[1] : ur.b[0];
-    const uint32_t wbytes = live ? static_cast<uint32_t>(wpr) * 4u : 0u;
-    const uint32_t gbytes = live ? static_cast<uint32_t>(G) * 2u : 0u;
-    const int word0 = c * kChunkWords + lane * 4;
-    const int go = (word0 >> 3) * 2;
-    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(wp + static_cast<size_t>(u) * wpr, wbytes);
-    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(sp + static_cast<size_t>(u) * G, gbytes);
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(bp + static_cast<size_t>(u) * G, gbytes);
+    // byte offsets from the unit's first row, 32-bit (a unit is at most 8
+    // rows of at most 16 KiB): row slot u, then chunk c
+    const uint32_t cw = static_cast<uint32_t>(c) * kChunkWords * 4u;      // bytes of the row before chunk c
+    const uint32_t cg = static_cast<uint32_t>(c) * (kChunkWords / 8) * 2u;  // bytes of its scales before it
+    const uint32_t ow = static_cast<uint32_t>(u * wpr) * 4u + cw;
+    const uint32_t og = static_cast<uint32_t>(u * G) * 2u + cg;
+    const uint32_t wbytes = live ? static_cast<uint32_t>(wpr) * 4u - cw : 0u;
+    const uint32_t gbytes = live ? static_cast<uint32_t>(G) * 2u - cg : 0u;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc(reinterpret_cast<const char*>(wp) + ow, wbytes);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(reinterpret_cast<const char*>(sp) + og, gbytes);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(reinterpret_cast<const char*>(bp) + og, gbytes);
     // the three loads in a fixed order wherever an item is loaded: the
     // partial waits on the ring are computed from the issue order, which
     // must then be the same on entry to the main loop as around it.  The
@@ -193,11 +198,11 @@ __device__ __forceinline__ void load_item(Item& it, const UnitRows& ur, int unit
     // and with the neighbouring rows.
     constexpr int kNonTemporal = 2;
     __builtin_amdgcn_sched_barrier(0);
-    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, word0 * 4, 0, kNonTemporal));
+    it.w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, vo_w, 0, kNonTemporal));
     __builtin_amdgcn_sched_barrier(0);
-    it.s = __builtin_amdgcn_raw_buffer_load_b16(rs, go, 0, 0);
+    it.s = __builtin_amdgcn_raw_buffer_load_b16(rs, vo_g, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    it.b = __builtin_amdgcn_raw_buffer_load_b16(rb, go, 0, 0);
+    it.b = __builtin_amdgcn_raw_buffer_load_b16(rb, vo_g, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
 }
 
@@ -320,12 +325,15 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     const bool has_work = first_unit < n_units;                   // uniform
     constexpr int kE = RING < kEarly ? RING : kEarly;
     Item ring[RING];
+    // the lane's byte offsets inside an item: its 16 bytes of weights, the
+    // fp16 scale/bias of its group (two lanes per group)
+    const uint32_t vo_w = static_cast<uint32_t>(lane) * 16u, vo_g = static_cast<uint32_t>(lane >> 1) * 2u;
     int pf_unit = first_unit, pf_c = 0, pf_r = 0;                 // prefetch cursor (uniform)
     UnitRows pf_rows;
     unit_rows<PAIR>(pf_rows, ml, pf_unit, UB, wpr, G);
 #pragma unroll
     for (int d = 0; d < kE; d++) {
-        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, lane, has_work);
+        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, has_work);
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
 
@@ -414,7 +422,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     }
 #pragma unroll
     for (int d = kE; d < RING; d++) {
-        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, lane, has_work);
+        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, has_work);
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
     if (tid == 0) *claim_ctr = 0;
@@ -465,9 +473,11 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     // one item: the integer dots of chunk c against row slot u, one fp32
     // term per group written by the group's last lane
     auto consume = [&](const Item& itm, int c, int u) {
-        const int word0 = c * kChunkWords + lane * 4;
-        const bool lead = word0 < wpr && (lane & (lpg - 1)) == lpg - 1;
-        const int g = word0 >> 3;
+        // group g = c * 32 + lane / 2: a uniform part and a lane part; the
+        // lead (last) lane of a group writes its term if the group is in the row
+        const int lim = wpr - c * kChunkWords;                    // uniform
+        const bool lead = lane * 4 < lim && (lane & (lpg - 1)) == lpg - 1;
+        const int g = c * (kChunkWords / 8) + (lane >> 1);
         uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
 #pragma unroll
         for (int m = 0; m < MR; m++)
@@ -565,7 +575,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
                 // the refill may not be scheduled above the consume of its
                 // slot, so that the slot keeps its registers
                 __builtin_amdgcn_sched_barrier(0);
-                load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, lane, true);
+                load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, true);
                 if (++pf_r == NU) { pf_r = 0; ++pf_c; }
             }
             ++cyc_pf;
