@@ -384,10 +384,14 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGemmLdsK = 72;            // LDS row stride in bf16 (64 + 8 pad: conflict-free)
 
+// a in the low half, b in the high half, each rounded to nearest even: one
+// v_cvt_pk_bf16_f32 (two scalar conversions became a conversion each plus
+// shifts and ors)
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    const __bf16 ha = static_cast<__bf16>(a), hb = static_cast<__bf16>(b);   // RNE
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, ha)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hb)) << 16);
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+    const f32x2 p = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2v));
 }
 
 // x rounded to bf16 (RNE) once per call, 8 values per thread.
@@ -417,7 +421,12 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
 // past the workgroup's K range read 0 and cost no access.  Split-K:
 // blockIdx.z takes steps [z*kt_split, (z+1)*kt_split) and writes its
 // partial sums to out + z*M*N.
-template <int BM, int BN, int D>
+// EVENG (an even number of groups per row): the scales and biases come in
+// 32-bit words of two consecutive steps, the step's half picked when it is
+// dequantised.  16-bit loads were packed in pairs into one register right
+// after they were issued, which made the compiler wait for every load in
+// flight, the whole prefetch ring included.
+template <int BM, int BN, int D, bool EVENG>
 __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
     const uint16_t* __restrict__ xb, const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
     const uint16_t* __restrict__ bi, float* __restrict__ out, int M, int N, int K, int kt_split) {
@@ -427,7 +436,8 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
     uint16_t* Bs = As + 2 * BM * kGemmLdsK;                        // [2][BN][72]
     constexpr int TM = BM / 64, TN = BN / 64;                      // 32x32 tiles per wave
     constexpr int A_PER = BM * 8 / 256;                            // uint4 (8 bf16) of x per thread and step
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);       // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
     const int G = K >> 6, wpr = K >> 3;
@@ -440,46 +450,71 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
     const __amdgpu_buffer_rsrc_t br = buf_rsrc(bi + static_cast<size_t>(n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
     // B: 256 / BN threads per row, WPT words (8 nibbles each) per thread
     constexpr int QPR = 256 / BN, WPT = 8 / QPR;
-    static_assert(WPT == 4 || WPT == 2, "BN is 64 or 128");
+    static_assert(WPT == 8 || WPT == 4 || WPT == 2, "BN is 64, 128 or 256");
     const int brow = tid / QPR, bq = tid % QPR;
-    using BVec = typename std::conditional<WPT == 4, uint4, uint2>::type;
+    struct BVec {
+        uint32_t v[WPT];
+    };
 
     uint4 ra[D][A_PER];
     BVec rb[D];
-    uint16_t rs[D], rbb[D];
+    using SB = typename std::conditional<EVENG, uint32_t, uint16_t>::type;
+    SB rs[D], rbb[D];
     // issue the loads of step `it` (relative to kt0) into slot j
-    auto load = [&](uint4 (&a)[A_PER], BVec& bw, uint16_t& s16, uint16_t& b16, int it) {
-        const bool live = it < nk;
-        const int kt = kt0 + it;
+    // the lanes' offsets inside a step; a step adds a uniform offset, or an
+    // offset past every range when it is past the K range (reads 0).  An
+    // add, not a select: a select on the offsets became branches around
+    // duplicated loads, after which every wait on the ring was a full one.
+    uint32_t a_off[A_PER];
 #pragma unroll
-        for (int i = 0; i < A_PER; i++) {
-            const int idx = tid + 256 * i, row = idx >> 3, c = idx & 7;
-            const uint32_t off = live ? static_cast<uint32_t>(row * K + kt * 64 + c * 8) * 2u : kOutOfRange;
-            a[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+    for (int i = 0; i < A_PER; i++) {
+        const int idx = tid + 256 * i, row = idx >> 3, c = idx & 7;
+        a_off[i] = static_cast<uint32_t>(row * K + c * 8) * 2u;
+    }
+    const uint32_t w_off = static_cast<uint32_t>(brow * wpr + bq * WPT) * 4u;
+    const uint32_t g_off = static_cast<uint32_t>(brow * G) * 2u;
+    auto load = [&](uint4 (&a)[A_PER], BVec& bw, SB& s16, SB& b16, int it) {
+        const int kt = kt0 + it;
+        const uint32_t dead = __builtin_amdgcn_readfirstlane(it < nk ? 0u : kOutOfRange);
+        const uint32_t sa = static_cast<uint32_t>(kt) * 128u + dead;     // 64 bf16 of x per step
+        const uint32_t sw = static_cast<uint32_t>(kt) * 32u + dead;      // 8 words of w per step
+        const uint32_t sg = (EVENG ? static_cast<uint32_t>(kt >> 1) * 4u : static_cast<uint32_t>(kt) * 2u) + dead;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < A_PER; i++)
+            a[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, a_off[i] + sa, 0, 0));
+        const uint32_t wo = w_off + sw;
+        const uint32_t go = g_off + sg;
+        if constexpr (WPT >= 4) {
+#pragma unroll
+            for (int q = 0; q < WPT / 4; q++) {
+                const uint4 t = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo + 16 * q, 0, 2));
+                bw.v[4 * q] = t.x; bw.v[4 * q + 1] = t.y; bw.v[4 * q + 2] = t.z; bw.v[4 * q + 3] = t.w;
+            }
+        } else {
+            const uint2 t = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
+            bw.v[0] = t.x; bw.v[1] = t.y;
         }
-        const uint32_t wo = live ? static_cast<uint32_t>(brow * wpr + kt * 8 + bq * WPT) * 4u : kOutOfRange;
-        const uint32_t go = live ? static_cast<uint32_t>(brow * G + kt) * 2u : kOutOfRange;
-        if constexpr (WPT == 4)
-            bw = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo, 0, 2));
-        else
-            bw = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
-        s16 = __builtin_amdgcn_raw_buffer_load_b16(sr, go, 0, 0);
-        b16 = __builtin_amdgcn_raw_buffer_load_b16(br, go, 0, 0);
+        if constexpr (EVENG) {
+            s16 = __builtin_amdgcn_raw_buffer_load_b32(sr, go, 0, 0);
+            b16 = __builtin_amdgcn_raw_buffer_load_b32(br, go, 0, 0);
+        } else {
+            s16 = __builtin_amdgcn_raw_buffer_load_b16(sr, go, 0, 0);
+            b16 = __builtin_amdgcn_raw_buffer_load_b16(br, go, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     };
-    auto store = [&](const uint4 (&a)[A_PER], const BVec& bw, uint16_t s16, uint16_t b16, int buf) {
+    // store step `it` (relative to kt0), held in slot (a, bw, s16, b16), into LDS buffer `buf`
+    auto store = [&](const uint4 (&a)[A_PER], const BVec& bw, SB s16, SB b16, int buf, int it) {
 #pragma unroll
         for (int i = 0; i < A_PER; i++) {
             const int idx = tid + 256 * i, row = idx >> 3, c = idx & 7;
             *reinterpret_cast<uint4*>(As + (buf * BM + row) * kGemmLdsK + 8 * c) = a[i];
         }
         {
-            const float sf = h2f(s16), bf = h2f(b16);
-            uint32_t wd[WPT];
-            if constexpr (WPT == 4) {
-                wd[0] = bw.x; wd[1] = bw.y; wd[2] = bw.z; wd[3] = bw.w;
-            } else {
-                wd[0] = bw.x; wd[1] = bw.y;
-            }
+            const int sh = EVENG ? 16 * ((kt0 + it) & 1) : 0;              // uniform
+            const float sf = h2f(static_cast<uint16_t>(s16 >> sh)), bf = h2f(static_cast<uint16_t>(b16 >> sh));
+            const uint32_t* wd = bw.v;
 #pragma unroll
             for (int t = 0; t < WPT; t++) {
                 // even values in the bytes of lo, odd ones in hi; v_cvt_f32_ubyteN
@@ -509,7 +544,7 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
 
 #pragma unroll
     for (int j = 0; j < D; j++) load(ra[j], rb[j], rs[j], rbb[j], j);
-    store(ra[0], rb[0], rs[0], rbb[0], 0);
+    store(ra[0], rb[0], rs[0], rbb[0], 0, 0);
     __syncthreads();
     const int ngroups = (nk + D - 1) / D;
     for (int g = 0; g < ngroups; g++) {
@@ -517,11 +552,11 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
         for (int j = 0; j < D; j++) {
             const int it = g * D + j;
             const int cur = j & 1;
-            // slot j held step `it` (already in LDS): refill it with step it + D.
-            // Steps past the K range multiply zeros (their loads read 0), so
-            // the multiply needs no branch.
-            load(ra[j], rb[j], rs[j], rbb[j], it + D);
-            {
+            // slot j held step `it` (already in LDS): refill it with step it + D,
+            // then store step it + 1 (loaded D - 1 steps ago) into the other
+            // buffer.  Steps past the K range multiply zeros (their loads read
+            // 0), so the multiply needs no branch.
+            auto mfma_step = [&]() {
 #pragma unroll
                 for (int ks = 0; ks < 4; ks++) {
                     bf16x8 av[TM], bv[TN];
@@ -543,9 +578,10 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
                         for (int jj = 0; jj < TN; jj++)
                             acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[jj], acc[i][jj], 0, 0, 0);
                 }
-            }
-            // the next step, loaded D - 1 steps ago, into the other buffer
-            store(ra[(j + 1) % D], rb[(j + 1) % D], rs[(j + 1) % D], rbb[(j + 1) % D], cur ^ 1);
+            };
+            load(ra[j], rb[j], rs[j], rbb[j], it + D);
+            mfma_step();
+            store(ra[(j + 1) % D], rb[(j + 1) % D], rs[(j + 1) % D], rbb[(j + 1) % D], cur ^ 1, it + 1);
             __syncthreads();
         }
     }
@@ -999,11 +1035,10 @@ int dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, void
 }
 
 
-template <int BM, int BN>
+template <int BM, int BN, bool EVENG, int D = 4>      // D: steps in flight
 int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* xb, float* out,
                 int M, int N, int K, int S, int kt_split, hipStream_t st) {
-    constexpr int D = 4;                 // steps in flight
-    auto kern = gemm_q4_bf16_kernel<BM, BN, D>;
+    auto kern = gemm_q4_bf16_kernel<BM, BN, D, EVENG>;
     const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
     static bool attr_set = false;
     if (!attr_set) {
@@ -1356,8 +1391,12 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
     HIP_TRY(hipGetLastError());
     const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
     float* dst = S > 1 ? static_cast<float*>(ws->part) : out;
-    rc = BN == 128 ? launch_gemm<128, 128>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st)
-                   : launch_gemm<128, 64>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st);
+    if (G % 2 == 0)
+        rc = BN == 128 ? launch_gemm<128, 128, true>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st)
+                       : launch_gemm<128, 64, true>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st);
+    else
+        rc = BN == 128 ? launch_gemm<128, 128, false>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st)
+                       : launch_gemm<128, 64, false>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st);
     if (rc || S == 1) return rc;
     hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, st,
                        static_cast<const float*>(ws->part), out, static_cast<long>(mn), S);
