@@ -149,9 +149,11 @@ constexpr int kMaxChunks = 1024;        // cap <= 65536
 // also rotates the new key, writes the new key and value rows to the cache
 // and takes them from registers instead of the cache.
 // G: query heads per kv head, a template parameter so that the per-head
-// loops unroll and their LDS reads are issued together.
-template <bool ROPE, int G>
-__global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restrict__ q,
+// loops unroll and their LDS reads are issued together.  NW: waves (4, or 8
+// for head_dim >= 64), which split the head dimension of the scores and the
+// positions of the outputs between them.
+template <bool ROPE, int G, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_partial_kernel(const float* __restrict__ q,
                                                            uint16_t* __restrict__ kc,
                                                            uint16_t* __restrict__ vc,
                                                            const int64_t* __restrict__ pos_p,
@@ -161,11 +163,16 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
                                                            const float* __restrict__ bias,
                                                            const float* __restrict__ cos_t,
                                                            const float* __restrict__ sin_t) {
+    constexpr int NT = 64 * NW;                              // threads
+    constexpr int KV = kChunk * (kMaxD / 8) / NT;            // uint4 of K (and of V) per thread at d = 128
+    constexpr int QR = kMaxG * (kMaxD / 2) / NT;             // rounds of the RoPE'd query pairs
+    constexpr int PW = kChunk / NW;                          // positions per wave in the output pass
     __shared__ float4 q_s[kMaxG][kMaxD / 4];
     __shared__ uint4 k_s[kChunk][kRowU4];
     __shared__ uint4 v_s[kChunk][kRowU4];
     __shared__ __attribute__((aligned(16))) float p_s[kMaxG][kChunk];
-    __shared__ float sc_part[4][kMaxG][kChunk];
+    __shared__ float sc_part[NW][kMaxG][kChunk];
+    __shared__ float out_part[NW][kMaxG][kMaxD];
     const int chunk = blockIdx.x, kvh = blockIdx.y, n_chunks = gridDim.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t pos = *pos_p;
@@ -193,12 +200,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         buf_rsrc(kc + (static_cast<size_t>(kvh) * cap + c0) * d, static_cast<uint32_t>(nkv4) * 16u);
     const __amdgpu_buffer_rsrc_t vr =
         buf_rsrc(vc + (static_cast<size_t>(kvh) * cap + c0) * d, static_cast<uint32_t>(nkv4) * 16u);
-    uint4 kv[4], vv[4];
+    uint4 kv[KV], vv[KV];
     uint16_t fh1 = 0, fh2 = 0;                               // the fresh row's values of this thread
     auto load_kv = [&]() {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t off = static_cast<uint32_t>(r * 256 + tid) * 16u;
+        for (int r = 0; r < KV; r++) {
+            const uint32_t off = static_cast<uint32_t>(r * NT + tid) * 16u;
             kv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
             vv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
         }
@@ -208,10 +215,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         // fp32 operations as rope_kv_kernel
         const int half = d >> 1;
         const size_t prow = static_cast<size_t>(pos < 0 ? 0 : (pos >= cap ? cap - 1 : pos));
-        float qa[2][2], qb[2][2], cs[2][2];
+        float qa[QR][2], qb[QR][2], cs[QR][2];
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int e = r * 256 + tid;
+        for (int r = 0; r < QR; r++) {
+            const int e = r * NT + tid;
             if (e < G * half) {
                 const int g = e / half, i = e - g * half;
                 const int e1 = (kvh * G + g) * d + i;
@@ -236,8 +243,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         load_kv();
         float* qf = reinterpret_cast<float*>(&q_s[0][0]);
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int e = r * 256 + tid;
+        for (int r = 0; r < QR; r++) {
+            const int e = r * NT + tid;
             if (e < G * half) {
                 const int g = e / half, i = e - g * half;
                 const float x1 = __fadd_rn(qa[r][0], qb[r][0]), x2 = __fadd_rn(qa[r][1], qb[r][1]);
@@ -272,8 +279,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
     // position) hold 0, so the output loop needs no bound
     const int frow = fresh ? static_cast<int>(pos - c0) : -1;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int e = r * 256 + tid;
+    for (int r = 0; r < KV; r++) {
+        const int e = r * NT + tid;
         if (e < kChunk * du4 && e / du4 != frow) {
             k_s[e / du4][e % du4] = kv[r];
             v_s[e / du4][e % du4] = vv[r];
@@ -291,12 +298,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         }
     }
     __syncthreads();
-    // scores: wave w takes dims [w*d/4, (w+1)*d/4) of every position of the
-    // chunk (lane = position) for all G heads, so each K element is
-    // converted once; the four partial dots are added in wave order below
+    // scores: wave w takes dims [w*d/NW, (w+1)*d/NW) of every position of
+    // the chunk (lane = position) for all G heads, so each K element is
+    // converted once; the NW partial dots are added in wave order below
     {
         const int s = lane;
-        const int c_begin = wave * (du4 >> 2), c_end = c_begin + (du4 >> 2);
+        const int c_begin = wave * (du4 / NW), c_end = c_begin + du4 / NW;
         float acc[kMaxG];
 #pragma unroll
         for (int g = 0; g < kMaxG; g++) acc[g] = 0.0f;
@@ -326,11 +333,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
             if (g < G) sc_part[wave][g][s] = acc[g];
     }
     __syncthreads();
-    // softmax over the chunk, heads wave and wave + 4 (lane = position)
-    for (int g = wave; g < G; g += 4) {
+    // softmax over the chunk, heads wave, wave + NW, ... (lane = position)
+    for (int g = wave; g < G; g += NW) {
         const int s = lane;
-        const float dot = __fadd_rn(__fadd_rn(__fadd_rn(sc_part[0][g][s], sc_part[1][g][s]), sc_part[2][g][s]),
-                                    sc_part[3][g][s]);
+        float dot = sc_part[0][g][s];
+#pragma unroll
+        for (int w = 1; w < NW; w++) dot = __fadd_rn(dot, sc_part[w][g][s]);
         const float sc = s < valid ? __fmul_rn(dot, scale) : -__builtin_inff();
         const float m = wave_max(sc);
         const float p = s < valid ? expf(__fsub_rn(sc, m)) : 0.0f;
@@ -343,10 +351,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
         }
     }
     __syncthreads();
-    // unnormalised outputs: wave w takes positions [16w, 16w + 16), lane =
-    // fp16 pair of the row, all G heads; the K rows are no longer read, so
-    // their space holds the four partial outputs, added in wave order
-    float* out_part = reinterpret_cast<float*>(&k_s[0][0]);          // [4][kMaxG][kMaxD]
+    // unnormalised outputs: wave w takes positions [PW*w, PW*w + PW), lane
+    // = fp16 pair of the row, all G heads; the NW partial outputs are
+    // added in wave order
     {
         const int i = lane, dp = d >> 1;
         float a0[kMaxG], a1[kMaxG];
@@ -356,7 +363,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
             const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v_s[0][0]);
             constexpr int kRowW = kRowU4 * 4;
             // p is 0 and the V row is 0 past the valid positions
-            for (int s0 = 16 * wave; s0 < 16 * wave + 16; s0 += 4) {
+            for (int s0 = PW * wave; s0 < PW * wave + PW; s0 += 4) {
                 uint32_t w2[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) w2[j] = vw[(s0 + j) * kRowW + i];
@@ -381,37 +388,50 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* __restri
 #pragma unroll
             for (int g = 0; g < kMaxG; g++)
                 if (g < G) {
-                    float* op = out_part + (wave * kMaxG + g) * kMaxD;
-                    op[2 * i] = a0[g];
-                    op[2 * i + 1] = a1[g];
+                    out_part[wave][g][2 * i] = a0[g];
+                    out_part[wave][g][2 * i + 1] = a1[g];
                 }
         }
     }
     __syncthreads();
-    for (int e = tid; e < G * d; e += blockDim.x) {
+    for (int e = tid; e < G * d; e += NT) {
         const int g = e / d, j = e - g * d;
-        const float* op = out_part + g * kMaxD + j;
-        const float o = __fadd_rn(__fadd_rn(__fadd_rn(op[0], op[kMaxG * kMaxD]), op[2 * kMaxG * kMaxD]),
-                                  op[3 * kMaxG * kMaxD]);
+        float o = out_part[0][g][j];
+#pragma unroll
+        for (int w = 1; w < NW; w++) o = __fadd_rn(o, out_part[w][g][j]);
         my[(static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2) + 2 + j] = o;
     }
 }
 
-template <bool ROPE>
-void launch_partial(int G, dim3 grid, hipStream_t st, const float* q, uint16_t* kc, uint16_t* vc, const int64_t* pos,
-                    float* part, int nh, int nkv, int d, int cap, float scale, const float* kraw, const float* vraw,
-                    const float* bias, const float* cos_t, const float* sin_t) {
+template <bool ROPE, int NW>
+void launch_partial_nw(int G, dim3 grid, hipStream_t st, const float* q, uint16_t* kc, uint16_t* vc,
+                       const int64_t* pos, float* part, int nh, int nkv, int d, int cap, float scale,
+                       const float* kraw, const float* vraw, const float* bias, const float* cos_t,
+                       const float* sin_t) {
     switch (G) {
-#define Q4_ATTN_CASE(g)                                                                                        \
-    case g:                                                                                                    \
-        hipLaunchKernelGGL((attn_partial_kernel<ROPE, g>), grid, dim3(256), 0, st, q, kc, vc, pos, part, nh, nkv, d, \
-                           cap, scale, kraw, vraw, bias, cos_t, sin_t);                                       \
+#define Q4_ATTN_CASE(g)                                                                                      \
+    case g:                                                                                                  \
+        hipLaunchKernelGGL((attn_partial_kernel<ROPE, g, NW>), grid, dim3(64 * NW), 0, st, q, kc, vc, pos, part, \
+                           nh, nkv, d, cap, scale, kraw, vraw, bias, cos_t, sin_t);                          \
         break;
         Q4_ATTN_CASE(1) Q4_ATTN_CASE(2) Q4_ATTN_CASE(3) Q4_ATTN_CASE(4)
         Q4_ATTN_CASE(5) Q4_ATTN_CASE(6) Q4_ATTN_CASE(7) Q4_ATTN_CASE(8)
 #undef Q4_ATTN_CASE
         default: break;                        // the callers check 1 <= G <= kMaxG
     }
+}
+
+// 8 waves when every wave gets a whole uint4 of the head dimension (d >= 64)
+template <bool ROPE>
+void launch_partial(int G, dim3 grid, hipStream_t st, const float* q, uint16_t* kc, uint16_t* vc, const int64_t* pos,
+                    float* part, int nh, int nkv, int d, int cap, float scale, const float* kraw, const float* vraw,
+                    const float* bias, const float* cos_t, const float* sin_t) {
+    if (d >= 64)
+        launch_partial_nw<ROPE, 8>(G, grid, st, q, kc, vc, pos, part, nh, nkv, d, cap, scale, kraw, vraw, bias,
+                                   cos_t, sin_t);
+    else
+        launch_partial_nw<ROPE, 4>(G, grid, st, q, kc, vc, pos, part, nh, nkv, d, cap, scale, kraw, vraw, bias,
+                                   cos_t, sin_t);
 }
 
 // one workgroup per query head: M = max_c m_c, w_c = e^(m_c - M),
