@@ -429,7 +429,7 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
 template <int BM, int BN, int D, bool EVENG>
 __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
     const uint16_t* __restrict__ xb, const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
-    const uint16_t* __restrict__ bi, float* __restrict__ out, int M, int N, int K, int kt_split) {
+    const uint16_t* __restrict__ bi, float* __restrict__ out, int M, int N, int K, int kt_split, int nb0, int ldo) {
     static_assert(D % 2 == 0, "the LDS buffer of a step is its slot parity");
     extern __shared__ uint4 gemm_lds[];
     uint16_t* As = reinterpret_cast<uint16_t*>(gemm_lds);          // [2][BM][72]
@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);       // wave-uniform
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int m0 = blockIdx.x * BM, n0 = (blockIdx.y + nb0) * BN;
     const int G = K >> 6, wpr = K >> 3;
     const int kt0 = blockIdx.z * kt_split;
     const int nk = G - kt0 < kt_split ? G - kt0 : kt_split;
@@ -586,7 +586,10 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
         }
     }
     // C tile layout: lane l, register v holds row 8*(v/4) + 4*(l/32) + v%4, column l%32
-    float* o = out + static_cast<size_t>(blockIdx.z) * M * N;
+    // out: this split's [M][ldo] block, whose column 0 is column nb0 * BN of the
+    // product (nb0 = 0 and ldo = N: the whole output)
+    float* o = out + static_cast<size_t>(blockIdx.z) * M * ldo;
+    const int c0 = nb0 * BN;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -595,18 +598,21 @@ __global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
             for (int v = 0; v < 16; v++) {
                 const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
                 const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
-                if (row < M && col < N) o[static_cast<size_t>(row) * N + col] = acc[i][j][v];
+                if (row < M && col < N) o[static_cast<size_t>(row) * ldo + (col - c0)] = acc[i][j][v];
             }
 }
 
-// out = sum over the S split-K partials, in split order.
+// out[r][c0 + c] = sum over the S split-K partials part[s][r][c] (r < M,
+// c < W), in split order; out has row stride ldo.
 __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                         long n, int S) {
+                                                         int M, int W, int ldo, int c0, int S) {
+    const long n = static_cast<long>(M) * W;
     const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     if (i < n) {
         float a = part[i];
         for (int s = 1; s < S; s++) a = __fadd_rn(a, part[static_cast<long>(s) * n + i]);
-        out[i] = a;
+        const long r = i / W;
+        out[r * ldo + c0 + (i - r * W)] = a;
     }
 }
 
@@ -1037,7 +1043,7 @@ int dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, void
 
 template <int BM, int BN, bool EVENG, int D = 4>      // D: steps in flight
 int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* xb, float* out,
-                int M, int N, int K, int S, int kt_split, hipStream_t st) {
+                int M, int N, int K, int S, int kt_split, hipStream_t st, int nb0 = 0, int nblocks = -1, int ldo = -1) {
     auto kern = gemm_q4_bf16_kernel<BM, BN, D, EVENG>;
     const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
     static bool attr_set = false;
@@ -1047,10 +1053,26 @@ int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const u
         if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
         attr_set = true;
     }
-    dim3 grid((M + BM - 1) / BM, (N + BN - 1) / BN, S);
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, xb, w, s, b, out, M, N, K, kt_split);
+    dim3 grid((M + BM - 1) / BM, nblocks < 0 ? (N + BN - 1) / BN : nblocks, S);
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, xb, w, s, b, out, M, N, K, kt_split, nb0, ldo < 0 ? N : ldo);
     HIP_TRY(hipGetLastError());
     return 0;
+}
+
+// Workgroups of the prefill GEMM resident per CU (its LDS decides it).
+template <int BM, int BN>
+int gemm_blocks_per_cu() {
+    static int cached = 0;
+    if (!cached) {
+        const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
+        auto kern = gemm_q4_bf16_kernel<BM, BN, 4, true>;
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(lds));
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, lds) != hipSuccess || n < 1) n = 1;
+        cached = n;
+    }
+    return cached;
 }
 
 // The arguments of the norm-prologue entry points: gs 64, n_in in
@@ -1382,26 +1404,63 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
     while (S < 8 && tiles * S < 2L * cus && G / (2 * S) >= 8) S *= 2;
     const int kt_split = (G + S - 1) / S;
     S = (G + kt_split - 1) / kt_split;
+    // A last round of resident workgroups that is at most half full gets its
+    // tiles (the last N-blocks) in a launch of its own, split along K to fill
+    // the round: gate/up at M=512 are 592 tiles of 128 x 128 on 512 slots.
+    const int MB = (m + 127) / 128, NB = (n_out + BN - 1) / BN;
+    int main_nb = NB, rem_nb = 0, S2 = 1, kt2 = G;
+    if (S == 1) {
+        const long P = static_cast<long>(cus) * (BN == 128 ? gemm_blocks_per_cu<128, 128>() : gemm_blocks_per_cu<128, 64>());
+        const long full = (tiles / P) * P;
+        if (full > 0 && tiles > full && tiles - full <= P / 2) {
+            const int nb = static_cast<int>(full / MB);
+            int s2 = static_cast<int>(P / (static_cast<long>(MB) * (NB - nb)));
+            if (s2 > 8) s2 = 8;
+            while (s2 > 1 && G / s2 < 8) --s2;
+            if (s2 >= 2) {
+                main_nb = nb;
+                rem_nb = NB - nb;
+                kt2 = (G + s2 - 1) / s2;
+                S2 = (G + kt2 - 1) / kt2;
+            }
+        }
+    }
+    const int W = rem_nb ? (n_out - main_nb * BN < rem_nb * BN ? n_out - main_nb * BN : rem_nb * BN) : 0;
     const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * n_out;
     if ((rc = ensure_raw(ws->xbf, ws->cap_xbf, mk * 2, st, "prefill"))) return rc;
-    if (S > 1 && (rc = ensure_raw(ws->part, ws->cap_part, S * mn * 4, st, "prefill"))) return rc;
+    const size_t part_bytes = S > 1 ? S * mn * 4 : static_cast<size_t>(S2) * m * W * 4;
+    if (part_bytes && (rc = ensure_raw(ws->part, ws->cap_part, part_bytes, st, "prefill"))) return rc;
     const long n8 = static_cast<long>(mk / 8);
     hipLaunchKernelGGL(x_to_bf16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, st, x,
                        static_cast<uint4*>(ws->xbf), n8);
     HIP_TRY(hipGetLastError());
     const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
-    float* dst = S > 1 ? static_cast<float*>(ws->part) : out;
-    if (G % 2 == 0)
-        rc = BN == 128 ? launch_gemm<128, 128, true>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st)
-                       : launch_gemm<128, 64, true>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st);
-    else
-        rc = BN == 128 ? launch_gemm<128, 128, false>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st)
-                       : launch_gemm<128, 64, false>(w, scales, biases, xb, dst, m, n_out, n_in, S, kt_split, st);
-    if (rc || S == 1) return rc;
-    hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0, st,
-                       static_cast<const float*>(ws->part), out, static_cast<long>(mn), S);
-    HIP_TRY(hipGetLastError());
-    return 0;
+    float* part = static_cast<float*>(ws->part);
+    auto gemm = [&](float* dst, int splits, int kts, int nb0, int nblocks, int ldo) {
+        if (G % 2 == 0)
+            return BN == 128 ? launch_gemm<128, 128, true>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
+                                                           nb0, nblocks, ldo)
+                             : launch_gemm<128, 64, true>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
+                                                          nb0, nblocks, ldo);
+        return BN == 128 ? launch_gemm<128, 128, false>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
+                                                        nb0, nblocks, ldo)
+                         : launch_gemm<128, 64, false>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
+                                                       nb0, nblocks, ldo);
+    };
+    auto ksum = [&](int width, int c0, int splits) -> int {
+        const long n = static_cast<long>(m) * width;
+        hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+                           static_cast<const float*>(part), out, m, width, n_out, c0, splits);
+        HIP_TRY(hipGetLastError());
+        return 0;
+    };
+    if (rem_nb) {
+        if ((rc = gemm(out, 1, G, 0, main_nb, n_out))) return rc;
+        if ((rc = gemm(part, S2, kt2, main_nb, rem_nb, W))) return rc;
+        return ksum(W, main_nb * BN, S2);
+    }
+    if ((rc = gemm(S > 1 ? part : out, S, kt_split, 0, NB, n_out)) || S == 1) return rc;
+    return ksum(n_out, 0, S);
 }
 
 int q4_dequant_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,
