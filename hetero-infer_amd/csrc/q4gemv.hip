@@ -1392,12 +1392,14 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
         if ((rc = current_device(&dev))) return rc;
         ws = &g_dev[dev].ws[st];
     }
-    // tiles: 128 x 128 once they fill the CUs, else 128 x 64; split K in
-    // two while the workgroups do not fill the CUs twice and every split
-    // keeps at least 8 groups of K
+    // tiles: 128 x 128 when split-K (up to 8) can fill the CUs with them,
+    // else 128 x 64.  The A tile (x) is read once per N-block, so the wider
+    // tile halves the bytes of x read (down at M=512: 1.1 GB per call with
+    // 64 columns).  Split K in two while the workgroups do not fill the CUs
+    // twice and every split keeps at least 8 groups of K.
     const int cus = num_cus();
     const long tiles128 = static_cast<long>((m + 127) / 128) * ((n_out + 127) / 128);
-    const int BN = tiles128 >= cus ? 128 : 64;
+    const int BN = tiles128 * 8 >= cus ? 128 : 64;
     const long tiles = static_cast<long>((m + 127) / 128) * ((n_out + BN - 1) / BN);
     const int G = n_in / 64;
     int S = 1;
