@@ -80,6 +80,9 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
     m = 512
     xs = {k: torch.randn((m, k), device=dev) for k in (3584, 18944)}
     outs = {n: torch.empty((m, n), device=dev) for n in (512, 3584, 18944)}
+    # the weights and x come from the default stream; the GEMMs run on a
+    # non-blocking one
+    torch.cuda.synchronize()
     stream = torch.cuda.Stream(device=dev)
     flops = 0
 

@@ -1,0 +1,380 @@
+// Small-M GEMV on the int8 matrix cores (2 <= M <= 8 activation rows, gs 64).
+//
+// The arithmetic is the reference's x86 path of kernel/q4gemv.c:232-301 for
+// every row of x: x quantised to int16 once per row (:244-270), an exact
+// integer dot per group of 64 (:80-111), and per output
+//   acc = acc + fma(scale, xscale * (float)idot, bias * xsum[g])   (:173-180)
+// in ascending group order.  Only the integer dots move to the MFMA; the fp32
+// steps stay in the order above, so the result is bit-identical to the
+// streaming kernel and to the reference.
+//
+// Integer dots.  v_mfma_i32_32x32x32_i8 takes A (32 x 32, int8) from x and
+// B (32 x 32, int8) from the weights.  A row of A is one byte plane of one
+// activation row; the 32 columns of B are 32 weight rows.  xq = 256 * xh + xl
+// with xh the signed high byte and xl the unsigned low byte; A carries
+// xl ^ 0x80 (= xl - 128, a signed byte) and xh, plus two rows of ones, so
+//   idot = D[xl] + 256 * D[xh] + 128 * D[ones]          (exact in int32)
+// Weights are 0..15, already valid signed bytes: the low and high nibbles of
+// each packed word go to two MFMAs (even and odd k), and the A operand holds
+// the matching even/odd bytes of x.  A rows: 0..7 xl of activation rows
+// 0..7, 8..15 xh (loaded), 16 and 20 ones (made in registers), the rest
+// zero, which puts every plane an output needs into the same lane of D.
+//
+// Work split.  A workgroup owns a tile of 32 weight rows (PAIR: 32 gate rows
+// and the same 32 up rows, one A operand for both) and runs S waves over K
+// in windows of 8*S groups, 8 consecutive groups per wave, each wave
+// streaming its groups through a register ring of 8 (the next window's
+// loads are in flight while the window's terms are chained).  Each group's
+// fp32 term goes to an LDS table; after a barrier one lane per (activation
+// row, weight row) adds the window's terms in ascending group order.  The K
+// split keeps enough waves in flight for the 3584-row shapes; the ordered
+// chain keeps it exact.
+//
+// Loads per group and wave: 32 rows x 32 bytes of weights (per matrix), the
+// A operand (the 32 lanes of rows 0..15, 32 bytes each) and the xsum of the
+// lane's four activation rows.  Scales and biases come once per window: the
+// lane's row, 8 groups in 16 bytes, scales in k-half 0 and biases in k-half
+// 1, exchanged across the halves (when the group count is a multiple of 8;
+// else one 2-byte load each per group).
+#pragma once
+
+#include "q4_common.h"
+
+namespace q4k {
+
+constexpr int kMfRing = 8;          // groups per wave and window, and ring slots
+constexpr int kMfArows = 16;        // A rows stored per (group, k-half): xl 0..7, xh 8..15
+
+// x of up to 8 rows, prepared for the small-M MFMA kernel (one workgroup per
+// row slot; slots >= M write zeros).  The fp32 steps are xprep_kernel's:
+//   xa[((g*2 + h)*16 + r)*8 + s]  uint32: A row r, k-half h of group g;
+//                                 s 0..3 even-k bytes of words 4h..4h+3 of
+//                                 the group, 4..7 the odd-k bytes
+//   xsum_t[g*8 + m], xscale[m]
+// The row is staged in LDS by 16-byte loads all issued at once (one memory
+// round trip); amax, the group sums and the quantisation then read LDS.
+constexpr int kMfPrepMaxK = 32768;           // floats of one x row staged in LDS
+__global__ __launch_bounds__(1024) void xprep_mf_kernel(const float* __restrict__ x, int M, int n_in,
+                                                        uint32_t* __restrict__ xa, float* __restrict__ xsum_t,
+                                                        float* __restrict__ xscale_out) {
+    extern __shared__ float4 xrow4[];                            // [n_in / 4]
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int G = n_in >> 6, wpr = n_in >> 3;
+    if (m >= M) {
+        for (int i = tid; i < G * 2 * 8; i += nt) {
+            const int s = i & 7, gh = i >> 3;
+            xa[(static_cast<size_t>(gh) * kMfArows + m) * 8 + s] = 0u;
+            xa[(static_cast<size_t>(gh) * kMfArows + 8 + m) * 8 + s] = 0u;
+        }
+        for (int g = tid; g < G; g += nt) xsum_t[static_cast<size_t>(g) * 8 + m] = 0.0f;
+        if (tid == 0) xscale_out[m] = 1.0f;
+        return;
+    }
+    __shared__ float red[16];
+    __shared__ float s_inv;
+    const float4* xr4 = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * n_in);
+    const int n4 = n_in >> 2;
+
+    // stage the row; amax on the way (kernel/q4gemv.c:258-259, NaN-skipping)
+    float amax = 0.0f;
+    constexpr int kPer = kMfPrepMaxK / 4 / 1024;                // float4 per thread at most
+    float4 v[kPer];
+#pragma unroll
+    for (int r = 0; r < kPer; r++) {
+        const int i = r * nt + tid;
+        v[r] = i < n4 ? xr4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int r = 0; r < kPer; r++) {
+        const int i = r * nt + tid;
+        if (i < n4) {
+            xrow4[i] = v[r];
+            const float a[4] = {v[r].x, v[r].y, v[r].z, v[r].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float t = a[k] < 0 ? -a[k] : a[k];
+                amax = t > amax ? t : amax;
+            }
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        float o = __shfl_xor(amax, off);
+        amax = o > amax ? o : amax;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    const float* xl = reinterpret_cast<const float*>(xrow4);
+    for (int g = tid; g < G; g += nt) {                          // kernel/q4gemv.c:244-248
+        const float4* p = xrow4 + g * 16;
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float4 q = p[i];
+            s = __fadd_rn(s, q.x);
+            s = __fadd_rn(s, q.y);
+            s = __fadd_rn(s, q.z);
+            s = __fadd_rn(s, q.w);
+        }
+        xsum_t[static_cast<size_t>(g) * 8 + m] = s;
+    }
+    if (tid == 0) {
+        float a = 0.0f;
+        for (int i = 0; i < (nt >> 6); i++) a = red[i] > a ? red[i] : a;
+        const float sc = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;   // :260
+        xscale_out[m] = sc;
+        s_inv = __fdiv_rn(1.0f, sc);                                  // :261
+    }
+    __syncthreads();
+    const float inv = s_inv;
+    for (int j = tid; j < wpr; j += nt) {
+        uint32_t le = 0, lo = 0, he = 0, ho = 0;
+#pragma unroll
+        for (int n = 0; n < 8; n++) {
+            const float a = __fmul_rn(xl[8 * j + n], inv);             // :266
+            const float r = a < 0 ? __fsub_rn(a, 0.5f) : __fadd_rn(a, 0.5f);  // :267-268
+            const int32_t q = to_i16_like_x86(r);
+            const uint32_t xlb = static_cast<uint32_t>(q) & 0xFFu;
+            const uint32_t xhb = static_cast<uint32_t>(q >> 8) & 0xFFu;
+            const int sh = 8 * (n >> 1);
+            if (n & 1) { lo |= xlb << sh; ho |= xhb << sh; }
+            else       { le |= xlb << sh; he |= xhb << sh; }
+        }
+        const int g = j >> 3, h = (j >> 2) & 1, wd = j & 3;
+        uint32_t* base = xa + static_cast<size_t>(g * 2 + h) * kMfArows * 8;
+        base[m * 8 + wd] = le ^ 0x80808080u;
+        base[m * 8 + 4 + wd] = lo ^ 0x80808080u;
+        base[(8 + m) * 8 + wd] = he;
+        base[(8 + m) * 8 + 4 + wd] = ho;
+    }
+}
+
+template <bool PAIR>
+struct MfSlot {
+    uint4 w[PAIR ? 2 : 1];  // 16 bytes of the lane's weight row (per matrix): words 4h..4h+3 of the group
+    uint4 xe, xo;           // A operand, even and odd k
+    float4 xs;              // xsum of activation rows 4h..4h+3
+    uint32_t s[PAIR ? 2 : 1], b[PAIR ? 2 : 1];   // per-group scale/bias (fp16, low half) without SB8
+};
+
+typedef int mf_v4i __attribute__((ext_vector_type(4)));
+typedef int mf_v16i __attribute__((ext_vector_type(16)));
+
+// Weight-side arguments: one matrix, or (PAIR) gate in 0 and up in 1.
+struct MfMats {
+    const uint32_t* w[2];
+    const uint16_t* s[2];
+    const uint16_t* b[2];
+};
+
+__device__ __forceinline__ mf_v4i lo_nibbles(const uint4& w) {
+    return {static_cast<int>(w.x & 0x0F0F0F0Fu), static_cast<int>(w.y & 0x0F0F0F0Fu),
+            static_cast<int>(w.z & 0x0F0F0F0Fu), static_cast<int>(w.w & 0x0F0F0F0Fu)};
+}
+__device__ __forceinline__ mf_v4i hi_nibbles(const uint4& w) {
+    return {static_cast<int>((w.x >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.y >> 4) & 0x0F0F0F0Fu),
+            static_cast<int>((w.z >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.w >> 4) & 0x0F0F0F0Fu)};
+}
+
+// fp16 k of the 8 packed in a uint4 (k = 0..7, wave-uniform)
+__device__ __forceinline__ uint32_t half_of(const uint4& v, int k) {
+    const uint32_t d = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
+    return (k & 1) ? d >> 16 : d & 0xFFFFu;
+}
+
+// out[m][row] for m < M (PAIR: h[m][row] = SiLU(gate) * up), row stride ldo.
+// Grid: one workgroup per tile of 32 rows; block: 64 * S threads (S = 4 or
+// 8: the ring takes about 150-200 registers, so at most two waves per SIMD).
+// SB8: the group count is a multiple of 8 (scales/biases by window).
+template <bool PAIR, int S, bool SB8>
+__global__ __launch_bounds__(64 * S) void gemv_mfma_kernel(MfMats mt, int N, int K, int M,
+                                                         const uint32_t* __restrict__ xa,
+                                                         const float* __restrict__ xsum_t,
+                                                         const float* __restrict__ xscale,
+                                                         float* __restrict__ out, int ldo) {
+    constexpr int NM = PAIR ? 2 : 1;
+    static_assert(S == 4 || S == 8, "the chain lanes are waves 0..3; the ring fits two waves per SIMD");
+    constexpr int GW = kMfRing * S, GWp = GW + 4;
+    extern __shared__ float tbl[];                   // [NM][8][32][GWp] terms of one window
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = K >> 6;
+    const int nwin = (G + GW - 1) / GW;
+    const uint32_t rowb = static_cast<uint32_t>(K) >> 1;          // bytes of a weight row
+
+    // the lane's weight row; rows past N read 0 and are not stored
+    const int row = blockIdx.x * 32 + j;
+    const bool live = row < N;
+    __amdgpu_buffer_rsrc_t rw[NM], rs[NM], rb[NM];
+#pragma unroll
+    for (int k = 0; k < NM; k++) {
+        rw[k] = buf_rsrc(mt.w[k], static_cast<uint32_t>(N) * rowb);
+        rs[k] = buf_rsrc(mt.s[k], static_cast<uint32_t>(N) * G * 2u);
+        rb[k] = buf_rsrc(mt.b[k], static_cast<uint32_t>(N) * G * 2u);
+    }
+    const __amdgpu_buffer_rsrc_t rx = buf_rsrc(xa, static_cast<uint32_t>(G) * 2u * kMfArows * 32u);
+    const __amdgpu_buffer_rsrc_t rxs = buf_rsrc(xsum_t, static_cast<uint32_t>(G) * 32u);
+    // per-lane offsets at group 0, each below 2^31 (the host checks the
+    // matrix sizes), and a dead bit OR-ed in after the group's offset is
+    // added: rows past N and the A rows not stored read 0 without an access.
+    // A group past the last one adds 2^31 itself; the sum of two in-range
+    // parts never reaches 2^32.
+    const uint32_t rowc = live ? static_cast<uint32_t>(row) : 0u;
+    const uint32_t ow = rowc * rowb + static_cast<uint32_t>(h) * 16u;
+    const uint32_t og = rowc * static_cast<uint32_t>(G) * 2u;
+    const uint32_t dead = live ? 0u : kOutOfRange;
+    const uint32_t ox = static_cast<uint32_t>(h * kMfArows + (j & 15)) * 32u;
+    const uint32_t deadx = j < kMfArows ? 0u : kOutOfRange;
+    const uint32_t onesv = (j == 16 || j == 20) ? 0x01010101u : 0u;   // A rows 16 and 20
+    const uint32_t oxs = static_cast<uint32_t>(h) * 16u;
+    auto load = [&](MfSlot<PAIR>& sl, int g) {
+        const bool gv = g < G;                                       // uniform
+        const uint32_t dw = gv ? static_cast<uint32_t>(g) * 32u : kOutOfRange;
+        const uint32_t dg = gv ? static_cast<uint32_t>(g) * 2u : kOutOfRange;
+        const uint32_t dx = gv ? static_cast<uint32_t>(g) * (2u * kMfArows * 32u) : kOutOfRange;
+        const uint32_t dxs = gv ? static_cast<uint32_t>(g) * 32u : kOutOfRange;
+        __builtin_amdgcn_sched_barrier(0);
+        // default cache policy: the 32 bytes a lane reads share their
+        // 128-byte line with the row's next three groups, read by the next
+        // three loads (non-temporal loads fetched the line again each time)
+#pragma unroll
+        for (int k = 0; k < NM; k++)
+            sl.w[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw[k], (ow + dw) | dead, 0, 0));
+        if constexpr (!SB8) {
+#pragma unroll
+            for (int k = 0; k < NM; k++) {
+                sl.s[k] = __builtin_amdgcn_raw_buffer_load_b16(rs[k], (og + dg) | dead, 0, 0);
+                sl.b[k] = __builtin_amdgcn_raw_buffer_load_b16(rb[k], (og + dg) | dead, 0, 0);
+            }
+        }
+        sl.xe = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (ox + dx) | deadx, 0, 0));
+        sl.xo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (ox + dx + 16u) | deadx, 0, 0));
+        sl.xs = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rxs, oxs + dxs, 0, 0));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // SB8: 8 groups of scales (k-half 0) or biases (k-half 1) of the lane's
+    // row in 16 bytes, from the window's first group of the wave
+    auto load_sb = [&](uint4 (&sb)[NM], int g) {
+        const bool gv = g < G;                                       // uniform
+        const uint32_t dg = gv ? static_cast<uint32_t>(g) * 2u : kOutOfRange;
+        __builtin_amdgcn_sched_barrier(0);
+        // both loads on every lane, the other half's through a dead offset:
+        // no divergent branch around a load
+        const uint32_t ds = h == 0 ? dead : kOutOfRange, db = h == 0 ? kOutOfRange : dead;
+#pragma unroll
+        for (int k = 0; k < NM; k++) {
+            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs[k], (og + dg) | ds, 0, 0));
+            const uint4 c = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb[k], (og + dg) | db, 0, 0));
+            sb[k] = make_uint4(a.x | c.x, a.y | c.y, a.z | c.z, a.w | c.w);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // xscale of the lane's four activation rows (4h .. 4h+3): the eight
+    // values by scalar loads (uniform addresses), picked per k-half.  A
+    // vector load here would be one more vector-memory result the loop
+    // header's wait accounting merges with the ring, and the first group of
+    // every window then waited for the whole ring.
+    float xsc[4];
+    {
+        float xa8[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) xa8[k] = xscale[k];
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++) xsc[mm] = h ? xa8[4 + mm] : xa8[mm];
+    }
+
+    MfSlot<PAIR> ring[kMfRing];
+    uint4 sb_next[NM];
+    const int g_wave = wave * kMfRing;                               // the wave's first group of a window
+    if constexpr (SB8) load_sb(sb_next, g_wave);
+#pragma unroll
+    for (int d = 0; d < kMfRing; d++) load(ring[d], g_wave + d);
+
+    // chain lanes: waves 0..3, activation row 2*wave + h, weight row j
+    const int cm = 2 * wave + h;
+    const bool chain = wave < 4 && 2 * wave < M;                     // uniform
+    float acc[NM];
+#pragma unroll
+    for (int k = 0; k < NM; k++) acc[k] = 0.0f;
+    for (int t = 0; t < nwin; t++) {
+        const int g0 = t * GW + g_wave;
+        // this window's scales and biases: own half plus the other half's
+        uint4 sv[NM], bv[NM];
+        if constexpr (SB8) {
+#pragma unroll
+            for (int k = 0; k < NM; k++) {
+                uint4 other;
+                other.x = __shfl_xor(sb_next[k].x, 32);
+                other.y = __shfl_xor(sb_next[k].y, 32);
+                other.z = __shfl_xor(sb_next[k].z, 32);
+                other.w = __shfl_xor(sb_next[k].w, 32);
+                sv[k] = h == 0 ? sb_next[k] : other;
+                bv[k] = h == 0 ? other : sb_next[k];
+            }
+            load_sb(sb_next, g0 + GW);
+        }
+#pragma unroll
+        for (int d = 0; d < kMfRing; d++) {
+            const MfSlot<PAIR>& sl = ring[d];
+            const uint4 xe = make_uint4(sl.xe.x | onesv, sl.xe.y | onesv, sl.xe.z | onesv, sl.xe.w | onesv);
+            const uint4 xo = make_uint4(sl.xo.x | onesv, sl.xo.y | onesv, sl.xo.z | onesv, sl.xo.w | onesv);
+            const mf_v4i ae = __builtin_bit_cast(mf_v4i, xe), ao = __builtin_bit_cast(mf_v4i, xo);
+            const float xs4[4] = {sl.xs.x, sl.xs.y, sl.xs.z, sl.xs.w};
+            const int gl = wave * kMfRing + d;                       // group within the window
+#pragma unroll
+            for (int k = 0; k < NM; k++) {
+                mf_v16i D = {};
+                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(ae, lo_nibbles(sl.w[k]), D, 0, 0, 0);
+                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao, hi_nibbles(sl.w[k]), D, 0, 0, 0);
+                uint32_t sraw, braw;
+                if constexpr (SB8) {
+                    sraw = half_of(sv[k], d);
+                    braw = half_of(bv[k], d);
+                } else {
+                    sraw = sl.s[k];
+                    braw = sl.b[k];
+                }
+                const float sc = h2f(static_cast<uint16_t>(sraw)), bi = h2f(static_cast<uint16_t>(braw));
+                float* tk = tbl + k * (256 * GWp);
+#pragma unroll
+                for (int mm = 0; mm < 4; mm++) {
+                    // kernel/q4gemv.c:173-180 with xq = 256 xh + (xl' + 128)
+                    const int32_t idot = D[mm] + D[4 + mm] * 256 + D[8] * 128;
+                    const float dot = __fmul_rn(xsc[mm], static_cast<float>(idot));
+                    const float bx = __fmul_rn(bi, xs4[mm]);
+                    tk[((4 * h + mm) * 32 + j) * GWp + gl] = __fmaf_rn(sc, dot, bx);
+                }
+            }
+            load(ring[d], g0 + GW + d);                              // the next window's group
+        }
+        __syncthreads();
+        if (chain) {
+            const int n = G - t * GW < GW ? G - t * GW : GW;
+#pragma unroll
+            for (int k = 0; k < NM; k++) {
+                const float* tp = tbl + k * (256 * GWp) + (cm * 32 + j) * GWp;
+                float a = acc[k];
+                int g = 0;
+                for (; g + 4 <= n; g += 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(tp + g);
+                    a = __fadd_rn(a, v.x);
+                    a = __fadd_rn(a, v.y);
+                    a = __fadd_rn(a, v.z);
+                    a = __fadd_rn(a, v.w);
+                }
+                for (; g < n; g++) a = __fadd_rn(a, tp[g]);
+                acc[k] = a;
+            }
+        }
+        __syncthreads();
+    }
+    if (!chain || !live || cm >= M) return;
+    if constexpr (PAIR)
+        out[static_cast<size_t>(cm) * ldo + row] = silu_mul(acc[0], acc[1]);
+    else
+        out[static_cast<size_t>(cm) * ldo + row] = acc[0];
+}
+
+}  // namespace q4k

@@ -40,6 +40,7 @@
 #include <vector>
 
 #include "q4_stream.h"
+#include "q4_mfma_m.h"
 #include "q4decode.h"
 
 namespace q4k {
@@ -882,9 +883,80 @@ int gemv_split(const uint32_t* w, const uint16_t* s, const uint16_t* b, const fl
     return 0;
 }
 
-// GEMV of m (<= kMaxM) rows already on the device: fused when possible.
+template <bool PAIR, int S, bool SB8>
+int launch_mfma_k(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace& ws, float* out, int tiles,
+                  hipStream_t st) {
+    auto kern = q4k::gemv_mfma_kernel<PAIR, S, SB8>;
+    constexpr size_t lds = (PAIR ? 2 : 1) * 256 * (q4k::kMfRing * S + 4) * sizeof(float);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * S), lds, st, mt, n, n_in, m,
+                       reinterpret_cast<const uint32_t*>(ws.planes), ws.xsum, ws.xscale, out, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q4_EHIP, "mfma gemv launch: %s", hipGetErrorString(e));
+    return 1;
+}
+
+template <bool PAIR, bool SB8>
+int launch_mfma_s(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace& ws, float* out, hipStream_t st) {
+    // 8 waves per tile while the tiles do not fill the CUs twice (the
+    // 3584-row shapes: 112 tiles), else 4
+    const int tiles = (n + 31) / 32;
+    return tiles < 2 * num_cus() ? launch_mfma_k<PAIR, 8, SB8>(mt, n, n_in, m, ws, out, tiles, st)
+                                 : launch_mfma_k<PAIR, 4, SB8>(mt, n, n_in, m, ws, out, tiles, st);
+}
+
+// Rows of x from which the matrix-core path is used (measured on the q_proj
+// and MLP shapes of Qwen2.5-7B: below it the streaming kernel is faster).
+constexpr int kMfMinRows = 5;
+
+// Small-M GEMV on the int8 matrix cores (q4_mfma_m.h): kMfMinRows <= m <= kMaxM,
+// gs 64, n_in <= 32768, x 16-byte aligned, every byte offset into the
+// matrix below 2^31.  PAIR: mt holds gate and up, out receives
+// SiLU(gate) * up.  x is prepared into the stream's workspace by
+// xprep_mf_kernel.  Returns 1 if it launched, 0 if the shape is not one it
+// takes, <0 on error.
+int gemv_mfma(const q4k::MfMats& mt, bool pair, const float* x, float* out, int m, int n, int n_in, int gs,
+              hipStream_t st, Workspace& ws) {
+    if (m < kMfMinRows || m > kMaxM || gs != 64 || n_in <= 0 || n <= 0 || n_in > q4k::kMfPrepMaxK) return 0;
+    if (reinterpret_cast<uintptr_t>(x) & 15) return 0;
+    const long G = n_in / 64;
+    if (static_cast<long>(n) * (n_in / 2) >= (1L << 31) || static_cast<long>(n) * G * 2 >= (1L << 31)) return 0;
+    int rc = ensure_ws(ws, st, static_cast<size_t>(G) * 2 * q4k::kMfArows * 2, static_cast<size_t>(G) * 8);
+    if (rc) return rc;
+    static bool prep_attr = false;
+    if (!prep_attr) {
+        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(q4k::xprep_mf_kernel),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(q4k::kMfPrepMaxK * sizeof(float)));
+        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
+        prep_attr = true;
+    }
+    hipLaunchKernelGGL(q4k::xprep_mf_kernel, dim3(kMaxM), dim3(1024), static_cast<size_t>(n_in) * sizeof(float), st,
+                       x, m, n_in, reinterpret_cast<uint32_t*>(ws.planes), ws.xsum, ws.xscale);
+    HIP_TRY(hipGetLastError());
+    const bool sb8 = G % 8 == 0;
+    if (pair) return sb8 ? launch_mfma_s<true, true>(mt, n, n_in, m, ws, out, st)
+                         : launch_mfma_s<true, false>(mt, n, n_in, m, ws, out, st);
+    return sb8 ? launch_mfma_s<false, true>(mt, n, n_in, m, ws, out, st)
+               : launch_mfma_s<false, false>(mt, n, n_in, m, ws, out, st);
+}
+
+// GEMV of m (<= kMaxM) rows already on the device: the matrix cores for
+// kMfMinRows..8 rows, else fused when possible.
 int gemv_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
               float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws) {
+    if (m >= kMfMinRows) {
+        const q4k::MfMats mt{{w, w}, {s, s}, {b, b}};
+        const int rc = gemv_mfma(mt, false, x, out, m, n_out, n_in, gs, st, ws);
+        if (rc < 0) return rc;
+        if (rc == 1) return 0;
+    }
     MatList ml{};
     ml.w[0] = w; ml.s[0] = s; ml.b[0] = b; ml.out[0] = out; ml.n_out[0] = n_out;
     ml.row_begin[0] = 0;
@@ -1219,7 +1291,7 @@ int q4_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const
     if (m == 0) return 0;
     if (!x) return fail(Q4_EARG, "null x");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (m <= kMaxM) {
+    if (m < kMfMinRows) {  // one grouped streaming launch; more rows: a matrix-core launch per matrix
         MatList ml{};
         ml.row_begin[0] = 0;
         for (int k = 0; k < kMaxMats; k++) {
@@ -1268,7 +1340,19 @@ int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const ui
         ml.count = 2;
         ml.mrows = mm;
         int done = 0;
-        if (gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
+        if (mm >= kMfMinRows) {
+            Workspace* ws;
+            {
+                std::lock_guard<std::mutex> lock(g_mu);
+                int dev;
+                if ((rc = current_device(&dev))) return rc;
+                ws = &g_dev[dev].ws[st];
+            }
+            const q4k::MfMats mt{{gate_w, up_w}, {gate_s, up_s}, {gate_b, up_b}};
+            done = gemv_mfma(mt, true, xm, hm, mm, n_inter, n_in, gs, st, *ws);
+            if (done < 0) return done;
+        }
+        if (!done && gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
             (n_in / 8 + kChunkWords - 1) / kChunkWords <= 16) {
             done = mm == 1   ? launch_stream<1, true>(ml, xm, n_in, st)
                    : mm == 2 ? launch_stream<2, true>(ml, xm, n_in, st)

@@ -165,14 +165,24 @@ class GpuStage:
                              self.s0, self.hist.numel(), st), "argmax")
 
     # -- driving --------------------------------------------------------------
+    def _eager_step(self):
+        """One step on the stage's stream, ordered after the caller's stream
+        (the state set up or copied there: token, caches, clones) and before
+        its later work (a read of the token).  torch's side streams do not
+        synchronise with the default stream by themselves."""
+        cur = self.torch.cuda.current_stream()
+        self.stream.wait_stream(cur)
+        with self.torch.cuda.stream(self.stream):
+            self._step()
+        cur.wait_stream(self.stream)
+
     def capture(self):
         """Run one step eagerly (sizes every workspace), restore the state and
         capture the step as a HIP graph."""
         torch = self.torch
         tok0, pos0 = self.tok.clone(), self.pos.clone()
         caches = [(L["k_cache"].clone(), L["v_cache"].clone()) for L in self.layers]
-        with torch.cuda.stream(self.stream):
-            self._step()
+        self._eager_step()
         torch.cuda.synchronize()
         self.tok.copy_(tok0)
         self.pos.copy_(pos0)
@@ -206,8 +216,7 @@ class GpuStage:
     def step(self) -> int:
         """One decode step (graph replay once captured); returns the greedy token."""
         if self.graph is None:
-            with self.torch.cuda.stream(self.stream):
-                self._step()
+            self._eager_step()
         else:
             self.graph.replay()
         return int(self.tok.item())

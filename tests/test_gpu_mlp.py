@@ -78,3 +78,22 @@ def test_gate_up_silu_sign_structure():
     u = orc.gemv(*un, x[0], 64)
     nz = (g != 0) & (u != 0)
     assert np.array_equal(np.sign(h[nz]), np.sign(g[nz]) * np.sign(u[nz]))
+
+
+@pytest.mark.parametrize("hidden,inter", [(1024, 2816), (3584, 18944), (512, 200), (4096, 40)])
+def test_gate_up_silu_rows_match_one_row_launches(hidden, inter):
+    """Several rows (the matrix-core path) against each row on its own (the
+    streaming path): the same gate/up dots and the same SiLU*mul, so h is
+    bit-identical; inter 200 and 40 leave a partial 16-row tile."""
+    import torch
+    (_, gt), (_, ut) = mats(620, inter, hidden), mats(621, inter, hidden)
+    x = synth.activations(622, 8, hidden)
+    tx = tensors(x)[0]
+    ones = [q4.gate_up_silu_dev(gt, ut, tx[r:r + 1].contiguous()).cpu().numpy()[0] for r in range(8)]
+    for m in (2, 3, 5, 8):
+        print(f"gate/up rows hidden={hidden} inter={inter} m={m}", flush=True)
+        h = q4.gate_up_silu_dev(gt, ut, tx[:m].contiguous())
+        torch.cuda.synchronize()
+        h = h.cpu().numpy()
+        for r in range(m):
+            assert np.array_equal(h[r].view(np.uint32), ones[r].view(np.uint32)), f"m={m} row {r}"
