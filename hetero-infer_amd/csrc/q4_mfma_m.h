@@ -30,9 +30,12 @@
 // split keeps enough waves in flight for the 3584-row shapes; the ordered
 // chain keeps it exact.
 //
-// Loads per group and wave: 32 rows x 32 bytes of weights (per matrix), the
-// A operand (the 32 lanes of rows 0..15, 32 bytes each) and the xsum of the
-// lane's four activation rows.  Scales and biases come once per window: the
+// Loads per pair of groups and wave: per matrix two loads of 16 rows x 64
+// contiguous bytes (the two groups of each row; 32-byte pieces per row made
+// twice the L2 requests), turned into the B operands of the two groups by
+// v_permlane16_swap and v_permlane32_swap; per group the A operand (the 32
+// lanes of rows 0..15, 32 bytes each) and the xsum of the lane's four
+// activation rows.  Scales and biases come once per window: the
 // lane's row, 8 groups in 16 bytes, scales in k-half 0 and biases in k-half
 // 1, exchanged across the halves (when the group count is a multiple of 8;
 // else one 2-byte load each per group).
@@ -42,7 +45,7 @@
 
 namespace q4k {
 
-constexpr int kMfRing = 8;          // groups per wave and window, and ring slots
+constexpr int kMfRing = 8;          // groups per wave and window (ring: 4 slots of 2 groups)
 constexpr int kMfArows = 16;        // A rows stored per (group, k-half): xl 0..7, xh 8..15
 
 // x of up to 8 rows, prepared for the small-M MFMA kernel (one workgroup per
@@ -149,12 +152,14 @@ __global__ __launch_bounds__(1024) void xprep_mf_kernel(const float* __restrict_
     }
 }
 
+// One ring slot: a pair of consecutive groups.
 template <bool PAIR>
 struct MfSlot {
-    uint4 w[PAIR ? 2 : 1];  // 16 bytes of the lane's weight row (per matrix): words 4h..4h+3 of the group
-    uint4 xe, xo;           // A operand, even and odd k
-    float4 xs;              // xsum of activation rows 4h..4h+3
-    uint32_t s[PAIR ? 2 : 1], b[PAIR ? 2 : 1];   // per-group scale/bias (fp16, low half) without SB8
+    uint4 w[PAIR ? 2 : 1][2];   // per matrix: rows 0..15 and 16..31 of the tile, 64 bytes of each row
+                                //   (the pair's two groups) over four lanes; permuted into B at use
+    uint4 xe[2], xo[2];         // per group: A operand, even and odd k
+    float4 xs[2];               // per group: xsum of activation rows 4h..4h+3
+    uint32_t s[PAIR ? 2 : 1][2], b[PAIR ? 2 : 1][2];   // per matrix and group without SB8 (fp16, low half)
 };
 
 typedef int mf_v4i __attribute__((ext_vector_type(4)));
@@ -176,6 +181,17 @@ __device__ __forceinline__ mf_v4i hi_nibbles(const uint4& w) {
             static_cast<int>((w.z >> 4) & 0x0F0F0F0Fu), static_cast<int>((w.w >> 4) & 0x0F0F0F0Fu)};
 }
 
+// [a0 a1 a2 a3], [b0 b1 b2 b3] (quarters of 16 lanes) -> [a0 b0 a1 b1],
+// [a2 b2 a3 b3]: the odd quarters of the first swap with the even quarters
+// of the second, then the upper halves of the first with the lower halves
+// of the second.
+__device__ __forceinline__ void pair_permute(uint32_t i0, uint32_t i1, uint32_t& b0, uint32_t& b1) {
+    const auto pq = __builtin_amdgcn_permlane16_swap(i0, i1, false, false);    // [a0 b0 a2 b2], [a1 b1 a3 b3]
+    const auto r = __builtin_amdgcn_permlane32_swap(pq[0], pq[1], false, false);
+    b0 = r[0];
+    b1 = r[1];
+}
+
 // fp16 k of the 8 packed in a uint4 (k = 0..7, wave-uniform)
 __device__ __forceinline__ uint32_t half_of(const uint4& v, int k) {
     const uint32_t d = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
@@ -186,7 +202,9 @@ __device__ __forceinline__ uint32_t half_of(const uint4& v, int k) {
 // Grid: one workgroup per tile of 32 rows; block: 64 * S threads (S = 4 or
 // 8: the ring takes about 150-200 registers, so at most two waves per SIMD).
 // SB8: the group count is a multiple of 8 (scales/biases by window).
-template <bool PAIR, int S, bool SB8>
+// TR: weight rows per tile, 32, or 16 (B columns 16..31 dead) to spread a
+// matrix of few rows over twice the workgroups.
+template <bool PAIR, int S, bool SB8, int TR>
 __global__ __launch_bounds__(64 * S) void gemv_mfma_kernel(MfMats mt, int N, int K, int M,
                                                          const uint32_t* __restrict__ xa,
                                                          const float* __restrict__ xsum_t,
@@ -194,8 +212,12 @@ __global__ __launch_bounds__(64 * S) void gemv_mfma_kernel(MfMats mt, int N, int
                                                          float* __restrict__ out, int ldo) {
     constexpr int NM = PAIR ? 2 : 1;
     static_assert(S == 4 || S == 8, "the chain lanes are waves 0..3; the ring fits two waves per SIMD");
-    constexpr int GW = kMfRing * S, GWp = GW + 4;
-    extern __shared__ float tbl[];                   // [NM][8][32][GWp] terms of one window
+    constexpr int GW = kMfRing * S;
+    // terms of one window, [NM][GW][8 activation rows][32 weight rows]: a
+    // term store (fixed group and row of x) and a chain load (fixed group)
+    // touch 32 consecutive floats per half wave, so no bank conflict past
+    // the two halves
+    extern __shared__ float tbl[];
     const int tid = threadIdx.x;
     const int lane = tid & 63, j = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -204,8 +226,9 @@ __global__ __launch_bounds__(64 * S) void gemv_mfma_kernel(MfMats mt, int N, int
     const uint32_t rowb = static_cast<uint32_t>(K) >> 1;          // bytes of a weight row
 
     // the lane's weight row; rows past N read 0 and are not stored
-    const int row = blockIdx.x * 32 + j;
-    const bool live = row < N;
+    static_assert(TR == 32 || (TR == 16 && !PAIR), "16-row tiles for one matrix");
+    const int row = blockIdx.x * TR + j;
+    const bool live = row < N && j < TR;
     __amdgpu_buffer_rsrc_t rw[NM], rs[NM], rb[NM];
 #pragma unroll
     for (int k = 0; k < NM; k++) {
@@ -220,37 +243,54 @@ __global__ __launch_bounds__(64 * S) void gemv_mfma_kernel(MfMats mt, int N, int
     // added: rows past N and the A rows not stored read 0 without an access.
     // A group past the last one adds 2^31 itself; the sum of two in-range
     // parts never reaches 2^32.
+    // Weight loads: lane l reads row (l % 16) (+16 for the second load) at
+    // byte 16 * (l / 16) of the pair's 64 bytes.
+    const int lrow = blockIdx.x * TR + (lane & 15);
+    const uint32_t olw = static_cast<uint32_t>(lrow < N ? lrow : 0) * rowb + static_cast<uint32_t>(lane >> 4) * 16u;
+    const uint32_t deadw0 = lrow < N ? 0u : kOutOfRange, deadw1 = lrow + 16 < N ? 0u : kOutOfRange;
+    const uint32_t row16 = 16u * rowb;
     const uint32_t rowc = live ? static_cast<uint32_t>(row) : 0u;
-    const uint32_t ow = rowc * rowb + static_cast<uint32_t>(h) * 16u;
     const uint32_t og = rowc * static_cast<uint32_t>(G) * 2u;
     const uint32_t dead = live ? 0u : kOutOfRange;
     const uint32_t ox = static_cast<uint32_t>(h * kMfArows + (j & 15)) * 32u;
     const uint32_t deadx = j < kMfArows ? 0u : kOutOfRange;
     const uint32_t onesv = (j == 16 || j == 20) ? 0x01010101u : 0u;   // A rows 16 and 20
     const uint32_t oxs = static_cast<uint32_t>(h) * 16u;
+
+    // slot of groups (g, g + 1), g even
     auto load = [&](MfSlot<PAIR>& sl, int g) {
         const bool gv = g < G;                                       // uniform
         const uint32_t dw = gv ? static_cast<uint32_t>(g) * 32u : kOutOfRange;
-        const uint32_t dg = gv ? static_cast<uint32_t>(g) * 2u : kOutOfRange;
-        const uint32_t dx = gv ? static_cast<uint32_t>(g) * (2u * kMfArows * 32u) : kOutOfRange;
-        const uint32_t dxs = gv ? static_cast<uint32_t>(g) * 32u : kOutOfRange;
         __builtin_amdgcn_sched_barrier(0);
-        // default cache policy: the 32 bytes a lane reads share their
-        // 128-byte line with the row's next three groups, read by the next
-        // three loads (non-temporal loads fetched the line again each time)
+        // default cache policy: the 64 bytes a lane group reads share their
+        // 128-byte line with the row's next pair, read by the next slot
 #pragma unroll
-        for (int k = 0; k < NM; k++)
-            sl.w[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw[k], (ow + dw) | dead, 0, 0));
-        if constexpr (!SB8) {
-#pragma unroll
-            for (int k = 0; k < NM; k++) {
-                sl.s[k] = __builtin_amdgcn_raw_buffer_load_b16(rs[k], (og + dg) | dead, 0, 0);
-                sl.b[k] = __builtin_amdgcn_raw_buffer_load_b16(rb[k], (og + dg) | dead, 0, 0);
-            }
+        for (int k = 0; k < NM; k++) {
+            sl.w[k][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw[k], (olw + dw) | deadw0, 0, 0));
+            if constexpr (TR == 32)
+                sl.w[k][1] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rw[k], (olw + row16 + dw) | deadw1, 0, 0));
+            else
+                sl.w[k][1] = make_uint4(0u, 0u, 0u, 0u);
         }
-        sl.xe = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (ox + dx) | deadx, 0, 0));
-        sl.xo = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (ox + dx + 16u) | deadx, 0, 0));
-        sl.xs = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rxs, oxs + dxs, 0, 0));
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const bool ge = g + e < G;                               // uniform
+            const uint32_t dg = ge ? static_cast<uint32_t>(g + e) * 2u : kOutOfRange;
+            const uint32_t dx = ge ? static_cast<uint32_t>(g + e) * (2u * kMfArows * 32u) : kOutOfRange;
+            const uint32_t dxs = ge ? static_cast<uint32_t>(g + e) * 32u : kOutOfRange;
+            if constexpr (!SB8) {
+#pragma unroll
+                for (int k = 0; k < NM; k++) {
+                    sl.s[k][e] = __builtin_amdgcn_raw_buffer_load_b16(rs[k], (og + dg) | dead, 0, 0);
+                    sl.b[k][e] = __builtin_amdgcn_raw_buffer_load_b16(rb[k], (og + dg) | dead, 0, 0);
+                }
+            }
+            sl.xe[e] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (ox + dx) | deadx, 0, 0));
+            sl.xo[e] = __builtin_bit_cast(uint4,
+                                          __builtin_amdgcn_raw_buffer_load_b128(rx, (ox + dx + 16u) | deadx, 0, 0));
+            sl.xs[e] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rxs, oxs + dxs, 0, 0));
+        }
         __builtin_amdgcn_sched_barrier(0);
     };
     // SB8: 8 groups of scales (k-half 0) or biases (k-half 1) of the lane's
@@ -278,19 +318,21 @@ __global__ __launch_bounds__(64 * S) void gemv_mfma_kernel(MfMats mt, int N, int
     // every window then waited for the whole ring.
     float xsc[4];
     {
-        float xa8[8];
+        // a bit mask, not a select: a select of the two loads became one
+        // load at a per-lane index, i.e. an array in scratch memory
+        const uint32_t hm = 0u - static_cast<uint32_t>(h);
 #pragma unroll
-        for (int k = 0; k < 8; k++) xa8[k] = xscale[k];
-#pragma unroll
-        for (int mm = 0; mm < 4; mm++) xsc[mm] = h ? xa8[4 + mm] : xa8[mm];
+        for (int mm = 0; mm < 4; mm++)
+            xsc[mm] = __uint_as_float((__float_as_uint(xscale[4 + mm]) & hm) | (__float_as_uint(xscale[mm]) & ~hm));
     }
 
-    MfSlot<PAIR> ring[kMfRing];
+    constexpr int kSlots = kMfRing / 2;
+    MfSlot<PAIR> ring[kSlots];
     uint4 sb_next[NM];
     const int g_wave = wave * kMfRing;                               // the wave's first group of a window
     if constexpr (SB8) load_sb(sb_next, g_wave);
 #pragma unroll
-    for (int d = 0; d < kMfRing; d++) load(ring[d], g_wave + d);
+    for (int d = 0; d < kSlots; d++) load(ring[d], g_wave + 2 * d);
 
     // chain lanes: waves 0..3, activation row 2*wave + h, weight row j
     const int cm = 2 * wave + h;
@@ -316,55 +358,77 @@ __global__ __launch_bounds__(64 * S) void gemv_mfma_kernel(MfMats mt, int N, int
             load_sb(sb_next, g0 + GW);
         }
 #pragma unroll
-        for (int d = 0; d < kMfRing; d++) {
+        for (int d = 0; d < kSlots; d++) {
             const MfSlot<PAIR>& sl = ring[d];
-            const uint4 xe = make_uint4(sl.xe.x | onesv, sl.xe.y | onesv, sl.xe.z | onesv, sl.xe.w | onesv);
-            const uint4 xo = make_uint4(sl.xo.x | onesv, sl.xo.y | onesv, sl.xo.z | onesv, sl.xo.w | onesv);
-            const mf_v4i ae = __builtin_bit_cast(mf_v4i, xe), ao = __builtin_bit_cast(mf_v4i, xo);
-            const float xs4[4] = {sl.xs.x, sl.xs.y, sl.xs.z, sl.xs.w};
-            const int gl = wave * kMfRing + d;                       // group within the window
+            // B operands of the slot's two groups: from [a0 a1 a2 a3] (rows
+            // 0..15) and [b0 b1 b2 b3] (rows 16..31), quarters of 16 lanes,
+            // to [a0 b0 a1 b1] (first group) and [a2 b2 a3 b3] (second)
+            mf_v4i bw[NM][2][2];                                     // [matrix][group][even, odd k]
 #pragma unroll
             for (int k = 0; k < NM; k++) {
-                mf_v16i D = {};
-                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(ae, lo_nibbles(sl.w[k]), D, 0, 0, 0);
-                D = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao, hi_nibbles(sl.w[k]), D, 0, 0, 0);
-                uint32_t sraw, braw;
-                if constexpr (SB8) {
-                    sraw = half_of(sv[k], d);
-                    braw = half_of(bv[k], d);
-                } else {
-                    sraw = sl.s[k];
-                    braw = sl.b[k];
-                }
-                const float sc = h2f(static_cast<uint16_t>(sraw)), bi = h2f(static_cast<uint16_t>(braw));
-                float* tk = tbl + k * (256 * GWp);
+                uint4 b0, b1;
+                pair_permute(sl.w[k][0].x, sl.w[k][1].x, b0.x, b1.x);
+                pair_permute(sl.w[k][0].y, sl.w[k][1].y, b0.y, b1.y);
+                pair_permute(sl.w[k][0].z, sl.w[k][1].z, b0.z, b1.z);
+                pair_permute(sl.w[k][0].w, sl.w[k][1].w, b0.w, b1.w);
+                bw[k][0][0] = lo_nibbles(b0);
+                bw[k][0][1] = hi_nibbles(b0);
+                bw[k][1][0] = lo_nibbles(b1);
+                bw[k][1][1] = hi_nibbles(b1);
+            }
 #pragma unroll
-                for (int mm = 0; mm < 4; mm++) {
-                    // kernel/q4gemv.c:173-180 with xq = 256 xh + (xl' + 128)
-                    const int32_t idot = D[mm] + D[4 + mm] * 256 + D[8] * 128;
-                    const float dot = __fmul_rn(xsc[mm], static_cast<float>(idot));
-                    const float bx = __fmul_rn(bi, xs4[mm]);
-                    tk[((4 * h + mm) * 32 + j) * GWp + gl] = __fmaf_rn(sc, dot, bx);
+            for (int e = 0; e < 2; e++) {
+                const uint4 xe = make_uint4(sl.xe[e].x | onesv, sl.xe[e].y | onesv, sl.xe[e].z | onesv,
+                                            sl.xe[e].w | onesv);
+                const uint4 xo = make_uint4(sl.xo[e].x | onesv, sl.xo[e].y | onesv, sl.xo[e].z | onesv,
+                                            sl.xo[e].w | onesv);
+                const mf_v4i ae = __builtin_bit_cast(mf_v4i, xe), ao = __builtin_bit_cast(mf_v4i, xo);
+                const float xs4[4] = {sl.xs[e].x, sl.xs[e].y, sl.xs[e].z, sl.xs[e].w};
+                const int gi = 2 * d + e;                            // group of the wave's 8
+                const int gl = wave * kMfRing + gi;                  // group within the window
+#pragma unroll
+                for (int k = 0; k < NM; k++) {
+                    mf_v16i D = {};
+                    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(ae, bw[k][e][0], D, 0, 0, 0);
+                    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao, bw[k][e][1], D, 0, 0, 0);
+                    uint32_t sraw, braw;
+                    if constexpr (SB8) {
+                        sraw = half_of(sv[k], gi);
+                        braw = half_of(bv[k], gi);
+                    } else {
+                        sraw = sl.s[k][e];
+                        braw = sl.b[k][e];
+                    }
+                    const float sc = h2f(static_cast<uint16_t>(sraw)), bi = h2f(static_cast<uint16_t>(braw));
+                    float* tk = tbl + (k * GW + gl) * 256;
+#pragma unroll
+                    for (int mm = 0; mm < 4; mm++) {
+                        // kernel/q4gemv.c:173-180 with xq = 256 xh + (xl' + 128)
+                        const int32_t idot = D[mm] + D[4 + mm] * 256 + D[8] * 128;
+                        const float dot = __fmul_rn(xsc[mm], static_cast<float>(idot));
+                        const float bx = __fmul_rn(bi, xs4[mm]);
+                        tk[(4 * h + mm) * 32 + j] = __fmaf_rn(sc, dot, bx);
+                    }
                 }
             }
-            load(ring[d], g0 + GW + d);                              // the next window's group
+            load(ring[d], g0 + GW + 2 * d);                          // the next window's pair
         }
         __syncthreads();
         if (chain) {
             const int n = G - t * GW < GW ? G - t * GW : GW;
 #pragma unroll
             for (int k = 0; k < NM; k++) {
-                const float* tp = tbl + k * (256 * GWp) + (cm * 32 + j) * GWp;
+                const float* tp = tbl + k * GW * 256 + cm * 32 + j;
                 float a = acc[k];
                 int g = 0;
-                for (; g + 4 <= n; g += 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(tp + g);
-                    a = __fadd_rn(a, v.x);
-                    a = __fadd_rn(a, v.y);
-                    a = __fadd_rn(a, v.z);
-                    a = __fadd_rn(a, v.w);
+                for (; g + 8 <= n; g += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] = tp[(g + i) * 256];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) a = __fadd_rn(a, v[i]);
                 }
-                for (; g < n; g++) a = __fadd_rn(a, tp[g]);
+                for (; g < n; g++) a = __fadd_rn(a, tp[g * 256]);
                 acc[k] = a;
             }
         }

@@ -883,11 +883,10 @@ int gemv_split(const uint32_t* w, const uint16_t* s, const uint16_t* b, const fl
     return 0;
 }
 
-template <bool PAIR, int S, bool SB8>
-int launch_mfma_k(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace& ws, float* out, int tiles,
-                  hipStream_t st) {
-    auto kern = q4k::gemv_mfma_kernel<PAIR, S, SB8>;
-    constexpr size_t lds = (PAIR ? 2 : 1) * 256 * (q4k::kMfRing * S + 4) * sizeof(float);
+template <bool PAIR, int S, bool SB8, int TR>
+int launch_mfma_k(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace& ws, float* out, hipStream_t st) {
+    auto kern = q4k::gemv_mfma_kernel<PAIR, S, SB8, TR>;
+    constexpr size_t lds = (PAIR ? 2 : 1) * 256 * q4k::kMfRing * S * sizeof(float);
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -895,6 +894,7 @@ int launch_mfma_k(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace
         if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
         attr_set = true;
     }
+    const int tiles = (n + TR - 1) / TR;
     hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * S), lds, st, mt, n, n_in, m,
                        reinterpret_cast<const uint32_t*>(ws.planes), ws.xsum, ws.xscale, out, n);
     hipError_t e = hipGetLastError();
@@ -904,16 +904,23 @@ int launch_mfma_k(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace
 
 template <bool PAIR, bool SB8>
 int launch_mfma_s(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace& ws, float* out, hipStream_t st) {
-    // 8 waves per tile while the tiles do not fill the CUs twice (the
-    // 3584-row shapes: 112 tiles), else 4
-    const int tiles = (n + 31) / 32;
-    return tiles < 2 * num_cus() ? launch_mfma_k<PAIR, 8, SB8>(mt, n, n_in, m, ws, out, tiles, st)
-                                 : launch_mfma_k<PAIR, 4, SB8>(mt, n, n_in, m, ws, out, tiles, st);
+    // One workgroup per CU holds a fixed number of weight bytes in flight
+    // (the register ring), so the workgroups must cover the CUs: 16-row
+    // tiles of 8 waves when 32-row tiles would leave CUs idle (one matrix of
+    // 3584 rows: 224 tiles), 32-row tiles of 8 waves while they do not fill
+    // the CUs twice, else 4 waves.
+    const int tiles = (n + 31) / 32, cus = num_cus();
+    if constexpr (!PAIR)
+        if (tiles < cus) return launch_mfma_k<PAIR, 8, SB8, 16>(mt, n, n_in, m, ws, out, st);
+    return tiles < 2 * cus ? launch_mfma_k<PAIR, 8, SB8, 32>(mt, n, n_in, m, ws, out, st)
+                           : launch_mfma_k<PAIR, 4, SB8, 32>(mt, n, n_in, m, ws, out, st);
 }
 
-// Rows of x from which the matrix-core path is used (measured on the q_proj
-// and MLP shapes of Qwen2.5-7B: below it the streaming kernel is faster).
-constexpr int kMfMinRows = 5;
+// Rows of x from which the matrix-core path is used.  Its cost does not
+// depend on the row count; the streaming kernel's grows with it (Qwen2.5-7B
+// MLP block: 60 us at 2 rows and 80 us at 3-4 rows streaming, 64 us on the
+// matrix cores; q_proj about even at 3-4 rows).
+constexpr int kMfMinRows = 3;
 
 // Small-M GEMV on the int8 matrix cores (q4_mfma_m.h): kMfMinRows <= m <= kMaxM,
 // gs 64, n_in <= 32768, x 16-byte aligned, every byte offset into the
@@ -926,7 +933,8 @@ int gemv_mfma(const q4k::MfMats& mt, bool pair, const float* x, float* out, int 
     if (m < kMfMinRows || m > kMaxM || gs != 64 || n_in <= 0 || n <= 0 || n_in > q4k::kMfPrepMaxK) return 0;
     if (reinterpret_cast<uintptr_t>(x) & 15) return 0;
     const long G = n_in / 64;
-    if (static_cast<long>(n) * (n_in / 2) >= (1L << 31) || static_cast<long>(n) * G * 2 >= (1L << 31)) return 0;
+    // (n + 32 rows: a tile's second weight load starts 16 rows past the first)
+    if (static_cast<long>(n + 32) * (n_in / 2) >= (1L << 31) || static_cast<long>(n) * G * 2 >= (1L << 31)) return 0;
     int rc = ensure_ws(ws, st, static_cast<size_t>(G) * 2 * q4k::kMfArows * 2, static_cast<size_t>(G) * 8);
     if (rc) return rc;
     static bool prep_attr = false;
