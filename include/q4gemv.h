@@ -79,7 +79,11 @@ const char *q4_last_error(void);
  * per-stream x workspace is reused by the next call on that stream. */
 
 /* Batched GEMV over m rows (any m >= 1; rows are processed eight at a time).
- * Same arithmetic as q4_gemv.  x is [m][n_in], out is [m][n_out]. */
+ * Same arithmetic as q4_gemv.  x is [m][n_in], out is [m][n_out].  Blocks of
+ * 3..8 rows with gs 64 run their integer dots on the int8 matrix cores, with
+ * x quantised into the per-stream workspace first; the workspace grows on
+ * first use, so run the largest call once on a stream before capturing it
+ * in a graph. */
 int q4_gemv_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
                 const float *x, float *out, int m, int n_out, int n_in, int gs,
                 void *stream);
