@@ -149,6 +149,7 @@ def small_m_bench(torch, lib, layers, dev, ms=(1, 2, 4, 8), reps=5):
         y = torch.empty((m, 3584), device=dev)
         h = torch.empty((m, 18944), device=dev)
         mo = torch.empty((m, 3584), device=dev)
+        torch.cuda.synchronize()        # inputs from the default stream; the calls run on `stream`
 
         def step_q():
             for layer in layers:
@@ -200,6 +201,7 @@ def wire_bench(torch, lib, dev, rows_list=(1, 256, 2048), hidden=3584, reps=5):
         nb = int(min(64, max(2, -(-600_000_000 // (4 * n)))))
         xs = [torch.randn((rows, hidden), device=dev) for _ in range(nb)]
         outs = [torch.empty((rows, hidden), device=dev) for _ in range(nb)]
+        torch.cuda.synchronize()        # inputs from the default stream; the calls run on `stream`
         row = {}
         for codec, cid in (("fp16", 0), ("int8", 1)):
             pb = int(lib.q4_wire_payload_bytes(cid, rows, hidden))
@@ -564,6 +566,8 @@ def main():
                     help="only the grouped decode sweep (for rocprof runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the M=512 prefill leg (for counter runs)")
+    ap.add_argument("--small-m-only", action="store_true",
+                    help="only the small-M section (for rocprof runs)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode step (for rocprof runs)")
     ap.add_argument("--no-decode-check", action="store_true",
@@ -601,6 +605,9 @@ def main():
               for _ in range(LAYERS)]
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(torch, lib, layers, dev)}), flush=True)
+        return
+    if args.small_m_only:
+        print(json.dumps({"small_m": small_m_bench(torch, lib, layers, dev)}), flush=True)
         return
     head = make_weights(torch, gen, HEAD_SHAPE[2], HEAD_SHAPE[1], dev)
     xs = {k: torch.randn((1, k), device=dev, generator=gen) for k in (3584, 18944)}
