@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
@@ -126,6 +127,21 @@ __device__ __forceinline__ uint4 quant_word(const float (&v)[8], float inv, bool
 // host side, defined in q4gemv.hip
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int num_cus();
+
+// Dynamic LDS above 64 KiB needs the kernel's limit raised on each device
+// that runs it.  `done` holds one bit per device already raised (0..63; a
+// higher device id raises it on every call).
+inline int raise_lds_limit(const void* kern, size_t bytes, std::atomic<uint64_t>& done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(Q4_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t{1} << dev) : 0;
+    if (bit && (done.load(std::memory_order_relaxed) & bit)) return 0;
+    e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    if (e != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done.fetch_or(bit, std::memory_order_relaxed);
+    return 0;
+}
 constexpr size_t kStreamLdsMax = 160 * 1024;
 
 }  // namespace q4k

@@ -612,14 +612,8 @@ template <int MR, int RW, bool PAIR, int RING, bool NORM>
 int launch_stream_k(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
                     size_t lds, int grid, hipStream_t st) {
     auto kern = gemv_stream_kernel<MR, RW, PAIR, RING, NORM>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            static_cast<int>(kStreamLdsMax));
-        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_raised{0};
+    if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), kStreamLdsMax, lds_raised)) return rc;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB, na);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "stream gemv launch: %s", hipGetErrorString(e));

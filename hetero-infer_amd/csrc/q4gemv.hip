@@ -887,13 +887,8 @@ template <bool PAIR, int S, bool SB8, int TR>
 int launch_mfma_k(const q4k::MfMats& mt, int n, int n_in, int m, const Workspace& ws, float* out, hipStream_t st) {
     auto kern = q4k::gemv_mfma_kernel<PAIR, S, SB8, TR>;
     constexpr size_t lds = (PAIR ? 2 : 1) * 256 * q4k::kMfRing * S * sizeof(float);
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_raised{0};
+    if (int rc = q4k::raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
     const int tiles = (n + TR - 1) / TR;
     hipLaunchKernelGGL(kern, dim3(tiles), dim3(64 * S), lds, st, mt, n, n_in, m,
                        reinterpret_cast<const uint32_t*>(ws.planes), ws.xsum, ws.xscale, out, n);
@@ -937,14 +932,10 @@ int gemv_mfma(const q4k::MfMats& mt, bool pair, const float* x, float* out, int 
     if (static_cast<long>(n + 32) * (n_in / 2) >= (1L << 31) || static_cast<long>(n) * G * 2 >= (1L << 31)) return 0;
     int rc = ensure_ws(ws, st, static_cast<size_t>(G) * 2 * q4k::kMfArows * 2, static_cast<size_t>(G) * 8);
     if (rc) return rc;
-    static bool prep_attr = false;
-    if (!prep_attr) {
-        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(q4k::xprep_mf_kernel),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            static_cast<int>(q4k::kMfPrepMaxK * sizeof(float)));
-        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
-        prep_attr = true;
-    }
+    static std::atomic<uint64_t> prep_raised{0};
+    if ((rc = q4k::raise_lds_limit(reinterpret_cast<const void*>(q4k::xprep_mf_kernel),
+                                   q4k::kMfPrepMaxK * sizeof(float), prep_raised)))
+        return rc;
     hipLaunchKernelGGL(q4k::xprep_mf_kernel, dim3(kMaxM), dim3(1024), static_cast<size_t>(n_in) * sizeof(float), st,
                        x, m, n_in, reinterpret_cast<uint32_t*>(ws.planes), ws.xsum, ws.xscale);
     HIP_TRY(hipGetLastError());
@@ -1126,13 +1117,8 @@ int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const u
                 int M, int N, int K, int S, int kt_split, hipStream_t st, int nb0 = 0, int nblocks = -1, int ldo = -1) {
     auto kern = gemm_q4_bf16_kernel<BM, BN, D, EVENG>;
     const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t ea = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-        if (ea != hipSuccess) return fail(Q4_EHIP, "hipFuncSetAttribute: %s", hipGetErrorString(ea));
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_raised{0};
+    if (int rc = q4k::raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
     dim3 grid((M + BM - 1) / BM, nblocks < 0 ? (N + BN - 1) / BN : nblocks, S);
     hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, xb, w, s, b, out, M, N, K, kt_split, nb0, ldo < 0 ? N : ldo);
     HIP_TRY(hipGetLastError());
