@@ -923,13 +923,18 @@ constexpr int kMfMinRows = 3;
 // SiLU(gate) * up.  x is prepared into the stream's workspace by
 // xprep_mf_kernel.  Returns 1 if it launched, 0 if the shape is not one it
 // takes, <0 on error.
-int gemv_mfma(const q4k::MfMats& mt, bool pair, const float* x, float* out, int m, int n, int n_in, int gs,
-              hipStream_t st, Workspace& ws) {
-    if (m < kMfMinRows || m > kMaxM || gs != 64 || n_in <= 0 || n <= 0 || n_in > q4k::kMfPrepMaxK) return 0;
-    if (reinterpret_cast<uintptr_t>(x) & 15) return 0;
-    const long G = n_in / 64;
+bool mfma_takes(int m, int n, int n_in, int gs, const float* x) {
+    if (m < kMfMinRows || m > kMaxM || gs != 64 || n_in <= 0 || n <= 0 || n_in > q4k::kMfPrepMaxK) return false;
+    if (reinterpret_cast<uintptr_t>(x) & 15) return false;
     // (n + 32 rows: a tile's second weight load starts 16 rows past the first)
-    if (static_cast<long>(n + 32) * (n_in / 2) >= (1L << 31) || static_cast<long>(n) * G * 2 >= (1L << 31)) return 0;
+    const long G = n_in / 64;
+    return static_cast<long>(n + 32) * (n_in / 2) < (1L << 31) && static_cast<long>(n) * G * 2 < (1L << 31);
+}
+
+// x of m rows quantised into the stream's workspace for the matrix-core
+// kernel (xprep_mf_kernel); every later launch on the stream reads it.
+int mfma_prep(const float* x, int m, int n_in, hipStream_t st, Workspace& ws) {
+    const long G = n_in / 64;
     int rc = ensure_ws(ws, st, static_cast<size_t>(G) * 2 * q4k::kMfArows * 2, static_cast<size_t>(G) * 8);
     if (rc) return rc;
     static std::atomic<uint64_t> prep_raised{0};
@@ -939,11 +944,24 @@ int gemv_mfma(const q4k::MfMats& mt, bool pair, const float* x, float* out, int 
     hipLaunchKernelGGL(q4k::xprep_mf_kernel, dim3(kMaxM), dim3(1024), static_cast<size_t>(n_in) * sizeof(float), st,
                        x, m, n_in, reinterpret_cast<uint32_t*>(ws.planes), ws.xsum, ws.xscale);
     HIP_TRY(hipGetLastError());
-    const bool sb8 = G % 8 == 0;
+    return 0;
+}
+
+// The matrix-core GEMV on x prepared by mfma_prep.  Returns 1 (launched) or <0.
+int mfma_main(const q4k::MfMats& mt, bool pair, float* out, int m, int n, int n_in, hipStream_t st,
+              const Workspace& ws) {
+    const bool sb8 = (n_in / 64) % 8 == 0;
     if (pair) return sb8 ? launch_mfma_s<true, true>(mt, n, n_in, m, ws, out, st)
                          : launch_mfma_s<true, false>(mt, n, n_in, m, ws, out, st);
     return sb8 ? launch_mfma_s<false, true>(mt, n, n_in, m, ws, out, st)
                : launch_mfma_s<false, false>(mt, n, n_in, m, ws, out, st);
+}
+
+int gemv_mfma(const q4k::MfMats& mt, bool pair, const float* x, float* out, int m, int n, int n_in, int gs,
+              hipStream_t st, Workspace& ws) {
+    if (!mfma_takes(m, n, n_in, gs, x)) return 0;
+    if (int rc = mfma_prep(x, m, n_in, st, ws)) return rc;
+    return mfma_main(mt, pair, out, m, n, n_in, st, ws);
 }
 
 // GEMV of m (<= kMaxM) rows already on the device: the matrix cores for
@@ -1299,6 +1317,28 @@ int q4_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const
         rc = try_fused_m(ml, x, m, n_in, gs, st);
         if (rc < 0) return rc;
         if (rc == 1) return 0;
+    }
+    // 3..8 rows on the matrix cores: x prepared once for every matrix
+    bool all_mf = m <= kMaxM, any = false;
+    for (int k = 0; k < count && all_mf; k++) {
+        all_mf = n_out[k] == 0 || mfma_takes(m, n_out[k], n_in, gs, x);
+        any = any || n_out[k] > 0;
+    }
+    if (all_mf && any) {
+        Workspace* ws;
+        {
+            std::lock_guard<std::mutex> lock(g_mu);
+            int dev;
+            if ((rc = current_device(&dev))) return rc;
+            ws = &g_dev[dev].ws[st];
+        }
+        if ((rc = mfma_prep(x, m, n_in, st, *ws))) return rc;
+        for (int k = 0; k < count; k++) {
+            if (n_out[k] == 0) continue;
+            const q4k::MfMats mt{{w[k], w[k]}, {scales[k], scales[k]}, {biases[k], biases[k]}};
+            if ((rc = mfma_main(mt, false, out[k], m, n_out[k], n_in, st, *ws)) < 0) return rc;
+        }
+        return 0;
     }
     for (int k = 0; k < count; k++)
         if ((rc = q4_gemv_dev(w[k], scales[k], biases[k], x, out[k], m, n_out[k], n_in, gs, stream)))

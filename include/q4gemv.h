@@ -89,7 +89,9 @@ int q4_gemv_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biase
                 void *stream);
 
 /* Up to four matrices that share the activations x (q/k/v, gate/up) in one
- * launch: out[k] is [m][n_out[k]] = W_k x, each row bit-identical to q4_gemv.
+ * launch (1..2 rows; 3..8 rows: x quantised once, then one matrix-core launch
+ * per matrix): out[k] is [m][n_out[k]] = W_k x, each row bit-identical to
+ * q4_gemv.
  * w, scales, biases, out and n_out are host arrays of `count` device
  * pointers / sizes.  No counterpart in the reference, whose caller makes one
  * q4_gemv call per projection (hetero/cpu_model.py:269-275, :291-292). */
