@@ -229,3 +229,23 @@ def test_dev_all_m_and_paths(lib):
             got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
             torch.cuda.synchronize()
             assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} m={m}")
+
+
+def test_matrix_core_tile_variants(lib):
+    """3..8 rows on the matrix cores, bit-exact vs the oracle, for the
+    variants the Qwen shapes leave out: group counts not a multiple of 8
+    (per-group scale/bias loads; 13 and 44 groups), 16-row tiles with a
+    partial last tile (N = 300), 32-row tiles of 8 waves (N = 9000) and of 4
+    waves (N = 16400, a partial last tile)."""
+    import torch
+    o = oracle.Oracle()
+    for k_in, n_out in ((832, 300), (2816, 48), (512, 9000), (832, 16400)):
+        w, s, b = synth.qlinear(500 + k_in + n_out, n_out, k_in, 64)
+        x = synth.activations(501, 8, k_in)
+        want = o.gemv_rows(w, s, b, x, 64)
+        tw, ts, tb, tx = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16), x))
+        for m in (3, 5, 8):
+            print(f"matrix cores K={k_in} N={n_out} m={m}", flush=True)
+            got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
+            torch.cuda.synchronize()
+            assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} N={n_out} m={m}")

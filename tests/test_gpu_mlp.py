@@ -97,3 +97,20 @@ def test_gate_up_silu_rows_match_one_row_launches(hidden, inter):
         h = h.cpu().numpy()
         for r in range(m):
             assert np.array_equal(h[r].view(np.uint32), ones[r].view(np.uint32)), f"m={m} row {r}"
+
+
+def test_gate_up_silu_rows_odd_group_count():
+    """The fused gate/up tiles with 13 groups per row (per-group scale/bias
+    loads) and a partial tile: 3..8 rows against the one-row launches."""
+    import torch
+    hidden, inter = 832, 100
+    (_, gt), (_, ut) = mats(630, inter, hidden), mats(631, inter, hidden)
+    x = synth.activations(632, 8, hidden)
+    tx = tensors(x)[0]
+    ones = [q4.gate_up_silu_dev(gt, ut, tx[r:r + 1].contiguous()).cpu().numpy()[0] for r in range(8)]
+    for m in (3, 8):
+        h = q4.gate_up_silu_dev(gt, ut, tx[:m].contiguous())
+        torch.cuda.synchronize()
+        h = h.cpu().numpy()
+        for r in range(m):
+            assert np.array_equal(h[r].view(np.uint32), ones[r].view(np.uint32)), f"m={m} row {r}"
