@@ -36,7 +36,7 @@ HIPCC_FLAGS = [
 ]
 
 # (activation rows, gate/up pair, ring size) of the streaming kernel objects
-STREAM_INSTANCES = [(mr, pair, ring) for mr in (1, 2, 4, 8) for pair in (0, 1) for ring in (1, 2, 4)] + [(1, 0, 5)]
+STREAM_INSTANCES = [(mr, pair, ring) for mr in (1, 2) for pair in (0, 1) for ring in (1, 2, 4)] + [(1, 0, 5)]
 
 
 def hipcc() -> str:

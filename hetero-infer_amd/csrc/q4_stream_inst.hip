@@ -1,6 +1,6 @@
 // Instances of the streaming GEMV kernel, one object per (activation rows,
 // gate/up pair, ring size), one-row objects with the norm prologue too: the
-// build compiles this file once per -DQ4_MR=<1|2|4|8> -DQ4_PAIR=<0|1>
+// build compiles this file once per -DQ4_MR=<1|2> -DQ4_PAIR=<0|1>
 // -DQ4_RING=<1|2|4|5>, in parallel.
 #include "q4_stream.h"
 

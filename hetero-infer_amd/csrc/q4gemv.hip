@@ -87,9 +87,6 @@ Q4_STREAM_EXTERN(1, 3, false, 5, false) Q4_STREAM_EXTERN(1, 4, false, 5, false)
 Q4_STREAM_RINGS(1, 1, true, false) Q4_STREAM_RINGS(1, 2, true, false)
 Q4_STREAM_RINGS(2, 1, false, false) Q4_STREAM_RINGS(2, 2, false, false)
 Q4_STREAM_RINGS(2, 1, true, false) Q4_STREAM_RINGS(2, 2, true, false)
-Q4_STREAM_RINGS(4, 1, false, false) Q4_STREAM_RINGS(4, 2, false, false)
-Q4_STREAM_RINGS(4, 1, true, false) Q4_STREAM_RINGS(4, 2, true, false)
-Q4_STREAM_RINGS(8, 1, false, false) Q4_STREAM_RINGS(8, 1, true, false)
 Q4_STREAM_RINGS(1, 1, false, true) Q4_STREAM_EXTERN(1, 1, false, 5, true)
 Q4_STREAM_RINGS(1, 1, true, true)
 #undef Q4_STREAM_RINGS
@@ -830,16 +827,15 @@ int try_fused(const MatList& ml, const float* x, int n_in, int gs, hipStream_t s
     return launch_stream<MR>(ml, x, n_in, st);
 }
 
-// m rows run in the instance of the next power of two (3 -> 4, 5..7 -> 8),
-// the missing rows reading 0 and not stored.
+// One or two rows: the streaming kernel's instance of that row count.
 int try_fused_m(const MatList& ml, const float* x, int m, int n_in, int gs, hipStream_t st) {
     MatList mm = ml;
     mm.mrows = m;
     switch (m) {
         case 1: return try_fused<1>(mm, x, n_in, gs, st);
         case 2: return try_fused<2>(mm, x, n_in, gs, st);
-        case 3: case 4: return try_fused<4>(mm, x, n_in, gs, st);
-        case 5: case 6: case 7: case 8: return try_fused<8>(mm, x, n_in, gs, st);
+        // (3..8 rows take the matrix cores, or the split path where those
+        // decline the shape)
         default: return 0;
     }
 }
@@ -1386,12 +1382,9 @@ int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const ui
             done = gemv_mfma(mt, true, xm, hm, mm, n_inter, n_in, gs, st, *ws);
             if (done < 0) return done;
         }
-        if (!done && gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
+        if (!done && mm <= 2 && gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
             (n_in / 8 + kChunkWords - 1) / kChunkWords <= 16) {
-            done = mm == 1   ? launch_stream<1, true>(ml, xm, n_in, st)
-                   : mm == 2 ? launch_stream<2, true>(ml, xm, n_in, st)
-                   : mm <= 4 ? launch_stream<4, true>(ml, xm, n_in, st)
-                             : launch_stream<8, true>(ml, xm, n_in, st);
+            done = mm == 1 ? launch_stream<1, true>(ml, xm, n_in, st) : launch_stream<2, true>(ml, xm, n_in, st);
             if (done < 0) return done;
         }
         if (!done) {        // unfused: gate into h, up into the workspace, then SiLU * mul
