@@ -1,4 +1,5 @@
-// Small-M GEMV on the int8 matrix cores (2 <= M <= 8 activation rows, gs 64).
+// Small-M GEMV on the int8 matrix cores (up to 8 activation rows, gs 64; the
+// library takes it from 3 rows, below which the streaming kernel is faster).
 //
 // The arithmetic is the reference's x86 path of kernel/q4gemv.c:232-301 for
 // every row of x: x quantised to int16 once per row (:244-270), an exact
@@ -20,8 +21,9 @@
 // 0..7, 8..15 xh (loaded), 16 and 20 ones (made in registers), the rest
 // zero, which puts every plane an output needs into the same lane of D.
 //
-// Work split.  A workgroup owns a tile of 32 weight rows (PAIR: 32 gate rows
-// and the same 32 up rows, one A operand for both) and runs S waves over K
+// Work split.  A workgroup owns a tile of 32 weight rows (16 when 32-row
+// tiles would leave CUs idle; PAIR: 32 gate rows and the same 32 up rows,
+// one A operand for both) and runs S waves over K
 // in windows of 8*S groups, 8 consecutive groups per wave, each wave
 // streaming its groups through a register ring of 8 (the next window's
 // loads are in flight while the window's terms are chained).  Each group's
@@ -199,7 +201,7 @@ __device__ __forceinline__ uint32_t half_of(const uint4& v, int k) {
 }
 
 // out[m][row] for m < M (PAIR: h[m][row] = SiLU(gate) * up), row stride ldo.
-// Grid: one workgroup per tile of 32 rows; block: 64 * S threads (S = 4 or
+// Grid: one workgroup per tile of TR rows; block: 64 * S threads (S = 4 or
 // 8: the ring takes about 150-200 registers, so at most two waves per SIMD).
 // SB8: the group count is a multiple of 8 (scales/biases by window).
 // TR: weight rows per tile, 32, or 16 (B columns 16..31 dead) to spread a
