@@ -50,30 +50,34 @@ namespace q4k {
 constexpr int kMfRing = 8;          // groups per wave and window (ring: 4 slots of 2 groups)
 constexpr int kMfArows = 16;        // A rows stored per (group, k-half): xl 0..7, xh 8..15
 
-// x of up to 8 rows, prepared for the small-M MFMA kernel (one workgroup per
-// row slot; slots >= M write zeros).  The fp32 steps are xprep_kernel's:
+// x of up to 8 rows, prepared for the small-M MFMA kernel.  Grid (P, 8):
+// workgroup (p, m) takes row slot m (slots >= M write zeros) and the p-th
+// slice of its groups.  The fp32 steps are xprep_kernel's:
 //   xa[((g*2 + h)*16 + r)*8 + s]  uint32: A row r, k-half h of group g;
 //                                 s 0..3 even-k bytes of words 4h..4h+3 of
 //                                 the group, 4..7 the odd-k bytes
 //   xsum_t[g*8 + m], xscale[m]
-// The row is staged in LDS by 16-byte loads all issued at once (one memory
-// round trip); amax, the group sums and the quantisation then read LDS.
+// Every workgroup of a row stages the whole row in LDS by 16-byte loads all
+// issued at once (one memory round trip) and takes its amax; the group sums
+// and the quantisation of its slice then read LDS.
 constexpr int kMfPrepMaxK = 32768;           // floats of one x row staged in LDS
 __global__ __launch_bounds__(1024) void xprep_mf_kernel(const float* __restrict__ x, int M, int n_in,
                                                         uint32_t* __restrict__ xa, float* __restrict__ xsum_t,
                                                         float* __restrict__ xscale_out) {
     extern __shared__ float4 xrow4[];                            // [n_in / 4]
-    const int m = blockIdx.x;
+    const int m = blockIdx.y;
     const int tid = threadIdx.x, nt = blockDim.x;
-    const int G = n_in >> 6, wpr = n_in >> 3;
+    const int G = n_in >> 6;
+    const int gs = (G + gridDim.x - 1) / gridDim.x;              // groups per slice
+    const int g0 = blockIdx.x * gs, g1 = g0 + gs < G ? g0 + gs : G;
     if (m >= M) {
-        for (int i = tid; i < G * 2 * 8; i += nt) {
+        for (int i = g0 * 16 + tid; i < g1 * 16; i += nt) {
             const int s = i & 7, gh = i >> 3;
             xa[(static_cast<size_t>(gh) * kMfArows + m) * 8 + s] = 0u;
             xa[(static_cast<size_t>(gh) * kMfArows + 8 + m) * 8 + s] = 0u;
         }
-        for (int g = tid; g < G; g += nt) xsum_t[static_cast<size_t>(g) * 8 + m] = 0.0f;
-        if (tid == 0) xscale_out[m] = 1.0f;
+        for (int g = g0 + tid; g < g1; g += nt) xsum_t[static_cast<size_t>(g) * 8 + m] = 0.0f;
+        if (tid == 0 && blockIdx.x == 0) xscale_out[m] = 1.0f;
         return;
     }
     __shared__ float red[16];
@@ -109,8 +113,14 @@ __global__ __launch_bounds__(1024) void xprep_mf_kernel(const float* __restrict_
     }
     if ((tid & 63) == 0) red[tid >> 6] = amax;
     __syncthreads();
-    const float* xl = reinterpret_cast<const float*>(xrow4);
-    for (int g = tid; g < G; g += nt) {                          // kernel/q4gemv.c:244-248
+    if (tid == 0) {
+        float a = 0.0f;
+        for (int i = 0; i < (nt >> 6); i++) a = red[i] > a ? red[i] : a;
+        const float sc = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;   // :260
+        if (blockIdx.x == 0) xscale_out[m] = sc;
+        s_inv = __fdiv_rn(1.0f, sc);                                  // :261
+    }
+    for (int g = g0 + tid; g < g1; g += nt) {                    // kernel/q4gemv.c:244-248
         const float4* p = xrow4 + g * 16;
         float s = 0.0f;
 #pragma unroll
@@ -123,16 +133,10 @@ __global__ __launch_bounds__(1024) void xprep_mf_kernel(const float* __restrict_
         }
         xsum_t[static_cast<size_t>(g) * 8 + m] = s;
     }
-    if (tid == 0) {
-        float a = 0.0f;
-        for (int i = 0; i < (nt >> 6); i++) a = red[i] > a ? red[i] : a;
-        const float sc = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;   // :260
-        xscale_out[m] = sc;
-        s_inv = __fdiv_rn(1.0f, sc);                                  // :261
-    }
     __syncthreads();
     const float inv = s_inv;
-    for (int j = tid; j < wpr; j += nt) {
+    const float* xl = reinterpret_cast<const float*>(xrow4);
+    for (int j = g0 * 8 + tid; j < g1 * 8; j += nt) {
         uint32_t le = 0, lo = 0, he = 0, ho = 0;
 #pragma unroll
         for (int n = 0; n < 8; n++) {

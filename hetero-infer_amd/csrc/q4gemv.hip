@@ -937,8 +937,11 @@ int mfma_prep(const float* x, int m, int n_in, hipStream_t st, Workspace& ws) {
     if ((rc = q4k::raise_lds_limit(reinterpret_cast<const void*>(q4k::xprep_mf_kernel),
                                    q4k::kMfPrepMaxK * sizeof(float), prep_raised)))
         return rc;
-    hipLaunchKernelGGL(q4k::xprep_mf_kernel, dim3(kMaxM), dim3(1024), static_cast<size_t>(n_in) * sizeof(float), st,
-                       x, m, n_in, reinterpret_cast<uint32_t*>(ws.planes), ws.xsum, ws.xscale);
+    // each row's groups in slices of at least 32 over up to 8 workgroups
+    // (every workgroup of a row reads the whole row for its amax)
+    const int slices = static_cast<int>(G / 32 < 1 ? 1 : (G / 32 > 8 ? 8 : G / 32));
+    hipLaunchKernelGGL(q4k::xprep_mf_kernel, dim3(slices, kMaxM), dim3(1024), static_cast<size_t>(n_in) * sizeof(float),
+                       st, x, m, n_in, reinterpret_cast<uint32_t*>(ws.planes), ws.xsum, ws.xscale);
     HIP_TRY(hipGetLastError());
     return 0;
 }
