@@ -627,52 +627,64 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
 
 bool pow2_gs(int gs) { return gs >= 64 && gs <= 2048 && (gs & (gs - 1)) == 0; }
 
-// Per-stream x workspace (prologue outputs).  Grows only; before freeing an
-// old buffer the stream is drained, since earlier launches may still read it.
+// Per-stream workspace: the x prologue's outputs (byte planes, group sums,
+// scales), the unfused MLP's up rows, and the prefill's bf16 copy of x and
+// split-K partial sums.  Buffers only grow.  A buffer that a call used while
+// its stream was being captured may be baked into a graph, so when it has to
+// grow later it is retired -- kept allocated until the process ends --
+// instead of freed; a buffer no graph holds is freed once the stream has
+// drained (earlier launches may still read it).  A `fixed` workspace is the
+// library's static scratch (q4_gemv_noalloc_dev): it never grows.
 struct Workspace {
     uint4* planes = nullptr;
     float* xsum = nullptr;
     float* xscale = nullptr;
-    size_t cap_words = 0, cap_groups = 0;
     float* tmp = nullptr;                       // up-projection rows of the unfused MLP
-    size_t cap_tmp = 0;
     void* xbf = nullptr;                        // prefill: bf16 copy of x
-    size_t cap_xbf = 0;
     void* part = nullptr;                       // prefill: split-K partial sums
-    size_t cap_part = 0;
+    size_t cap[6] = {0, 0, 0, 0, 0, 0};         // bytes, in the order above
+    bool in_graph[6] = {false, false, false, false, false, false};
+    bool fixed = false;
+    std::vector<void*> retired;
 };
+enum WsBuf { kWsPlanes, kWsXsum, kWsXscale, kWsTmp, kWsXbf, kWsPart };
 
-// Grow one raw workspace buffer (bytes), outside graph capture.
-int ensure_raw(void*& p, size_t& cap, size_t bytes, hipStream_t st, const char* what) {
-    if (bytes <= cap && p) return 0;
+// Make buffer `which` (pointer p) of the workspace hold `bytes`.  Growing is
+// refused while the stream is captured (an allocation cannot be recorded).
+template <typename T>
+int grow(Workspace& ws, T*& p, WsBuf which, size_t bytes, hipStream_t st, const char* what) {
+    size_t& cap = ws.cap[which];
+    if (ws.fixed) {
+        if (bytes <= cap) return 0;
+        return fail(Q4_EARG, "%s: needs %zu bytes of scratch, above the library's fixed %zu", what, bytes, cap);
+    }
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     HIP_TRY(hipStreamIsCapturing(st, &cs));
-    if (cs != hipStreamCaptureStatusNone)
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (bytes <= cap && p) {
+        if (capturing) ws.in_graph[which] = true;
+        return 0;
+    }
+    if (capturing)
         return fail(Q4_EARG, "%s workspace of this stream must grow during graph capture: "
                              "run the largest call once on the stream before capturing", what);
     HIP_TRY(hipStreamSynchronize(st));
-    (void)hipFree(p);
+    if (p) {
+        if (ws.in_graph[which]) ws.retired.push_back(static_cast<void*>(p));
+        else (void)hipFree(static_cast<void*>(p));
+    }
     p = nullptr;
     cap = 0;
-    HIP_TRY(hipMalloc(&p, bytes));
+    ws.in_graph[which] = false;
+    void* np = nullptr;
+    HIP_TRY(hipMalloc(&np, bytes));
+    p = static_cast<T*>(np);
     cap = bytes;
     return 0;
 }
 
 int ensure_tmp(Workspace& ws, hipStream_t st, size_t n) {
-    if (n <= ws.cap_tmp && ws.tmp) return 0;
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    HIP_TRY(hipStreamIsCapturing(st, &cap));
-    if (cap != hipStreamCaptureStatusNone)
-        return fail(Q4_EARG, "MLP workspace of this stream must grow during graph capture: "
-                             "run the largest call once on the stream before capturing");
-    HIP_TRY(hipStreamSynchronize(st));
-    (void)hipFree(ws.tmp);
-    ws.tmp = nullptr;
-    ws.cap_tmp = 0;
-    HIP_TRY(hipMalloc(&ws.tmp, n * sizeof(float)));
-    ws.cap_tmp = n;
-    return 0;
+    return grow(ws, ws.tmp, kWsTmp, n * sizeof(float), st, "MLP");
 }
 
 struct DevState {
@@ -686,11 +698,15 @@ struct DevState {
     size_t dev_x_cap = 0, dev_out_cap = 0;
 };
 
+// HBM copy of host weights.  `base` is the host address of the whole
+// matrix's packed weights: q4_dequant registers row blocks under their own
+// addresses, and q4_release(base) must find them too.
 struct Resident {
     uint32_t* w = nullptr;
     uint16_t* s = nullptr;
     uint16_t* b = nullptr;
     uint64_t fp = 0;
+    const void* base = nullptr;
 };
 
 // (device, w, scales, biases, n_out, n_in, gs)
@@ -700,28 +716,12 @@ std::mutex g_mu;                       // serialises every host-pointer call
 std::map<int, DevState> g_dev;
 std::map<ResKey, Resident> g_res;
 
+// words: uint4 of planes; groups: floats of group sums
 int ensure_ws(Workspace& ws, hipStream_t st, size_t words, size_t groups) {
-    if (words <= ws.cap_words && groups <= ws.cap_groups && ws.planes) return 0;
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    HIP_TRY(hipStreamIsCapturing(st, &cap));
-    if (cap != hipStreamCaptureStatusNone)
-        return fail(Q4_EARG, "x workspace of this stream must grow during graph capture: "
-                             "run the largest call once on the stream before capturing");
-    HIP_TRY(hipStreamSynchronize(st));
-    (void)hipFree(ws.planes);
-    (void)hipFree(ws.xsum);
-    (void)hipFree(ws.xscale);
-    ws.planes = nullptr;
-    ws.xsum = nullptr;
-    ws.xscale = nullptr;
-    ws.cap_words = ws.cap_groups = 0;
-    size_t cw = words < 4096 ? 4096 : words, cg = groups < 1024 ? 1024 : groups;
-    HIP_TRY(hipMalloc(&ws.planes, cw * sizeof(uint4)));
-    HIP_TRY(hipMalloc(&ws.xsum, cg * sizeof(float)));
-    HIP_TRY(hipMalloc(&ws.xscale, kMaxM * sizeof(float)));
-    ws.cap_words = cw;
-    ws.cap_groups = cg;
-    return 0;
+    const size_t cw = words < 4096 ? 4096 : words, cg = groups < 1024 ? 1024 : groups;
+    if (int rc = grow(ws, ws.planes, kWsPlanes, (ws.fixed ? words : cw) * sizeof(uint4), st, "x")) return rc;
+    if (int rc = grow(ws, ws.xsum, kWsXsum, (ws.fixed ? groups : cg) * sizeof(float), st, "x")) return rc;
+    return grow(ws, ws.xscale, kWsXscale, kMaxM * sizeof(float), st, "x");
 }
 
 template <int MR>
@@ -1047,8 +1047,10 @@ uint64_t fingerprint(const void* p, size_t bytes) {
     return h;
 }
 
+// base: the host address of the whole matrix's packed weights (w itself
+// unless w is a row block of it)
 int resident(const uint32_t* w, const uint16_t* s, const uint16_t* b, int n_out, int n_in,
-             int gs, int dev, Resident** out) {
+             int gs, int dev, Resident** out, const void* base = nullptr) {
     const size_t wb = static_cast<size_t>(n_out) * (n_in / 8) * 4;
     const size_t gb = static_cast<size_t>(n_out) * (n_in / gs) * 2;
     const uint64_t fp = fingerprint(w, wb) * 31 + fingerprint(s, gb) * 7 + fingerprint(b, gb);
@@ -1066,6 +1068,7 @@ int resident(const uint32_t* w, const uint16_t* s, const uint16_t* b, int n_out,
     if (gb) HIP_TRY(hipMemcpy(r.s, s, gb, hipMemcpyHostToDevice));
     if (gb) HIP_TRY(hipMemcpy(r.b, b, gb, hipMemcpyHostToDevice));
     r.fp = fp;
+    r.base = base ? base : static_cast<const void*>(w);
     *out = &r;
     return 0;
 }
@@ -1210,11 +1213,12 @@ int q4_dequant(const uint32_t* w, const uint16_t* scales, const uint16_t* biases
     // The reference indexes whole-matrix bases with rows [row0,row1)
     // (kernel/q4gemv.c:372).  The caller walks a matrix block by block
     // (hetero/cpu_model.py:129-135), so each row block is registered as its
-    // own resident matrix, keyed by the block's first-row addresses; a block
+    // own resident matrix, keyed by the block's first-row addresses and
+    // tagged with the matrix base w, which q4_release(w) matches; a block
     // that is the whole matrix shares q4_gemv's entry.
     const size_t wpr = static_cast<size_t>(n_in / 8), ng = static_cast<size_t>(n_in / gs);
     Resident* r;
-    if ((rc = resident(w + row0 * wpr, scales + row0 * ng, biases + row0 * ng, rows, n_in, gs, dev, &r)))
+    if ((rc = resident(w + row0 * wpr, scales + row0 * ng, biases + row0 * ng, rows, n_in, gs, dev, &r, w)))
         return rc;
     const size_t ny = static_cast<size_t>(rows) * n_in;
     if ((rc = grow_pinned(&d->pin_out, &d->pin_out_cap, ny))) return rc;
@@ -1231,7 +1235,7 @@ int q4_release(const void* w) {
     std::lock_guard<std::mutex> lock(g_mu);
     int n = 0;
     for (auto it = g_res.begin(); it != g_res.end();) {
-        if (std::get<1>(it->first) == w) {
+        if (std::get<1>(it->first) == w || it->second.base == w) {
             int cur = 0;
             (void)hipGetDevice(&cur);
             (void)hipSetDevice(std::get<0>(it->first));
@@ -1543,9 +1547,9 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
     }
     const int W = rem_nb ? (n_out - main_nb * BN < rem_nb * BN ? n_out - main_nb * BN : rem_nb * BN) : 0;
     const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * n_out;
-    if ((rc = ensure_raw(ws->xbf, ws->cap_xbf, mk * 2, st, "prefill"))) return rc;
+    if ((rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
     const size_t part_bytes = S > 1 ? S * mn * 4 : static_cast<size_t>(S2) * m * W * 4;
-    if (part_bytes && (rc = ensure_raw(ws->part, ws->cap_part, part_bytes, st, "prefill"))) return rc;
+    if (part_bytes && (rc = grow(*ws, ws->part, kWsPart, part_bytes, st, "prefill"))) return rc;
     const long n8 = static_cast<long>(mk / 8);
     hipLaunchKernelGGL(x_to_bf16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, st, x,
                        static_cast<uint4*>(ws->xbf), n8);

@@ -47,7 +47,9 @@ class GpuStage:
         self.hd = self.h // self.nh
         self.inter = cfg["intermediate_size"]
         self.s0 = kv_k[0].shape[1]
-        self.cap = self.s0 + max_new
+        self.max_new = int(max_new)
+        self.cap = self.s0 + self.max_new
+        self.steps_done = 0       # decode steps since the last reset (the cache holds max_new)
         dev = self.dev
 
         def t(a, dtype=None):
@@ -195,6 +197,7 @@ class GpuStage:
         with torch.cuda.graph(self.graph, stream=self.stream):
             self._step()
         torch.cuda.synchronize()
+        self.steps_done = 0
 
     def set_token(self, tok: int):
         self.tok.fill_(int(tok))
@@ -204,10 +207,22 @@ class GpuStage:
         rewritten as decoding proceeds) with `tok` as the next input."""
         self.pos.fill_(self.s0)
         self.tok.fill_(int(tok))
+        self.steps_done = 0
+
+    def _take(self, n: int):
+        """Claim n steps of the cache; past max_new the kernels would clamp
+        the position and decode wrong tokens without an error."""
+        if n < 0 or self.steps_done + n > self.max_new:
+            raise ValueError(f"{n} more decode steps after {self.steps_done} exceed max_new={self.max_new}; "
+                             "reset() first or build the stage with a larger max_new")
+        self.steps_done += n
 
     def run(self, n: int) -> List[int]:
-        """n free-running steps as back-to-back graph replays (no host sync in
-        between); returns the n greedy tokens."""
+        """n free-running steps from the last reset() as back-to-back graph
+        replays (no host sync in between); returns the n greedy tokens."""
+        if self.steps_done:
+            raise ValueError("run() starts from the initial context: reset() first")
+        self._take(n)
         for _ in range(n):
             self.graph.replay()
         self.torch.cuda.synchronize()
@@ -215,6 +230,7 @@ class GpuStage:
 
     def step(self) -> int:
         """One decode step (graph replay once captured); returns the greedy token."""
+        self._take(1)
         if self.graph is None:
             self._eager_step()
         else:

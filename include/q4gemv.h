@@ -64,7 +64,8 @@ int q4_gemv_batched(const uint32_t *w, const uint16_t *scales, const uint16_t *b
                     int nthreads);
 
 /* Drop the HBM copies registered for host weights at address w (every
- * shape); q4_release_all drops every registered matrix on every device.
+ * shape, and every row block q4_dequant registered for the matrix whose
+ * base is w); q4_release_all drops every registered matrix on every device.
  * Return the number of entries released. */
 int q4_release(const void *w);
 int q4_release_all(void);

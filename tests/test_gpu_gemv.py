@@ -249,3 +249,95 @@ def test_matrix_core_tile_variants(lib):
             got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
             torch.cuda.synchronize()
             assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} N={n_out} m={m}")
+
+
+def test_matrix_core_uneven_prep_slices(lib):
+    """The matrix-core x prep splits each row's groups over up to 8
+    workgroups in slices of ceil(G / slices): K = 6208 (97 groups, slices of
+    33/33/31) and K = 9024 (141 groups, 36/36/36/33) leave a short last slice,
+    and rows past M are zero-filled across uneven slices.  Bit-exact vs the
+    oracle at 3, 5 and 8 rows."""
+    import torch
+    o = oracle.Oracle()
+    for k_in, n_out in ((6208, 200), (9024, 96)):
+        w, s, b = synth.qlinear(700 + k_in, n_out, k_in, 64)
+        x = synth.activations(701, 8, k_in)
+        want = o.gemv_rows(w, s, b, x, 64)
+        tw, ts, tb, tx = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16), x))
+        for m in (3, 5, 8):
+            print(f"uneven prep slices K={k_in} N={n_out} m={m}", flush=True)
+            got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
+            torch.cuda.synchronize()
+            assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} N={n_out} m={m}")
+
+
+def test_release_drops_dequant_row_blocks(lib):
+    """q4_dequant registers each row block it is asked for under the block's
+    own address; q4_release(base) must drop those blocks too, so weights
+    rewritten in place after a release are uploaded again."""
+    o = oracle.Oracle()
+    n_out, n_in = 1536, 512
+    w, s, b = synth.qlinear(810, n_out, n_in, 64)
+    w, s, b = w.copy(), s.view(np.uint16).copy(), b.view(np.uint16).copy()
+    out = np.empty((512, n_in), np.float32)
+
+    def dq(r0, r1):
+        rc = lib.q4_dequant(w.ctypes.data, s.ctypes.data, b.ctypes.data, out.ctypes.data, r0, r1, n_in, 64, 1)
+        assert rc == 0, q4.last_error(lib)
+        return out[: r1 - r0].copy()
+
+    lib.q4_release(w.ctypes.data)
+    for r0 in (0, 512, 1024):
+        assert_bit_exact(dq(r0, r0 + 512), o.dequant(w, s.view(np.float16), b.view(np.float16), 64, r0, r0 + 512),
+                         f"rows {r0}..")
+    assert lib.q4_release(w.ctypes.data) == 3
+    assert lib.q4_release(w.ctypes.data) == 0
+    # new weights at the same addresses (every sampled word may even be equal:
+    # the release, not the fingerprint, has to make the library read them)
+    w2, s2, b2 = synth.qlinear(811, n_out, n_in, 64)
+    w[:] = w2
+    s[:] = s2.view(np.uint16)
+    b[:] = b2.view(np.uint16)
+    got = dq(512, 1024)
+    assert_bit_exact(got, o.dequant(w, s.view(np.float16), b.view(np.float16), 64, 512, 1024), "after release")
+    assert lib.q4_release(w.ctypes.data) == 1
+
+
+def test_workspace_grown_after_capture_keeps_graph_valid(lib):
+    """A graph captured with the stream's workspace at one size must stay
+    valid after an eager call on the same stream grows it: the buffers the
+    graph holds are retired, not freed.  Replays, with eager work between
+    them, match the eager result bit for bit."""
+    import torch
+    o = oracle.Oracle()
+    st = torch.cuda.Stream()
+    ws_, ss_, bs_ = synth.qlinear(820, 256, 1536, 64)
+    wb_, sb_, bb_ = synth.qlinear(821, 128, 18944, 64)
+    xs = synth.activations(822, 4, 1536)
+    xb = synth.activations(823, 4, 18944)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    small = (t(ws_), t(ss_.view(np.int16)), t(bs_.view(np.int16)))
+    big = (t(wb_), t(sb_.view(np.int16)), t(bb_.view(np.int16)))
+    txs, txb = t(xs), t(xb)
+    out_s = torch.empty((4, 256), device="cuda")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        q4.gemv_dev(*small, txs, out=out_s, stream=st)      # sizes the workspace for the small call
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        q4.gemv_dev(*small, txs, out=out_s, stream=st)
+    torch.cuda.synchronize()
+    want_s = o.gemv_rows(ws_, ss_, bs_, xs, 64)
+    want_b = o.gemv_rows(wb_, sb_, bb_, xb, 64)
+    for rep in range(3):
+        with torch.cuda.stream(st):
+            got_b = q4.gemv_dev(*big, txb, stream=st)       # grows the workspace (first time)
+        torch.cuda.synchronize()
+        assert_bit_exact(got_b.cpu().numpy(), want_b, f"eager big call {rep}")
+        out_s.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            g.replay()
+        torch.cuda.synchronize()
+        assert_bit_exact(out_s.cpu().numpy(), want_s, f"graph replay {rep}")
