@@ -31,10 +31,11 @@ def bf16_round(a):
 
 # (500, 16600, 1024) and (512, 18944, 3584) have more 128 x 128 tiles than one
 # round of resident workgroups holds, so their last tiles take the launch of
-# their own split along K (a partial last tile in the first of them)
+# their own split along K (a partial last tile in the first of them);
+# (512, 3584, 18944) is down_proj of a 512-token prompt, split along K
 @pytest.mark.parametrize("m,n_out,n_in", [(37, 200, 512), (130, 96, 1024), (512, 3584, 3584),
                                           (512, 512, 3584), (64, 3584, 18944), (500, 16600, 1024),
-                                          (512, 18944, 3584)])
+                                          (512, 18944, 3584), (512, 3584, 18944)])
 def test_gemm_bf16(m, n_out, n_in):
     import torch
     print(f"gemm m={m} n={n_out} k={n_in}", flush=True)
