@@ -1177,6 +1177,53 @@ int check_norm_args(const char* who, const float* x, const float* delta, const f
     return 0;
 }
 
+// ---------------------------------------------------- static scratch ----
+//
+// The workspace of q4_gemv_noalloc_dev: a fixed array in device memory, so
+// that call allocates nothing.  Sized for up to 8 rows at a time of
+// n_in <= kNoAllocMaxIn: the x planes (8 rows x n_in/8 words as uint4 for
+// the split path; 64 uint4 per group for the matrix-core prep -- both
+// 32768 uint4 at the limit), the group sums (8 rows x 512 groups) and the
+// 8 row scales.  Each GPU holds its own copy for the life of the process.
+constexpr int kNoAllocMaxIn = 32768;
+constexpr size_t kScrPlanes = static_cast<size_t>(kMaxM) * (kNoAllocMaxIn / 8);   // uint4
+constexpr size_t kScrXsum = static_cast<size_t>(kMaxM) * (kNoAllocMaxIn / 64);    // floats
+constexpr size_t kScrXscale = 64;                                                  // floats
+static_assert(kScrPlanes >= static_cast<size_t>(kNoAllocMaxIn / 64) * 2 * q4k::kMfArows * 2,
+              "the matrix-core prep fits the planes");
+static __device__ __align__(256) uint4 scratch[kScrPlanes + (kScrXsum + kScrXscale) / 4];
+
+// Device address of `scratch` per device (the array's name is only a host
+// stand-in), looked up once per device with that device current.
+std::mutex g_scr_mu;
+void* g_scr_ptr[64] = {};
+
+int scratch_workspace(Workspace* ws) {
+    int dev;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(Q4_EARG, "device %d: the static scratch is kept for devices 0..63", dev);
+    void* p;
+    {
+        std::lock_guard<std::mutex> lock(g_scr_mu);
+        if (!g_scr_ptr[dev]) {
+            void* a = nullptr;
+            HIP_TRY(hipGetSymbolAddress(&a, HIP_SYMBOL(scratch)));
+            if (!a) return fail(Q4_EHIP, "hipGetSymbolAddress(scratch) gave a null address");
+            g_scr_ptr[dev] = a;
+        }
+        p = g_scr_ptr[dev];
+    }
+    uint4* base = static_cast<uint4*>(p);
+    ws->fixed = true;
+    ws->planes = base;
+    ws->xsum = reinterpret_cast<float*>(base + kScrPlanes);
+    ws->xscale = ws->xsum + kScrXsum;
+    ws->cap[kWsPlanes] = kScrPlanes * sizeof(uint4);
+    ws->cap[kWsXsum] = kScrXsum * sizeof(float);
+    ws->cap[kWsXscale] = kScrXscale * sizeof(float);
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================ C-ABI ====
@@ -1286,6 +1333,29 @@ int q4_gemv_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biase
         const int mm = m - m0 < kMaxM ? m - m0 : kMaxM;
         rc = gemv_rows(w, scales, biases, x + static_cast<size_t>(m0) * n_in,
                        out + static_cast<size_t>(m0) * n_out, mm, n_out, n_in, gs, st, *ws);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+int q4_gemv_noalloc_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const float* x,
+                        float* out, int m, int n_out, int n_in, int gs, void* stream) {
+    int rc = check_gemv_shape(n_out, n_in, gs);
+    if (rc) return rc;
+    if (m < 0) return fail(Q4_EARG, "m=%d", m);
+    if (n_in > kNoAllocMaxIn)
+        return fail(Q4_EARG, "q4_gemv_noalloc_dev takes n_in <= %d (got %d): its scratch is fixed", kNoAllocMaxIn,
+                    n_in);
+    if (n_out == 0 || m == 0) return 0;
+    if (!w || !scales || !biases || !x || !out) return fail(Q4_EARG, "null pointer");
+    if (reinterpret_cast<uintptr_t>(w) & 15) return fail(Q4_EARG, "w must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Workspace ws;
+    if ((rc = scratch_workspace(&ws))) return rc;
+    for (int m0 = 0; m0 < m; m0 += kMaxM) {
+        const int mm = m - m0 < kMaxM ? m - m0 : kMaxM;
+        rc = gemv_rows(w, scales, biases, x + static_cast<size_t>(m0) * n_in,
+                       out + static_cast<size_t>(m0) * n_out, mm, n_out, n_in, gs, st, ws);
         if (rc) return rc;
     }
     return 0;

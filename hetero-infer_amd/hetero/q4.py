@@ -20,7 +20,7 @@ PKG_PARENT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
 
 EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
-           "q4_last_error", "q4_gemv_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
+           "q4_last_error", "q4_gemv_dev", "q4_gemv_noalloc_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
            "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_dequant_dev", "q4_dequant_bf16_dev",
            # decode-step kernels (include/q4decode.h)
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
@@ -51,6 +51,8 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_last_error.restype = ctypes.c_char_p
         lib.q4_gemv_dev.argtypes = [_VP] * 5 + [_I] * 4 + [_VP]
         lib.q4_gemv_dev.restype = _I
+        lib.q4_gemv_noalloc_dev.argtypes = [_VP] * 5 + [_I] * 4 + [_VP]
+        lib.q4_gemv_noalloc_dev.restype = _I
         lib.q4_gemv_multi_dev.argtypes = [_I] + [_VP] * 6 + [_I] * 3 + [_VP]
         lib.q4_gemv_multi_dev.restype = _I
         lib.q4_gate_up_silu_dev.argtypes = [_VP] * 8 + [_I] * 4 + [_VP]

@@ -89,6 +89,19 @@ int q4_gemv_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biase
                 const float *x, float *out, int m, int n_out, int n_in, int gs,
                 void *stream);
 
+/* q4_gemv_dev for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments, arithmetic and results as
+ * q4_gemv_dev, but every scratch buffer (the x planes, group sums and row
+ * scales of blocks of 3..8 rows and of group sizes other than 64) is a fixed
+ * array in device memory, one per GPU, held until the process ends; the call
+ * makes no hipMalloc/hipFree.  Limit: n_in <= 32768 (larger n_in returns
+ * Q4_EARG).  Every call on one GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (other streams, other threads) race. */
+int q4_gemv_noalloc_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                        const float *x, float *out, int m, int n_out, int n_in, int gs,
+                        void *stream);
+
 /* Up to four matrices that share the activations x (q/k/v, gate/up) in one
  * launch (1..2 rows; 3..8 rows: x quantised once, then one matrix-core launch
  * per matrix): out[k] is [m][n_out[k]] = W_k x, each row bit-identical to
