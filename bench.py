@@ -1,23 +1,33 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 int4 GEMV path on one MI355X.
 
-Workload (one "step"): the M=1 decode sweep of every Qwen2.5-7B 4-bit
-projection -- 28 layers x (q, k, v, o, gate, up, down) + lm_head, 197 GEMVs,
-3.99 GB of packed weights, fp16 scales/biases, fp32 x and y.  Each layer has
-its own weights (3.9 GB resident in HBM, far above the 256 MB Infinity
-Cache), so every step streams every weight from HBM once.  Each projection is
-one q4_gemv_dev call (its own x prologue included, as q4_gemv does per call);
-the step is captured once in a HIP graph and replayed.
+Workload (one "step", the headline): the M=1 decode sweep of every
+Qwen2.5-7B 4-bit projection -- 28 layers x (q, k, v, o, gate, up, down) +
+lm_head, 3.99 GB of packed weights, fp16 scales/biases, fp32 x and y -- in
+decode order with the projections that share x in one launch (q/k/v, and
+gate+up): 4 launches per layer + lm_head = 113 launches per step, each with
+its own x prologue.  Each layer has its own weights (3.9 GB resident in HBM,
+far above the 256 MB Infinity Cache), so every step streams every weight
+from HBM once.  The step is captured once in a HIP graph and replayed.  The
+same sweep with one launch per projection (197 per step, as the reference's
+caller makes one q4_gemv call per projection) is reported beside it.
 
 Prints one JSON line:
-  value      whole-step algorithmic GB/s (packed W + fp16 scales/biases +
-             fp32 x and y per call), inputs resident in HBM
-  roofline   the GEMV kernel's achieved GB/s vs 8 TB/s, from HIP events on
-             the launch stream over the timed replays
-  per_shape  GB/s of each projection shape (events over 28 back-to-back
-             calls on distinct weights)
+  value         whole-step algorithmic GB/s (packed W + fp16 scales/biases +
+                fp32 x and y per projection), inputs resident in HBM
+  roofline      the GEMV kernel's achieved GB/s vs 8 TB/s, from HIP events on
+                the launch stream over the timed replays
+  per_shape     GB/s of each projection shape (events over back-to-back calls
+                on distinct weights)
+  small_m, prefill, wire, load
+                the small-M / MLP block, M=512 prefill GEMM, activation wire
+                codec and checkpoint-to-HBM legs
+  decode        the 28-layer decode step (device-resident, HIP graph), its
+                token agreement with the reference path's fixture, and the
+                host CPU's decode rate on the reference kernel
+  dropin        the NumPy stage on libq4gemv.so through the host-pointer ABI
   cpu_baseline  the reference kernel/q4gemv.c (compiled from source, tuned on
-             this host) timed on a bounded sample of the same sweep
+                this host) timed on a bounded sample of the same sweep
 """
 from __future__ import annotations
 
@@ -288,9 +298,9 @@ def load_bench(torch, dev, layers=4, reps=2):
     import numpy as np
     from safetensors import safe_open
     from safetensors.numpy import save_file
-    from hetero import cpu_model
+    from hetero import qwen2
     from hetero.shard import ShardSpec, WeightIndex
-    cfg = cpu_model.qwen2_7b_config(layers)
+    cfg = qwen2.qwen2_7b_config(layers)
     h, inter = cfg["hidden_size"], cfg["intermediate_size"]
     kvd = h // cfg["num_attention_heads"] * cfg["num_key_value_heads"]
     rng = np.random.default_rng(0)
@@ -359,116 +369,183 @@ def load_bench(torch, dev, layers=4, reps=2):
         shutil.rmtree(d, ignore_errors=True)
 
 
-def decode_weights(torch, cfg, dev, seed=99):
-    """Random-init 4-bit Qwen2 weights (reference tensor names), generated on
-    the GPU and copied to host arrays for the NumPy stage."""
+DECODE_FIXTURE = os.path.join(ROOT, "tests", "golden", "decode_qwen7b.json")
+
+
+def decode_model(torch, dev):
+    """The Qwen2.5-7B-architecture decode workload of the committed fixture
+    (28 layers, fp16 KV cache holding 2048 positions, seeded random-init
+    4-bit weights), generated on the GPU; returns (cfg, meta, w, ks, vs)."""
+    from hetero import qwen2
+    with open(DECODE_FIXTURE) as f:
+        meta = json.load(f)
+    cfg = meta["config"]
+    w = qwen2.synthetic_weights_torch(cfg, meta["seed"], dev)
+    ks, vs = qwen2.synthetic_context_torch(cfg, meta["context"], meta["context_seed"], dev)
+    torch.cuda.synchronize()
+    return cfg, meta, w, ks, vs
+
+
+def decode_bench(torch, dev, cfg, meta, w, ks, vs, steps=128):
+    """Device-resident decode (one HIP graph replay per token) on the
+    fixture's workload: tok/s over `steps` free-running steps, and token
+    agreement with the reference path's tokens (tests/golden/decode_qwen7b.npz,
+    written by the oracle on kernel/q4gemv.c), free-running and
+    teacher-forced."""
     import numpy as np
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(seed)
-    host = {}
-    h, inter, v = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"]
-    kvd = h // cfg["num_attention_heads"] * cfg["num_key_value_heads"]
-
-    def lin(name, n_out, n_in, bias=False):
-        w, s, b = make_weights(torch, gen, n_out, n_in, dev)
-        host[f"{name}.weight"] = w.cpu().numpy().view(np.uint32)
-        host[f"{name}.scales"] = s.cpu().numpy().view(np.float16)
-        host[f"{name}.biases"] = b.cpu().numpy().view(np.float16)
-        if bias:
-            host[f"{name}.bias"] = (torch.randn(n_out, device=dev, generator=gen) * 0.02).cpu().numpy()
-
-    lin("model.embed_tokens", v, h)
-    for i in range(cfg["num_hidden_layers"]):
-        p = f"model.layers.{i}"
-        lin(f"{p}.self_attn.q_proj", h, h, True)
-        lin(f"{p}.self_attn.k_proj", kvd, h, True)
-        lin(f"{p}.self_attn.v_proj", kvd, h, True)
-        lin(f"{p}.self_attn.o_proj", h, h)
-        lin(f"{p}.mlp.gate_proj", inter, h)
-        lin(f"{p}.mlp.up_proj", inter, h)
-        lin(f"{p}.mlp.down_proj", h, inter)
-        for nrm in ("input_layernorm", "post_attention_layernorm"):
-            host[f"{p}.{nrm}.weight"] = (1.0 + torch.randn(h, device=dev, generator=gen) * 0.02).cpu().numpy()
-    host["model.norm.weight"] = (1.0 + torch.randn(h, device=dev, generator=gen) * 0.02).cpu().numpy()
-    lin("lm_head", v, h)
-    kv_k = [(torch.randn((cfg["num_key_value_heads"], 2048, h // cfg["num_attention_heads"]),
-                         device=dev, generator=gen)).half().cpu().numpy() for _ in range(cfg["num_hidden_layers"])]
-    kv_v = [(torch.randn((cfg["num_key_value_heads"], 2048, h // cfg["num_attention_heads"]),
-                         device=dev, generator=gen)).half().cpu().numpy() for _ in range(cfg["num_hidden_layers"])]
-    return host, kv_k, kv_v
-
-
-def decode_bench(torch, dev, steps=128, start_token=151643, ref_rows=1, ref_threads=16, check=True):
-    """Qwen2.5-7B-architecture decode step (28 layers, fp16 KV cache at 2048
-    context, greedy over 152064): device-resident tok/s, and token agreement
-    with the NumPy stage running the reference kernel on the host."""
-    import copy
-    import numpy as np
-    from hetero import cpu_model
     from hetero.gpu_model import GpuStage
-
-    cfg = cpu_model.qwen2_7b_config(28)
-    t0 = time.perf_counter()
-    w, kv_k, kv_v = decode_weights(torch, cfg, dev)
-    log(f"decode weights {time.perf_counter() - t0:.1f}s")
-    g = GpuStage(cfg, w, kv_k, kv_v, max_new=steps)
-    g.reset(start_token)
+    start = meta["start_token"]
+    g = GpuStage(cfg, w, ks, vs, max_new=steps)
+    g.reset(start)
     g.capture()
-    g.reset(start_token)
+    g.reset(start)
     g.run(2)                                     # warm replays
-    g.reset(start_token)
+    g.reset(start)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     dev_tokens = g.run(steps)
     dev_s = time.perf_counter() - t0
-    res = {"workload": "Qwen2-architecture decode: 28 layers, hidden 3584, 28/4 heads, head_dim 128, "
-                       "random-init 4-bit weights, fp16 KV cache at 2048 context, greedy over 152064, "
-                       f"{steps} steps, one HIP graph replay per token",
-           "tok_s": round(steps / dev_s, 1), "ms_per_token": round(dev_s * 1e3 / steps, 3)}
-    ref = reference_decode(cfg, w, kv_k, kv_v, steps, start_token, ref_rows, ref_threads) if check else None
-    if ref is not None:
-        ref_tokens, ref_s = ref
-        free = sum(int(a == b) for a, b in zip(dev_tokens, ref_tokens))
-        prefix = next((i for i, (a, b) in enumerate(zip(dev_tokens, ref_tokens)) if a != b), steps)
-        g.reset(start_token)
-        forced = g.generate(steps, tokens_in=[start_token] + ref_tokens[:-1])
-        tf = sum(int(a == b) for a, b in zip(forced, ref_tokens))
-        res.update({"agree_free_running": f"{free}/{steps}", "identical_prefix": prefix,
-                    "agree_teacher_forced": f"{tf}/{steps}",
-                    "cpu_reference_tok_s": round(steps / ref_s, 2),
-                    "cpu_reference": f"NumPy stage (hetero/cpu_model.py) on kernel/q4gemv.c ROWS={ref_rows}, "
-                                     f"{ref_threads} threads"})
+    res = {"workload": meta["workload"] + ", one HIP graph replay per token",
+           "steps": steps, "tok_s": round(steps / dev_s, 1), "ms_per_token": round(dev_s * 1e3 / steps, 3)}
+    fx = np.load(DECODE_FIXTURE.replace(".json", ".npz"))
+    ref = fx["greedy_tokens"].tolist()[:steps]
+    n = len(ref)
+    prefix = next((i for i, (a, b) in enumerate(zip(dev_tokens, ref)) if a != b), n)
+    agree = {}
+    for seq in ("greedy", "forced"):
+        inputs = fx[f"{seq}_inputs"].tolist()[:n]
+        g.reset(inputs[0])
+        got = g.generate(n, tokens_in=inputs)
+        agree[seq] = sum(int(a == b) for a, b in zip(got, fx[f"{seq}_tokens"].tolist()[:n]))
+    margin = None
+    if prefix < n:
+        top = fx["greedy_top_val"][prefix]
+        margin = round(float(top[0] - top[1]), 5)
+    res.update({"free_running_identical_prefix": f"{prefix}/{n}",
+                "reference_top2_margin_at_divergence": margin,
+                "agree_teacher_forced": f"{agree['greedy']}/{n}",
+                "agree_teacher_forced_random_tokens": f"{agree['forced']}/{n}",
+                "reference_tokens": "tests/golden/decode_qwen7b.npz (oracle/decode.py on kernel/q4gemv.c)"})
+    del g
+    torch.cuda.empty_cache()
     return res
 
 
-def reference_decode(cfg, w, kv_k, kv_v, steps, start_token, rows, threads):
-    """The same 128 greedy steps by the NumPy stage on the reference kernel
-    compiled from source (host CPU baseline and token oracle)."""
+def host_arrays(torch, w, ks, vs):
+    """The decode model's tensors as host NumPy arrays (weights uint32,
+    scales/biases float16, the rest float32; KV context float16)."""
     import numpy as np
-    import oracle
-    from hetero import cpu_model
-    if not os.path.exists(oracle.ref_path(rows)):
-        return None
-    os.environ.setdefault("HETERO_KERNEL_THREADS", str(max(threads, 1)))
-    cpu_model.NTHREADS = threads
-    stage = cpu_model.Stage(cfg, w, lib=oracle.load_ref(rows))
-    caches = []
-    for k, v in zip(kv_k, kv_v):
-        c = cpu_model.KVCache(np.float16)
-        c.fill(k[None], v[None])
-        caches.append(c)
-    tok, out = start_token, []
+    hw = {}
+    for k, t in w.items():
+        a = t.cpu().numpy()
+        hw[k] = a.view(np.uint32) if k.endswith(".weight") and a.dtype == np.int32 else a
+    return hw, [k.cpu().numpy() for k in ks], [v.cpu().numpy() for v in vs]
+
+
+def dropin_bench(cfg, meta, hw, hks, hvs, steps=12):
+    """The integration mode the reference's caller uses: the NumPy stage
+    (hetero/numpy_stage.py) with every projection a host-pointer q4_gemv
+    call into libq4gemv.so (x 14 KB in, y out through pinned staging; the
+    weights uploaded once and kept resident).  tok/s over `steps` greedy
+    steps after one warm-up step (which uploads the weights), the tokens
+    checked against the reference path's, and the latency of one q4_gemv
+    call on the q_proj shape."""
+    import numpy as np
+    from hetero import numpy_stage, q4
+    lib = q4.load()
+    st = numpy_stage.Stage(cfg, hw, lib=lib)
+    caches = st.new_caches(hks, hvs, extra=steps + 1, dtype=np.float16)
+    start = meta["start_token"]
+    t0 = time.perf_counter()
+    tok = numpy_stage.greedy(st(np.array([[start]]), caches, last_only=True))
+    warm_s = time.perf_counter() - t0
+    toks = [tok]
     t0 = time.perf_counter()
     for _ in range(steps):
-        logits = stage(np.array([[tok]]), caches, last_only=True)
-        tok = cpu_model.greedy(logits)
-        out.append(tok)
-    return out, time.perf_counter() - t0
+        tok = numpy_stage.greedy(st(np.array([[tok]]), caches, last_only=True))
+        toks.append(tok)
+    dt = time.perf_counter() - t0
+    ref = meta["tokens"][:len(toks)]
+    # one q4_gemv call: 3584 -> 3584 (7 KB of x in, 14 KB of y out)
+    qp = st.layers[0].q
+    x = np.random.default_rng(0).standard_normal(qp.n_in).astype(np.float32)
+    out = np.empty(qp.n_out, np.float32)
+    args = (qp.w.ctypes.data, qp.scales.ctypes.data, qp.biases.ctypes.data, x.ctypes.data, out.ctypes.data,
+            qp.n_out, qp.n_in, qp.group_size, 0)
+    for _ in range(20):
+        lib.q4_gemv(*args)
+    reps = 500
+    t1 = time.perf_counter()
+    for _ in range(reps):
+        lib.q4_gemv(*args)
+    call_us = (time.perf_counter() - t1) / reps * 1e6
+    lib.q4_release_all()
+    return {"workload": "NumPy stage (hetero/numpy_stage.py) on libq4gemv.so through the host-pointer "
+                        "q4_gemv ABI, the decode fixture's model and context",
+            "tok_s": round(steps / dt, 2), "ms_per_token": round(dt * 1e3 / steps, 2),
+            "first_step_s_incl_weight_upload": round(warm_s, 2),
+            "agree_with_reference_tokens": f"{sum(int(a == b) for a, b in zip(toks, ref))}/{len(toks)}",
+            "q4_gemv_call_us_3584x3584": round(call_us, 1)}
+
+
+def host_statement():
+    """The host the CPU baselines run on: CPU model, logical cpus allowed,
+    physical cores among them, NUMA nodes, last-level cache, pinning."""
+    allowed = sorted(os.sched_getaffinity(0))
+    info = {"cpu_model": None, "logical_cpus_allowed": len(allowed), "os_cpu_count": os.cpu_count(),
+            "physical_cores_allowed": None, "numa_nodes": None, "llc_bytes": None,
+            "pinning": f"process affinity {allowed[0]}-{allowed[-1]}" if allowed == list(range(allowed[0], allowed[-1] + 1))
+            else f"process affinity {allowed}"}
+    try:
+        cores, cur = set(), {}
+        with open("/proc/cpuinfo") as f:
+            for line in f.read().split("\n") + [""]:
+                if not line.strip():
+                    if cur.get("processor") is not None and int(cur["processor"]) in allowed:
+                        cores.add((cur.get("physical id", "0"), cur.get("core id", cur["processor"])))
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                cur[k.strip()] = v.strip()
+                if k.strip() == "model name" and info["cpu_model"] is None:
+                    info["cpu_model"] = v.strip()
+        info["physical_cores_allowed"] = len(cores) or None
+    except OSError:
+        pass
+    try:
+        nodes = {}
+        base = "/sys/devices/system/node"
+        for n in sorted(os.listdir(base)):
+            if n.startswith("node") and n[4:].isdigit():
+                with open(os.path.join(base, n, "cpulist")) as f:
+                    cl = f.read().strip()
+                cpus = set()
+                for part in cl.split(","):
+                    if part:
+                        a, _, b = part.partition("-")
+                        cpus |= set(range(int(a), int(b or a) + 1))
+                if cpus & set(allowed):
+                    nodes[n] = cl
+        info["numa_nodes"] = nodes
+    except OSError:
+        pass
+    try:
+        with open(f"/sys/devices/system/cpu/cpu{allowed[0]}/cache/index3/size") as f:
+            v = f.read().strip()
+        mult = {"K": 1024, "M": 1 << 20}.get(v[-1], 1)
+        info["llc_bytes"] = int(v.rstrip("KM")) * mult
+    except (OSError, ValueError):
+        pass
+    return info
 
 
 def cpu_baseline(budget_s: float = 20.0):
-    """Reference kernel/q4gemv.c on this host, tuned as kernel/autotune.py does."""
-    import ctypes
+    """The reference kernel/q4gemv.c, built from source (oracle/_ref, ROWS 1/2/4/8),
+    tuned on this host by the procedure of kernel/autotune.py:49-75 (every ROWS x
+    threads in {1, 2, 4, cpus, 2 cpus} within [1, 16]; 4 warm-up and 25 timed calls
+    per shape) on the Qwen2.5-7B layer shapes, then timed on the M=1 sweep: passes
+    over distinct layers whose weights span at least twice the last-level cache,
+    the median of at least 5 repeats, extrapolated to 28 layers + lm_head."""
     import numpy as np
     import oracle
     from hetero import synth
@@ -476,15 +553,18 @@ def cpu_baseline(budget_s: float = 20.0):
     if not os.path.exists(oracle.ref_path(1)):
         return {"value": None, "unit": "GB/s", "cores": 0, "kind": "reference",
                 "sample": "unavailable: oracle/_ref not built"}
-    cpus = len(os.sched_getaffinity(0))
+    host = host_statement()
+    cpus = host["logical_cpus_allowed"]
     threads_opts = sorted({1, 2, 4, cpus, 2 * cpus} & set(range(1, 17)))
     os.environ["HETERO_KERNEL_THREADS"] = str(max(threads_opts))   # pool size (q4gemv.c:218-223)
-    rng_layers = 2
-    layers = []
-    for li in range(rng_layers):
-        layers.append([synth.qlinear(5000 + 10 * li + j, n_out, n_in, GS)
-                       for j, (_, n_in, n_out) in enumerate(LAYER_SHAPES)])
-    head = synth.qlinear(5999, HEAD_SHAPE[2], HEAD_SHAPE[1], GS)
+    layer_bytes = sum(gemv_bytes(1, n_out, n_in) for _, n_in, n_out in LAYER_SHAPES)
+    llc = host["llc_bytes"] or (256 << 20)
+    n_rot = max(2, -(-2 * llc // layer_bytes))
+    t_gen = time.perf_counter()
+    layers = [[synth.qlinear_ih_np(5000 + 10 * li + j, n_out, n_in, GS, tag="cpu.")
+               for j, (_, n_in, n_out) in enumerate(LAYER_SHAPES)] for li in range(n_rot)]
+    head = synth.qlinear_ih_np(5999, HEAD_SHAPE[2], HEAD_SHAPE[1], GS, tag="cpu.")
+    gen_s = time.perf_counter() - t_gen
     xs = {k: synth.activations(77, 1, k)[0] for k in (3584, 18944)}
     outs = {n: np.empty(n, np.float32) for n in (512, 3584, 18944, 152064)}
 
@@ -495,55 +575,86 @@ def cpu_baseline(budget_s: float = 20.0):
                          outs[n_out].ctypes.data, n_out, n_in, GS, nt)
         assert rc == 0
 
-    def layer_time(lib, nt, reps):
-        t0 = time.perf_counter()
-        for r in range(reps):
-            for wsb in layers[r % rng_layers]:
-                call(lib, wsb, nt)
-        return (time.perf_counter() - t0) / reps
-
-    # autotune (kernel/autotune.py:49-75): ROWS x threads, on one layer's shapes
-    best = None
+    # autotune: kernel/autotune.py:40-45 per shape (4 warm-up + 25 timed), summed over a layer's shapes
     t_start = time.perf_counter()
+    tune = []
     libs = {}
     for rows in (1, 2, 4, 8):
         libs[rows] = oracle.load_ref(rows)
         for nt in threads_opts:
-            layer_time(libs[rows], nt, 1)
-            t = layer_time(libs[rows], nt, 3)
-            if best is None or t < best[2]:
-                best = (rows, nt, t)
-    rows, nt, _ = best
-    lib = libs[rows]
+            tot = 0.0
+            for wsb in layers[0]:
+                for _ in range(4):
+                    call(libs[rows], wsb, nt)
+                t0 = time.perf_counter()
+                for _ in range(25):
+                    call(libs[rows], wsb, nt)
+                tot += (time.perf_counter() - t0) / 25
+            tune.append((tot, rows, nt))
+    best_t, rows, nt = min(tune)
+    tuning = {"rows": rows, "threads": nt, "seconds": best_t, "cpus": cpus, "arch": os.uname().machine}
     tune_s = time.perf_counter() - t_start
-    # timed sample: layers (rotating copies) + lm_head, 4 warmup + N timed
-    for _ in range(4):
-        layer_time(lib, nt, 1)
-    reps = 0
-    t_layers = 0.0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s * 0.6 or reps < 5:
-        t_layers += layer_time(lib, nt, 1)
-        reps += 1
-    t_layer = t_layers / reps
+    lib = libs[rows]
+    # timed sample: each repeat is one pass over the n_rot distinct layers
+    for li in range(n_rot):
+        for wsb in layers[li]:
+            call(lib, wsb, nt)
+    per_layer, t0 = [], time.perf_counter()
+    while len(per_layer) < 5 or (time.perf_counter() - t0 < budget_s * 0.6 and len(per_layer) < 200):
+        t1 = time.perf_counter()
+        for li in range(n_rot):
+            for wsb in layers[li]:
+                call(lib, wsb, nt)
+        per_layer.append((time.perf_counter() - t1) / n_rot)
+    heads = []
     call(lib, head, nt)
-    hreps = 0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < budget_s * 0.2 or hreps < 3:
+    while len(heads) < 5 or (time.perf_counter() - t0 < budget_s * 0.2 and len(heads) < 100):
+        t1 = time.perf_counter()
         call(lib, head, nt)
-        hreps += 1
-    t_head = (time.perf_counter() - t0) / hreps
-    sweep_bytes = LAYERS * sum(gemv_bytes(1, n_out, n_in) for _, n_in, n_out in LAYER_SHAPES) \
-        + gemv_bytes(1, HEAD_SHAPE[2], HEAD_SHAPE[1])
+        heads.append(time.perf_counter() - t1)
+    t_layer, t_head = float(np.median(per_layer)), float(np.median(heads))
+    sweep_bytes = LAYERS * layer_bytes + gemv_bytes(1, HEAD_SHAPE[2], HEAD_SHAPE[1])
     t_sweep = LAYERS * t_layer + t_head
+    p10, p90 = (float(np.percentile(per_layer, q)) for q in (10, 90))
     return {"value": round(sweep_bytes / t_sweep / 1e9, 3), "unit": "GB/s", "cores": nt,
-            "kind": "reference", "rows": rows,
-            "sample": (f"kernel/q4gemv.c (clang -O3 -mavx2 -mfma -mf16c, ROWS={rows}, "
-                       f"{nt} threads, tuned over ROWS 1/2/4/8 x threads {threads_opts} in "
-                       f"{tune_s:.1f}s) on {cpus} host cpus: {reps} passes over one layer's 7 "
-                       f"projections (2 rotating weight copies) + {hreps} lm_head calls, "
-                       f"extrapolated to 28 layers + lm_head: {t_sweep*1e3:.1f} ms per sweep"),
-            "ms_per_sweep": round(t_sweep * 1e3, 3)}
+            "kind": "reference", "rows": rows, "tuning_json": tuning, "host": host,
+            "ms_per_sweep": round(t_sweep * 1e3, 3),
+            "layer_ms_median_p10_p90": [round(t_layer * 1e3, 3), round(p10 * 1e3, 3), round(p90 * 1e3, 3)],
+            "repeats": {"layer_passes": len(per_layer), "lm_head_calls": len(heads)},
+            "sample": (f"kernel/q4gemv.c (clang -O3 -mavx2 -mfma -mf16c, ROWS={rows}, {nt} threads; tuned over "
+                       f"ROWS 1/2/4/8 x threads {threads_opts} on the 7 layer shapes in {tune_s:.1f}s) on "
+                       f"{cpus} host cpus ({host['physical_cores_allowed']} physical cores, {host['cpu_model']}): "
+                       f"median of {len(per_layer)} passes over {n_rot} distinct layers "
+                       f"({n_rot * layer_bytes / 1e6:.0f} MB, >= 2x the {llc / 1e6:.0f} MB last-level cache) "
+                       f"and of {len(heads)} lm_head calls, extrapolated to 28 layers + lm_head: "
+                       f"{t_sweep * 1e3:.1f} ms per sweep (inputs generated in {gen_s:.1f}s)")}
+
+
+def cpu_decode_baseline(cfg, meta, hw, hks, hvs, rows, threads, steps=4):
+    """Decode tok/s of the reference path on this host: the oracle's NumPy
+    decode stage (oracle/decode.py) with every projection on the reference
+    kernel/q4gemv.c built from source (tuned ROWS and threads), the fixture's
+    workload, a bounded number of steps after one warm-up step; its tokens
+    are checked against the fixture's."""
+    import oracle
+    from oracle.decode import DecodeOracle, greedy
+    if not os.path.exists(oracle.ref_path(rows)):
+        return None
+    os.environ.setdefault("HETERO_KERNEL_THREADS", str(max(threads, 1)))
+    orc = DecodeOracle(cfg, hw, hks, hvs, oracle.load_ref(rows), extra=steps + 1, nthreads=threads)
+    tok = greedy(orc.logits(meta["start_token"]))
+    toks = [tok]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = greedy(orc.logits(tok))
+        toks.append(tok)
+    dt = time.perf_counter() - t0
+    ref = meta["tokens"][:len(toks)]
+    return {"tok_s": round(steps / dt, 3), "ms_per_token": round(dt * 1e3 / steps, 1), "steps": steps,
+            "agree_with_fixture": f"{sum(int(a == b) for a, b in zip(toks, ref))}/{len(toks)}",
+            "kind": "reference", "cores": threads,
+            "sample": f"oracle/decode.py on kernel/q4gemv.c ROWS={rows}, {threads} threads, {steps} timed steps"}
 
 
 def main():
@@ -570,8 +681,9 @@ def main():
                     help="only the small-M section (for rocprof runs)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode step (for rocprof runs)")
-    ap.add_argument("--no-decode-check", action="store_true",
-                    help="skip the token-agreement run of the NumPy stage on the host")
+    ap.add_argument("--no-dropin", action="store_true",
+                    help="skip the NumPy stage on libq4gemv.so through the host-pointer ABI")
+    ap.add_argument("--dropin-only", action="store_true", help="only the host-pointer drop-in leg")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a 256 MiB device copy: the known-size reference for PMC byte counters")
     args = ap.parse_args()
@@ -595,8 +707,16 @@ def main():
         print(json.dumps({"wire": res}), flush=True)
         return
     if args.decode_only:
-        res = decode_bench(torch, dev, steps=args.decode_steps, check=not args.no_decode_check)
+        cfg, meta, w, ks, vs = decode_model(torch, dev)
+        res = decode_bench(torch, dev, cfg, meta, w, ks, vs, steps=args.decode_steps)
         print(json.dumps({"decode": res}), flush=True)
+        return
+    if args.dropin_only:
+        cfg, meta, w, ks, vs = decode_model(torch, dev)
+        hw, hks, hvs = host_arrays(torch, w, ks, vs)
+        del w, ks, vs
+        torch.cuda.empty_cache()
+        print(json.dumps({"dropin": dropin_bench(cfg, meta, hw, hks, hvs)}), flush=True)
         return
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
@@ -758,7 +878,7 @@ def main():
     }
     if args.sweep_only:
         args.no_prefill = args.no_cpu_baseline = args.no_decode = args.no_small_m = args.no_wire = True
-        args.no_load = True
+        args.no_load = args.no_dropin = True
     if not args.no_small_m:
         log("small-M ...")
         result["small_m"] = small_m_bench(torch, lib, layers, dev)
@@ -781,12 +901,25 @@ def main():
         threads = result["cpu_baseline"].get("cores", 16) or 16
     else:
         result["cpu_baseline"] = None
-    if not args.no_decode:
+    if not (args.no_decode and args.no_dropin):
         del layers, head
         torch.cuda.empty_cache()
-        log("decode ...")
-        result["decode"] = decode_bench(torch, dev, steps=args.decode_steps, ref_rows=rows,
-                                        ref_threads=threads)
+        cfg, meta, w, ks, vs = decode_model(torch, dev)
+        if not args.no_decode:
+            log("decode ...")
+            result["decode"] = decode_bench(torch, dev, cfg, meta, w, ks, vs, steps=args.decode_steps)
+        hw = hks = hvs = None
+        if not args.no_dropin or not args.no_cpu_baseline:
+            hw, hks, hvs = host_arrays(torch, w, ks, vs)
+        del w, ks, vs
+        torch.cuda.empty_cache()
+        if not args.no_dropin:
+            log("drop-in (host-pointer ABI) ...")
+            result["dropin"] = dropin_bench(cfg, meta, hw, hks, hvs)
+        if not args.no_cpu_baseline and not args.no_decode:
+            log("cpu decode baseline ...")
+            result.setdefault("decode", {})["cpu_baseline"] = cpu_decode_baseline(cfg, meta, hw, hks, hvs, rows,
+                                                                                 threads)
     print(json.dumps(result), flush=True)
 
 

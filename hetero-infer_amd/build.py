@@ -55,8 +55,10 @@ def _run(cmd, what, verbose):
         raise RuntimeError(f"hipcc failed ({r.returncode}) building {what}")
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    os.makedirs(os.path.dirname(OUT), exist_ok=True)
+def build(verbose: bool = False, jobs: int | None = None, out: str = OUT, defines=()) -> str:
+    """Compile every object in parallel and link `out`; `defines` are extra
+    -D flags for every object."""
+    os.makedirs(os.path.dirname(out), exist_ok=True)
     cc = hipcc()
     inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
     jobs = jobs or min(16, os.cpu_count() or 4)
@@ -67,16 +69,16 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
             obj = os.path.join(tmpd, f"stream_m{mr}_p{pair}_r{ring}.o")
             units.append((INST, obj, [f"-DQ4_MR={mr}", f"-DQ4_PAIR={pair}", f"-DQ4_RING={ring}"]))
         with ThreadPoolExecutor(max_workers=jobs) as ex:
-            futs = [ex.submit(_run, [cc, *HIPCC_FLAGS, *inc, *defs, "-c", "-o", obj, src],
+            futs = [ex.submit(_run, [cc, *HIPCC_FLAGS, *inc, *defines, *defs, "-c", "-o", obj, src],
                               f"{os.path.basename(src)} {' '.join(defs)}", verbose)
                     for src, obj, defs in units]
             for f in futs:
                 f.result()
-        tmp = OUT + ".tmp"
+        tmp = out + ".tmp"
         _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *[o for _, o, _ in units]],
              "link", verbose)
-        os.replace(tmp, OUT)
-    return OUT
+        os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

@@ -6,6 +6,8 @@
 // -ffp-contract=off (explicit _rn operations), so RoPE and the bias adds give
 // the NumPy bits; the reductions (RMSNorm's mean, the softmax sums, the
 // attention dot products) are tree reductions, not NumPy's pairwise order.
+#include <mutex>
+
 #include "q4_common.h"
 #include "q4decode.h"
 
@@ -508,42 +510,24 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 }
 
 // ---------------------------------------------------------------- argmax ---
-// hetero/backends.py:106-109: np.argmax, the first index of the maximum.
+// hetero/backends.py:106-109: int(z.argmax()) -- NumPy's argmax, which
+// takes NaN as the largest value, so the result is the first NaN when there
+// is one, else the first index of the maximum.  Two launches: workgroup b
+// reduces slice b of the logits to (value, index) in the library's argmax
+// scratch, then one workgroup reduces the slices in order and does the
+// step's bookkeeping.
+constexpr int kArgmaxParts = 256;
+
+// (v, i) replaces (bv, bi) when it comes first in NumPy's order
 __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+    const bool vn = v != v, bn = bv != bv;
+    const bool take = vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)));
+    if (take) { bv = v; bi = i; }
 }
 
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                      int64_t* __restrict__ tok, int64_t* __restrict__ hist,
-                                                      int64_t* __restrict__ pos, int64_t s0, int hist_len) {
-    __shared__ float rv[16];
-    __shared__ int ri[16];
+// wave and workgroup reduction of (value, index); the result in thread 0
+__device__ __forceinline__ void argmax_reduce(float& bv, int& bi, float* rv, int* ri) {
     const int tid = threadIdx.x, nt = blockDim.x;
-    float bv = -__builtin_inff();
-    int bi = 0x7FFFFFFF;
-    // eight float4 loads in flight per thread, through a resource over the
-    // whole float4s (past the end: 0, never compared)
-    const int n4 = n >> 2;
-    const __amdgpu_buffer_rsrc_t lr = buf_rsrc(logits, static_cast<uint32_t>(n4) * 16u);
-    constexpr int kU = 8;
-    for (int base = 0; base < n4; base += kU * nt) {
-        float4 f[kU];
-#pragma unroll
-        for (int u = 0; u < kU; u++)
-            f[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  lr, static_cast<uint32_t>(base + u * nt + tid) * 16u, 0, 0));
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            const int i = base + u * nt + tid;
-            if (i < n4) {
-                better(bv, bi, f[u].x, 4 * i);
-                better(bv, bi, f[u].y, 4 * i + 1);
-                better(bv, bi, f[u].z, 4 * i + 2);
-                better(bv, bi, f[u].w, 4 * i + 3);
-            }
-        }
-    }
-    for (int i = 4 * n4 + tid; i < n; i += nt) better(bv, bi, logits[i], i);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(bv, o);
@@ -555,8 +539,62 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
         ri[tid >> 6] = bi;
     }
     __syncthreads();
-    if (tid == 0) {
+    if (tid == 0)
         for (int w = 1; w < (nt >> 6); w++) better(bv, bi, rv[w], ri[w]);
+}
+
+// workgroup b: float4s [b*per4, (b+1)*per4) of the logits (and the tail
+// values past the last float4 in the last workgroup)
+__global__ __launch_bounds__(256) void argmax_part_kernel(const float* __restrict__ logits, int n, int per4,
+                                                          float2* __restrict__ part) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const int tid = threadIdx.x, b = blockIdx.x;
+    float bv = -__builtin_inff();
+    int bi = 0x7FFFFFFF;
+    const int n4 = n >> 2;
+    const int lo = b * per4, hi = lo + per4 < n4 ? lo + per4 : n4;
+    const __amdgpu_buffer_rsrc_t lr = buf_rsrc(logits, static_cast<uint32_t>(n4) * 16u);
+    constexpr int kU = 4;
+    for (int base = lo; base < hi; base += kU * 256) {
+        float4 f[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int i = base + u * 256 + tid;
+            f[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  lr, i < hi ? static_cast<uint32_t>(i) * 16u : kOutOfRange, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int i = base + u * 256 + tid;
+            if (i < hi) {
+                better(bv, bi, f[u].x, 4 * i);
+                better(bv, bi, f[u].y, 4 * i + 1);
+                better(bv, bi, f[u].z, 4 * i + 2);
+                better(bv, bi, f[u].w, 4 * i + 3);
+            }
+        }
+    }
+    if (b == gridDim.x - 1)
+        for (int i = 4 * n4 + tid; i < n; i += 256) better(bv, bi, logits[i], i);
+    argmax_reduce(bv, bi, rv, ri);
+    if (tid == 0) part[b] = make_float2(bv, __int_as_float(bi));
+}
+
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float2* __restrict__ part, int parts,
+                                                           int64_t* __restrict__ tok, int64_t* __restrict__ hist,
+                                                           int64_t* __restrict__ pos, int64_t s0, int hist_len) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const int tid = threadIdx.x;
+    float bv = -__builtin_inff();
+    int bi = 0x7FFFFFFF;
+    for (int k = tid; k < parts; k += 256) {
+        const float2 c = part[k];
+        better(bv, bi, c.x, __float_as_int(c.y));
+    }
+    argmax_reduce(bv, bi, rv, ri);
+    if (tid == 0) {
         const int best = bi == 0x7FFFFFFF ? 0 : bi;
         *tok = best;
         const int64_t p = *pos;
@@ -565,6 +603,9 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ 
         *pos = p + 1;
     }
 }
+
+// The argmax partials: a fixed array in device memory, one per GPU.
+static __device__ __align__(256) float2 argmax_scratch[kArgmaxParts];
 
 int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
@@ -668,8 +709,31 @@ int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64
                   void* stream) {
     if (!logits || !tok || !pos || (hist_len > 0 && !hist)) return fail(Q4_EARG, "q4_argmax_dev: null pointer");
     if (n <= 0 || (reinterpret_cast<uintptr_t>(logits) & 15)) return fail(Q4_EARG, "q4_argmax_dev: bad n %d or logits not 16-byte aligned", n);
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), logits, n, tok, hist,
-                       pos, s0, hist_len);
+    static std::mutex mu;
+    static void* scr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(Q4_EHIP, "q4_argmax_dev: no device");
+    void* sp;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!scr[dev]) {
+            void* a = nullptr;
+            const hipError_t e = hipGetSymbolAddress(&a, HIP_SYMBOL(argmax_scratch));
+            if (e != hipSuccess || !a) return fail(Q4_EHIP, "hipGetSymbolAddress(argmax_scratch): %s", hipGetErrorString(e));
+            scr[dev] = a;
+        }
+        sp = scr[dev];
+    }
+    const int n4 = n >> 2;
+    // at least 1024 float4s per workgroup, at most kArgmaxParts workgroups
+    int parts = (n4 + 1023) / 1024;
+    parts = parts < 1 ? 1 : (parts > kArgmaxParts ? kArgmaxParts : parts);
+    const int per4 = (n4 + parts - 1) / parts;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(argmax_part_kernel, dim3(parts), dim3(256), 0, st, logits, n, per4, static_cast<float2*>(sp));
+    if (int rc = check_launch("q4_argmax_dev")) return rc;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, st, static_cast<const float2*>(sp), parts, tok,
+                       hist, pos, s0, hist_len);
     return check_launch("q4_argmax_dev");
 }
 

@@ -1,8 +1,8 @@
 """Device-resident Qwen2 decode step on one MI355X.
 
-The same stage as hetero/cpu_model.py (the reference's
-hetero/cpu_model.py:164-368), with every tensor resident in HBM and every
-operation a kernel of libq4gemv.so:
+The reference's Qwen2 stage (hetero/cpu_model.py:164-368; the host
+counterpart here is hetero/numpy_stage.py) with every tensor resident in HBM
+and every operation a kernel of libq4gemv.so:
   * 4-bit projections through the streaming GEMV: q/k/v in one grouped
     launch, o_proj, the fused gate/up/SiLU*mul launch, down and lm_head --
     every GEMV result is the reference q4_gemv's bit for bit given the same
@@ -31,10 +31,12 @@ from . import q4
 class GpuStage:
     def __init__(self, cfg: dict, w: Dict[str, np.ndarray], kv_k: List[np.ndarray],
                  kv_v: List[np.ndarray], max_new: int, device="cuda", lib=None):
-        """w: reference-named weights, NumPy arrays (cpu_model.synthetic_weights)
-        or device tensors (shard.WeightIndex.load_shard(..., framework="hip"));
+        """w: reference-named weights, NumPy arrays (qwen2.synthetic_weights)
+        or device tensors (qwen2.synthetic_weights_torch,
+        shard.WeightIndex.load_shard(..., framework="hip"));
         kv_k / kv_v: per layer [KH, S0, D] context already in the cache
-        (fp16 as stored); max_new: decode steps the cache must hold."""
+        (NumPy arrays or tensors; stored as fp16); max_new: decode steps the
+        cache must hold."""
         import torch
         self.torch = torch
         self.lib = lib or q4.load()
@@ -74,6 +76,12 @@ class GpuStage:
                 return a.to(dev, torch.float32)
             return t(np.asarray(a).astype(np.float32))
 
+        def f16(a):
+            """a KV context block [KH, S0, D] as fp16 values on the device"""
+            if isinstance(a, torch.Tensor):
+                return a.to(dev, torch.float16)
+            return t(np.asarray(a).astype(np.float16)).view(torch.float16)
+
         def mat(name):
             return (t(w[f"{name}.weight"]), f16_bits(w[f"{name}.scales"]), f16_bits(w[f"{name}.biases"]))
 
@@ -93,8 +101,8 @@ class GpuStage:
             }
             kc = torch.zeros((self.nkv, self.cap, self.hd), dtype=torch.float16, device=dev)
             vc = torch.zeros_like(kc)
-            kc[:, :self.s0] = t(kv_k[i].astype(np.float16)).view(torch.float16)
-            vc[:, :self.s0] = t(kv_v[i].astype(np.float16)).view(torch.float16)
+            kc[:, :self.s0] = f16(kv_k[i])
+            vc[:, :self.s0] = f16(kv_v[i])
             L["k_cache"], L["v_cache"] = kc, vc
             self.layers.append(L)
         self.norm_w = f32(w["model.norm.weight"])

@@ -112,3 +112,86 @@ QWEN7B_SHAPES = [
 def gemv_bytes(m: int, n_out: int, n_in: int, gs: int = 64) -> int:
     """Algorithmic bytes of one call: packed W + fp16 scales and biases + fp32 x and y."""
     return n_out * n_in // 2 + 4 * n_out * (n_in // gs) + 4 * m * n_in + 4 * m * n_out
+
+
+# ---- draws that NumPy and torch (CPU or GPU) reproduce bit for bit ---------
+#
+# A 28-layer model is 4 GB of weights: generating it with the NumPy stream
+# above takes about a minute, while torch on the GPU takes well under a
+# second.  The two agree bit for bit only where every floating-point step is
+# one IEEE operation, so these draws avoid transcendentals: a normal-like
+# value is the Irwin-Hall sum S of the four 16-bit fields of one splitmix64
+# output, centred and scaled to unit variance,
+#   z = float32(S - 131070) * float32(sigma * sqrt(3) / 65536)
+# (one float32 multiply; S - 131070 is exact in float32), bounded by
+# +-3.46 sigma.  Conversions to fp16 round to nearest even on both sides.
+# The packed weights are the integer stream of qweights() unchanged.
+
+_IH_CENTER = 2 * 65535
+_U64_MASK = (1 << 64) - 1
+
+
+def ih_scale(sigma: float) -> np.float32:
+    return np.float32(sigma * np.sqrt(3.0) / 65536.0)
+
+
+def ih_sum_np(seed: int, tag: str, n: int) -> np.ndarray:
+    """S - 131070 for n draws (int64)."""
+    z = u64(seed, tag, n)
+    m = np.uint64(0xFFFF)
+    s = (z & m) + ((z >> np.uint64(16)) & m) + ((z >> np.uint64(32)) & m) + (z >> np.uint64(48))
+    return s.astype(np.int64) - _IH_CENTER
+
+
+def ih_normal_np(seed: int, tag: str, n: int, sigma: float = 1.0) -> np.ndarray:
+    return ih_sum_np(seed, tag, n).astype(np.float32) * ih_scale(sigma)
+
+
+def qlinear_ih_np(seed: int, n_out: int, n_in: int, gs: int = 64, tag: str = "", center: float = 8.0):
+    """(w, scales, biases) with the distributions of qlinear(): packed U{0..15}
+    weights, fp16 scales |z * 0.02|, fp16 biases -center * scale + z' * 0.002
+    (center 8 by default; -center * scale is exact in fp32 for center 8 or
+    7.5)."""
+    w = qweights(seed, n_out, n_in, tag + "w")
+    g = n_out * (n_in // gs)
+    s = np.abs(ih_normal_np(seed, tag + "sb.s", g, 0.02)).astype(np.float16)
+    b = (np.float32(-center) * s.astype(np.float32) + ih_normal_np(seed, tag + "sb.b", g, 0.002)).astype(np.float16)
+    return w, s.reshape(n_out, -1), b.reshape(n_out, -1)
+
+
+def _signed(c: int) -> int:
+    return c - (1 << 64) if c >= 1 << 63 else c
+
+
+def _lsr(t, s: int):
+    """Logical right shift of int64 tensor bits."""
+    return (t >> s) & ((1 << (64 - s)) - 1)
+
+
+def u64_torch(seed: int, tag: str, n: int, device):
+    """u64() as int64 bit patterns in a torch tensor (wrapping arithmetic)."""
+    import torch
+    key = _signed(int(stream_key(seed, tag)))
+    z = torch.arange(1, n + 1, dtype=torch.int64, device=device) * _signed(int(_GOLDEN)) + key
+    z = (z ^ _lsr(z, 30)) * _signed(int(_M1))
+    z = (z ^ _lsr(z, 27)) * _signed(int(_M2))
+    return z ^ _lsr(z, 31)
+
+
+def ih_normal_torch(seed: int, tag: str, n: int, sigma: float, device):
+    import torch
+    z = u64_torch(seed, tag, n, device)
+    s = (z & 0xFFFF) + (_lsr(z, 16) & 0xFFFF) + (_lsr(z, 32) & 0xFFFF) + _lsr(z, 48)
+    return (s - _IH_CENTER).to(torch.float32) * float(ih_scale(sigma))
+
+
+def qlinear_ih_torch(seed: int, n_out: int, n_in: int, gs: int, device, tag: str = "", center: float = 8.0):
+    """qlinear_ih_np on a torch device: int32 weights, int16 (fp16 bit
+    pattern) scales and biases."""
+    import torch
+    words = n_out * (n_in // 8)
+    w = u64_torch(seed, tag + "w", (words + 1) // 2, device).view(torch.int32)[:words].reshape(n_out, n_in // 8)
+    g = n_out * (n_in // gs)
+    s = ih_normal_torch(seed, tag + "sb.s", g, 0.02, device).abs().to(torch.float16)
+    b = (s.to(torch.float32) * -float(center) + ih_normal_torch(seed, tag + "sb.b", g, 0.002, device)).to(torch.float16)
+    return w.contiguous(), s.view(torch.int16).reshape(n_out, -1), b.view(torch.int16).reshape(n_out, -1)

@@ -100,9 +100,13 @@ int q4_attention_rope_dev(const float* q, const float* k, const float* v, const 
                           const float* sin_t, const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache, float* out,
                           float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream);
 
-/* Greedy token (hetero/backends.py:106-109, NumpyBackend.sample: argmax,
- * the first index of the maximum) and the step's bookkeeping: *tok = argmax,
- * hist[*pos - s0] = *tok when that index is in [0, hist_len), *pos += 1. */
+/* Greedy token (hetero/backends.py:106-109, NumpyBackend.sample: NumPy's
+ * argmax, which takes NaN as the largest value -- the first NaN if there is
+ * one, else the first index of the maximum) and the step's bookkeeping:
+ * *tok = argmax, hist[*pos - s0] = *tok when that index is in [0, hist_len),
+ * *pos += 1.  Two launches; the per-slice maxima go through a fixed array
+ * of the library in device memory (one per GPU), so argmax calls that
+ * overlap in time on one GPU race. */
 int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0,
                   int hist_len, void* stream);
 

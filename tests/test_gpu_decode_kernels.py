@@ -223,3 +223,31 @@ def test_argmax_first_index_and_bookkeeping(torch, lib):
     t = torch.from_numpy(lg).to(dev)
     rc = lib.q4_argmax_dev(t.data_ptr(), 1001, tok.data_ptr(), hist.data_ptr(), pos.data_ptr(), 0, 0, sp(torch))
     assert rc == 0 and int(tok.item()) == int(np.argmax(lg))
+
+
+def test_argmax_nan_and_special_values_match_numpy(torch, lib):
+    """NumPy's argmax takes NaN as the largest value (the first NaN wins),
+    -inf and +inf order as numbers, and a tie keeps the first index; the
+    GPU argmax must return np.argmax for each planted case, across the
+    slices its first launch splits the vector into (n = 152064: 38 slices)
+    and for the short tail past the last float4."""
+    rng = np.random.default_rng(8)
+    dev = torch.device("cuda")
+    tok = torch.zeros(1, dtype=torch.int64, device=dev)
+    hist = torch.full((4,), -1, dtype=torch.int64, device=dev)
+    pos = torch.tensor([0], dtype=torch.int64, device=dev)
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    for n in (152064, 4099, 7, 1):
+        base = rng.normal(0, 1, n).astype(np.float32)
+        cases = [{}, {n - 1: nan}, {n // 2: nan, n - 1: nan}, {n // 3: inf, n // 2: nan}, {n // 4: inf, n - 1: inf},
+                 {0: nan}, {n // 5: 9.0, n - 1: 9.0}]
+        for planted in cases:
+            lg = base.copy()
+            for k, v in planted.items():
+                lg[k] = v
+            if not planted and n > 2:
+                lg[:] = -inf                                   # all -inf: index 0
+            t = torch.from_numpy(lg).to(dev)
+            rc = lib.q4_argmax_dev(t.data_ptr(), n, tok.data_ptr(), hist.data_ptr(), pos.data_ptr(), 0, 4, sp(torch))
+            assert rc == 0, q4.last_error(lib)
+            assert int(tok.item()) == int(np.argmax(lg)), (n, planted)

@@ -9,7 +9,7 @@ import os
 import numpy as np
 import pytest
 
-from hetero import cpu_model
+from hetero import qwen2
 from hetero.shard import Residency, ShardSpec, WeightIndex
 from test_shard import tiny_cfg, write_checkpoint, write_raw
 
@@ -24,7 +24,7 @@ def device_bytes(t):
 def ckpt(tmp_path_factory):
     d = str(tmp_path_factory.mktemp("ckpt_gpu"))
     cfg = tiny_cfg(layers=3)
-    w = cpu_model.synthetic_weights(cfg, seed=5)
+    w = qwen2.synthetic_weights(cfg, seed=5)
     write_checkpoint(d, cfg, w, split_at=2)
     return d, cfg, w
 
@@ -84,13 +84,11 @@ def test_stage_from_loaded_checkpoint_matches_numpy(tmp_path):
     from hetero.gpu_model import GpuStage
     from test_gpu_decode import small_cfg
     cfg = small_cfg()
-    w = cpu_model.synthetic_weights(cfg, seed=21)
-    caches = cpu_model.synthetic_kv(cfg, context=64, seed=22)
+    w = qwen2.synthetic_weights(cfg, seed=21)
+    kk, vv = qwen2.synthetic_context(cfg, 64, seed=22)
     write_checkpoint(str(tmp_path), cfg, w)
     dev_w = WeightIndex(str(tmp_path)).load_shard(ShardSpec(0, cfg["num_hidden_layers"], True, True),
                                                  framework="hip")
-    kk = [c.keys[0, :, :c.offset] for c in caches]
-    vv = [c.values[0, :, :c.offset] for c in caches]
     stages = [GpuStage(cfg, ww, kk, vv, max_new=6) for ww in (w, dev_w)]
     tokens = []
     for g in stages:

@@ -11,12 +11,12 @@ import struct
 import numpy as np
 import pytest
 
-from hetero import cpu_model
+from hetero import qwen2
 from hetero.shard import ShardSpec, WeightIndex, read_header
 
 
 def tiny_cfg(tied=False, layers=3):
-    cfg = cpu_model.qwen2_7b_config(layers=layers)
+    cfg = qwen2.qwen2_7b_config(layers=layers)
     cfg.update(hidden_size=128, intermediate_size=256, num_attention_heads=2, num_key_value_heads=1,
                vocab_size=96, tie_word_embeddings=tied)
     return cfg
@@ -55,7 +55,7 @@ def write_raw(path, tensors, metadata=None):
 def ckpt(tmp_path_factory):
     d = str(tmp_path_factory.mktemp("ckpt"))
     cfg = tiny_cfg()
-    w = cpu_model.synthetic_weights(cfg, seed=3)
+    w = qwen2.synthetic_weights(cfg, seed=3)
     write_checkpoint(d, cfg, w)
     return d, cfg, w
 
@@ -103,7 +103,7 @@ def test_ownership(ckpt):
 
 def test_tied_head_owns_the_embedding(tmp_path):
     cfg = tiny_cfg(tied=True, layers=2)
-    w = cpu_model.synthetic_weights(cfg, seed=4)
+    w = qwen2.synthetic_weights(cfg, seed=4)
     for k in [k for k in w if k.startswith("lm_head")]:
         del w[k]
     write_checkpoint(str(tmp_path), cfg, w)
