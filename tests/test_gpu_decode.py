@@ -20,12 +20,13 @@
        path's own step-0 logits move by 1.5e-3 when one layer's norm weights
        move by one ulp, and by 1.3e-3 / 1.0e-3 when RMSNorm / attention are
        evaluated in float64; with only its RMSNorm in float64, the reference
-       path run teacher-forced through the 128 steps drifts to 4.7e-3 on the
-       top-64 logits (tests/golden/decode_sensitivity.py, recorded in
-       decode_qwen7b.json), because each side's KV cache keeps its own
-       roundings.  The device-resident step rounds RMSNorm, softmax, exp and
-       the attention sums differently; FULL_TOL = 1e-2 is about twice that
-       one-rounding drift, while planted mistakes (tests/test_oracle_decode.py)
+       path run teacher-forced through the 128 steps drifts to 4.7e-3 and
+       5.8e-3 on the top-64 logits of the two sequences, and to 4.4e-3 and
+       5.2e-3 on the whole last-step vectors (tests/golden/
+       decode_sensitivity.py, recorded in decode_qwen7b.json), because each
+       side's KV cache keeps its own roundings.  The device-resident step
+       rounds RMSNorm, softmax, exp and the attention sums differently;
+       FULL_TOL = 1e-2 is under twice that one-rounding drift, while planted mistakes (tests/test_oracle_decode.py)
        move the logits by far more.  Checked: every step's top-64 logits and logit
        norm, the whole logit vector of the first and last steps, and the
        greedy token of every teacher-forced step -- on the reference path's
@@ -47,7 +48,7 @@ from hetero import numpy_stage, q4, qwen2
 pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 1e-3      # 2-layer model
-FULL_TOL = 1e-2       # 28 layers, 128 steps: about 2x the reference path's drift under one rounding change
+FULL_TOL = 1e-2       # 28 layers, 128 steps: under 2x the reference path's drift under one rounding change
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 needs_ref = pytest.mark.skipif(not os.path.exists(oracle.ref_path(1)), reason="oracle/_ref not built")
 
