@@ -54,10 +54,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_weights(torch, gen, n_out, n_in, dev):
+def make_weights(torch, gen, n_out, n_in, dev, gs=GS):
     w = torch.randint(-2**31, 2**31, (n_out, n_in // 8), dtype=torch.int64, device=dev,
                       generator=gen).to(torch.int32)
-    g = n_in // GS
+    g = n_in // gs
     s = (torch.randn((n_out, g), device=dev, generator=gen) * 0.02).abs().half()
     b = (-8.0 * s.float() + torch.randn((n_out, g), device=dev, generator=gen) * 0.002).half()
     return w, s.view(torch.int16), b.view(torch.int16)
@@ -79,8 +79,83 @@ def measured_traffic():
     return None
 
 
-def gemv_bytes(m, n_out, n_in):
-    return n_out * n_in // 2 + 4 * n_out * (n_in // GS) + 4 * m * n_in + 4 * m * n_out
+def gemv_bytes(m, n_out, n_in, gs=GS):
+    return n_out * n_in // 2 + 4 * n_out * (n_in // gs) + 4 * m * n_in + 4 * m * n_out
+
+
+def graph_us(torch, stream, body, calls, reps=5):
+    """Average microseconds per call of `body` (which makes `calls` launches)
+    captured in one HIP graph and replayed `reps` times on `stream`."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        body()
+    with torch.cuda.stream(stream):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * calls)
+
+
+def group128_bench(torch, lib, dev, reps=5):
+    """The M=1 projection sweep with group size 128 (MLX's other 4-bit
+    layout): the grouped decode-order sweep (qkv, o, gate+up, down per
+    layer, then lm_head) and each shape on its own, 28 distinct matrices
+    per layer shape."""
+    from hetero import q4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4321)
+    gs = 128
+    layers = [[make_weights(torch, gen, n_out, n_in, dev, gs) for _, n_in, n_out in LAYER_SHAPES]
+              for _ in range(LAYERS)]
+    head = make_weights(torch, gen, HEAD_SHAPE[2], HEAD_SHAPE[1], dev, gs)
+    xs = {k: torch.randn((1, k), device=dev, generator=gen) for k in (3584, 18944)}
+    outs = {n: [torch.empty((1, n), device=dev) for _ in range(3)] for n in (512, 3584, 18944, 152064)}
+    stream = torch.cuda.Stream(device=dev)
+    torch.cuda.synchronize()
+
+    def gemv(wsb):
+        w, s, b = wsb
+        n_out, n_in = w.shape[0], w.shape[1] * 8
+        q4.check(lib, lib.q4_gemv_dev(w.data_ptr(), s.data_ptr(), b.data_ptr(), xs[n_in].data_ptr(),
+                                      outs[n_out][0].data_ptr(), 1, n_out, n_in, gs, stream.cuda_stream),
+                 "q4_gemv_dev")
+
+    def multi(group):
+        q4.gemv_multi_dev(group, xs[group[0][0].shape[1] * 8],
+                          outs=[outs[g[0].shape[0]][i] for i, g in enumerate(group)], stream=stream, lib=lib)
+
+    def sweep():
+        for q, k, v, o, g, u, d in layers:
+            multi([q, k, v])
+            gemv(o)
+            multi([g, u])
+            gemv(d)
+        gemv(head)
+
+    n_launch = LAYERS * 4 + 1
+    with torch.cuda.stream(stream):
+        sweep()                                   # eager once: sizes the workspace
+    torch.cuda.synchronize()
+    us = graph_us(torch, stream, sweep, n_launch, reps)
+    nbytes = LAYERS * sum(gemv_bytes(1, n_out, n_in, gs) for _, n_in, n_out in LAYER_SHAPES) \
+        + gemv_bytes(1, HEAD_SHAPE[2], HEAD_SHAPE[1], gs)
+    ms = us * n_launch * 1e-3
+    res = {"gs": gs, "sweep_ms": round(ms, 4), "sweep_GB_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "bytes_per_sweep": nbytes, "launches": n_launch, "per_shape": {}}
+    for j, (name, n_in, n_out) in enumerate(LAYER_SHAPES + [HEAD_SHAPE]):
+        items = [layers[l][j] for l in range(LAYERS)] if j < len(LAYER_SHAPES) else [head] * 4
+        us = graph_us(torch, stream, lambda: [gemv(wsb) for wsb in items], len(items), reps)
+        gbs = gemv_bytes(1, n_out, n_in, gs) / (us * 1e-6) / 1e9
+        res["per_shape"][name] = {"K": n_in, "N": n_out, "us_per_call": round(us, 3), "GB_s": round(gbs, 1),
+                                  "frac_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    del layers, head
+    torch.cuda.empty_cache()
+    return res
 
 
 def prefill_bench(torch, lib, layers, dev, reps=3):
@@ -684,6 +759,8 @@ def main():
     ap.add_argument("--no-dropin", action="store_true",
                     help="skip the NumPy stage on libq4gemv.so through the host-pointer ABI")
     ap.add_argument("--dropin-only", action="store_true", help="only the host-pointer drop-in leg")
+    ap.add_argument("--no-gs128", action="store_true", help="skip the group-size-128 sweep")
+    ap.add_argument("--gs128-only", action="store_true", help="only the group-size-128 sweep")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run a 256 MiB device copy: the known-size reference for PMC byte counters")
     args = ap.parse_args()
@@ -710,6 +787,9 @@ def main():
         cfg, meta, w, ks, vs = decode_model(torch, dev)
         res = decode_bench(torch, dev, cfg, meta, w, ks, vs, steps=args.decode_steps)
         print(json.dumps({"decode": res}), flush=True)
+        return
+    if args.gs128_only:
+        print(json.dumps({"group128": group128_bench(torch, lib, dev)}), flush=True)
         return
     if args.dropin_only:
         cfg, meta, w, ks, vs = decode_model(torch, dev)
@@ -878,7 +958,7 @@ def main():
     }
     if args.sweep_only:
         args.no_prefill = args.no_cpu_baseline = args.no_decode = args.no_small_m = args.no_wire = True
-        args.no_load = args.no_dropin = True
+        args.no_load = args.no_dropin = args.no_gs128 = True
     if not args.no_small_m:
         log("small-M ...")
         result["small_m"] = small_m_bench(torch, lib, layers, dev)
@@ -920,6 +1000,9 @@ def main():
             log("cpu decode baseline ...")
             result.setdefault("decode", {})["cpu_baseline"] = cpu_decode_baseline(cfg, meta, hw, hks, hvs, rows,
                                                                                  threads)
+    if not args.no_gs128:
+        log("group size 128 ...")
+        result["group128"] = group128_bench(torch, lib, dev)
     print(json.dumps(result), flush=True)
 
 

@@ -35,8 +35,10 @@ HIPCC_FLAGS = [
     "-Wall", "-Wno-unused-command-line-argument",
 ]
 
-# (activation rows, gate/up pair, ring size) of the streaming kernel objects
-STREAM_INSTANCES = [(mr, pair, ring) for mr in (1, 2) for pair in (0, 1) for ring in (1, 2, 4)] + [(1, 0, 5)]
+# (activation rows, gate/up pair, ring size, group size 64 << gsh) of the
+# streaming kernel objects
+STREAM_INSTANCES = [(mr, pair, ring, gsh) for gsh in (0, 1) for mr in (1, 2) for pair in (0, 1)
+                    for ring in (1, 2, 4)] + [(1, 0, 5, 0), (1, 0, 5, 1)]
 
 
 def hipcc() -> str:
@@ -65,9 +67,9 @@ def build(verbose: bool = False, jobs: int | None = None, out: str = OUT, define
     with tempfile.TemporaryDirectory(prefix="q4build") as tmpd:
         units = [(SRC, os.path.join(tmpd, "q4gemv.o"), []), (DECODE, os.path.join(tmpd, "q4_decode.o"), []),
                  (WIRE, os.path.join(tmpd, "q4_wire.o"), [])]
-        for mr, pair, ring in STREAM_INSTANCES:
-            obj = os.path.join(tmpd, f"stream_m{mr}_p{pair}_r{ring}.o")
-            units.append((INST, obj, [f"-DQ4_MR={mr}", f"-DQ4_PAIR={pair}", f"-DQ4_RING={ring}"]))
+        for mr, pair, ring, gsh in STREAM_INSTANCES:
+            obj = os.path.join(tmpd, f"stream_m{mr}_p{pair}_r{ring}_g{gsh}.o")
+            units.append((INST, obj, [f"-DQ4_MR={mr}", f"-DQ4_PAIR={pair}", f"-DQ4_RING={ring}", f"-DQ4_GSH={gsh}"]))
         with ThreadPoolExecutor(max_workers=jobs) as ex:
             futs = [ex.submit(_run, [cc, *HIPCC_FLAGS, *inc, *defines, *defs, "-c", "-o", obj, src],
                               f"{os.path.basename(src)} {' '.join(defs)}", verbose)

@@ -168,7 +168,7 @@ __device__ __forceinline__ void unit_rows(UnitRows& ur, const MatList& ml, int u
 // gives an empty resource: every lane reads 0.  The chunk moves the
 // resource's base (scalar work); the lanes' offsets are the same for every
 // item.  No branch, so the waits on earlier loads stay exact.
-template <bool PAIR>
+template <bool PAIR, int GSH>
 __device__ __forceinline__ void load_item(Item& it, const UnitRows& ur, int unit, int c, int r, int UB,
                                           int wpr, int G, uint32_t vo_w, uint32_t vo_g, bool live) {
     it.unit = unit;
@@ -180,7 +180,7 @@ __device__ __forceinline__ void load_item(Item& it, const UnitRows& ur, int unit
     // byte offsets from the unit's first row, 32-bit (a unit is at most 8
     // rows of at most 16 KiB): row slot u, then chunk c
     const uint32_t cw = static_cast<uint32_t>(c) * kChunkWords * 4u;      // bytes of the row before chunk c
-    const uint32_t cg = static_cast<uint32_t>(c) * (kChunkWords / 8) * 2u;  // bytes of its scales before it
+    const uint32_t cg = static_cast<uint32_t>(c) * (kChunkWords / (8 << GSH)) * 2u;  // bytes of its scales before it
     const uint32_t ow = static_cast<uint32_t>(u * wpr) * 4u + cw;
     const uint32_t og = static_cast<uint32_t>(u * G) * 2u + cg;
     const uint32_t wbytes = live ? static_cast<uint32_t>(wpr) * 4u - cw : 0u;
@@ -248,16 +248,20 @@ __host__ __device__ constexpr int stream_waves_per_cu() { return MR >= 8 ? 8 : 1
 // kernel writes.  MR = 1 and RW = 1 only.
 // Rows of x past ml.mrows (an M below MR) read 0 and their outputs are not
 // stored.
-// Host guarantees: chunks * 256 <= RW * blockDim.x, n_in % 64 == 0, x
-// 16-byte aligned.
-template <int MR, int RW, bool PAIR, int RING, bool NORM>
+// GSH: the group size is 64 << GSH (64 or 128): a group is 8 << GSH
+// packed words, 2 << GSH lanes of an item.
+// Host guarantees: chunks * 256 <= RW * blockDim.x, n_in % (64 << GSH) == 0,
+// x 16-byte aligned.
+template <int MR, int RW, bool PAIR, int RING, bool NORM, int GSH>
 __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_kernel(MatList ml,
                                                                                      const float* __restrict__ x,
                                                                                      int n_in, int UB, NormArgs na) {
-    static_assert(!NORM || (MR == 1 && RW == 1), "the norm prologue takes one row, one word per thread");
+    static_assert(!NORM || (MR == 1 && RW == 1 && GSH == 0), "the norm prologue takes one row, one word per thread");
+    static_assert(GSH == 0 || GSH == 1, "group size 64 or 128");
     extern __shared__ uint4 lds4[];
-    constexpr int lpg = 2;                                        // lanes per group
-    const int wpr = n_in >> 3, G = n_in >> 6;
+    constexpr int lpg = 2 << GSH;                                 // lanes per group in an item
+    constexpr int WPG = 8 << GSH;                                 // packed words per group
+    const int wpr = n_in >> 3, G = n_in >> (6 + GSH);
     const int C = (wpr + kChunkWords - 1) / kChunkWords;
     const int Gr = (G + 3) & ~3, Ts = term_stride(G);
     const int tid = threadIdx.x, nt = blockDim.x;
@@ -327,13 +331,13 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     Item ring[RING];
     // the lane's byte offsets inside an item: its 16 bytes of weights, the
     // fp16 scale/bias of its group (two lanes per group)
-    const uint32_t vo_w = static_cast<uint32_t>(lane) * 16u, vo_g = static_cast<uint32_t>(lane >> 1) * 2u;
+    const uint32_t vo_w = static_cast<uint32_t>(lane) * 16u, vo_g = static_cast<uint32_t>(lane >> (1 + GSH)) * 2u;
     int pf_unit = first_unit, pf_c = 0, pf_r = 0;                 // prefetch cursor (uniform)
     UnitRows pf_rows;
     unit_rows<PAIR>(pf_rows, ml, pf_unit, UB, wpr, G);
 #pragma unroll
     for (int d = 0; d < kE; d++) {
-        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, has_work);
+        load_item<PAIR, GSH>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, has_work);
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
 
@@ -396,10 +400,10 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
             amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                                      fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
         }
-        const int sub = lane & 7;
+        const int sub = lane & (WPG - 1);
         if (wave * 64 < wpr) {                                    // uniform: the wave has words
 #pragma unroll
-            for (int step = 0; step < 8; step++) {
+            for (int step = 0; step < WPG; step++) {
 #pragma unroll
                 for (int r = 0; r < RW; r++) {
                     // lane 8k+step continues the chain of lane 8k+step-1
@@ -414,7 +418,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
 #pragma unroll
             for (int r = 0; r < RW; r++) {
                 const int j = r * nt + tid;
-                if (sub == 7 && j < wpr) xsum_lds[m * Gr + (j >> 3)] = acc[r];
+                if (sub == WPG - 1 && j < wpr) xsum_lds[m * Gr + j / WPG] = acc[r];
             }
         }
         amax = wave_max(amax);
@@ -422,7 +426,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     }
 #pragma unroll
     for (int d = kE; d < RING; d++) {
-        load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, has_work);
+        load_item<PAIR, GSH>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, has_work);
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
     if (tid == 0) *claim_ctr = 0;
@@ -477,7 +481,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
         // lead (last) lane of a group writes its term if the group is in the row
         const int lim = wpr - c * kChunkWords;                    // uniform
         const bool lead = lane * 4 < lim && (lane & (lpg - 1)) == lpg - 1;
-        const int g = c * (kChunkWords / 8) + (lane >> 1);
+        const int g = c * (kChunkWords / WPG) + (lane >> (1 + GSH));
         uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
 #pragma unroll
         for (int m = 0; m < MR; m++)
@@ -575,7 +579,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
                 // the refill may not be scheduled above the consume of its
                 // slot, so that the slot keeps its registers
                 __builtin_amdgcn_sched_barrier(0);
-                load_item<PAIR>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, true);
+                load_item<PAIR, GSH>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, true);
                 if (++pf_r == NU) { pf_r = 0; ++pf_c; }
             }
             ++cyc_pf;
@@ -600,18 +604,18 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
 
 // Workgroups of the kernel resident per CU (the ring-4 instance: the most
 // registers of the rings in use).
-template <int MR, int RW, bool PAIR, bool NORM>
+template <int MR, int RW, bool PAIR, bool NORM, int GSH>
 int stream_blocks_per_cu(int nwaves, size_t lds) {
     int per_cu = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, gemv_stream_kernel<MR, RW, PAIR, 4, NORM>, 64 * nwaves, lds);
+        &per_cu, gemv_stream_kernel<MR, RW, PAIR, 4, NORM, GSH>, 64 * nwaves, lds);
     return (e != hipSuccess || per_cu < 1) ? 1 : per_cu;
 }
 
-template <int MR, int RW, bool PAIR, int RING, bool NORM>
+template <int MR, int RW, bool PAIR, int RING, bool NORM, int GSH>
 int launch_stream_k(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
                     size_t lds, int grid, hipStream_t st) {
-    auto kern = gemv_stream_kernel<MR, RW, PAIR, RING, NORM>;
+    auto kern = gemv_stream_kernel<MR, RW, PAIR, RING, NORM, GSH>;
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), kStreamLdsMax, lds_raised)) return rc;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB, na);

@@ -72,23 +72,27 @@ int num_cus() {
 // The streaming kernel's instances are compiled in q4_stream_inst.hip
 // (a build with -DQ4_SINGLE_TU instantiates them here instead).
 #ifndef Q4_SINGLE_TU
-#define Q4_STREAM_EXTERN(MR, RW, PAIR, RING, NORM)                                              \
-    extern template int launch_stream_k<MR, RW, PAIR, RING, NORM>(const MatList&, const float*,   \
-                                                                  const NormArgs&, int, int, int, \
-                                                                  size_t, int, hipStream_t);
-#define Q4_STREAM_RINGS(MR, RW, PAIR, NORM)                                                         \
-    Q4_STREAM_EXTERN(MR, RW, PAIR, 1, NORM) Q4_STREAM_EXTERN(MR, RW, PAIR, 2, NORM)                 \
-    Q4_STREAM_EXTERN(MR, RW, PAIR, 4, NORM)                                                         \
-    extern template int stream_blocks_per_cu<MR, RW, PAIR, NORM>(int, size_t);
-Q4_STREAM_RINGS(1, 1, false, false) Q4_STREAM_RINGS(1, 2, false, false)
-Q4_STREAM_RINGS(1, 3, false, false) Q4_STREAM_RINGS(1, 4, false, false)
-Q4_STREAM_EXTERN(1, 1, false, 5, false) Q4_STREAM_EXTERN(1, 2, false, 5, false)
-Q4_STREAM_EXTERN(1, 3, false, 5, false) Q4_STREAM_EXTERN(1, 4, false, 5, false)
-Q4_STREAM_RINGS(1, 1, true, false) Q4_STREAM_RINGS(1, 2, true, false)
-Q4_STREAM_RINGS(2, 1, false, false) Q4_STREAM_RINGS(2, 2, false, false)
-Q4_STREAM_RINGS(2, 1, true, false) Q4_STREAM_RINGS(2, 2, true, false)
-Q4_STREAM_RINGS(1, 1, false, true) Q4_STREAM_EXTERN(1, 1, false, 5, true)
-Q4_STREAM_RINGS(1, 1, true, true)
+#define Q4_STREAM_EXTERN(MR, RW, PAIR, RING, NORM, GSH)                                            \
+    extern template int launch_stream_k<MR, RW, PAIR, RING, NORM, GSH>(const MatList&, const float*,   \
+                                                                       const NormArgs&, int, int, int, \
+                                                                       size_t, int, hipStream_t);
+#define Q4_STREAM_RINGS(MR, RW, PAIR, NORM, GSH)                                                    \
+    Q4_STREAM_EXTERN(MR, RW, PAIR, 1, NORM, GSH) Q4_STREAM_EXTERN(MR, RW, PAIR, 2, NORM, GSH)       \
+    Q4_STREAM_EXTERN(MR, RW, PAIR, 4, NORM, GSH)                                                    \
+    extern template int stream_blocks_per_cu<MR, RW, PAIR, NORM, GSH>(int, size_t);
+#define Q4_STREAM_GS(GSH)                                                                           \
+    Q4_STREAM_RINGS(1, 1, false, false, GSH) Q4_STREAM_RINGS(1, 2, false, false, GSH)              \
+    Q4_STREAM_RINGS(1, 3, false, false, GSH) Q4_STREAM_RINGS(1, 4, false, false, GSH)              \
+    Q4_STREAM_EXTERN(1, 1, false, 5, false, GSH) Q4_STREAM_EXTERN(1, 2, false, 5, false, GSH)      \
+    Q4_STREAM_EXTERN(1, 3, false, 5, false, GSH) Q4_STREAM_EXTERN(1, 4, false, 5, false, GSH)      \
+    Q4_STREAM_RINGS(1, 1, true, false, GSH) Q4_STREAM_RINGS(1, 2, true, false, GSH)                \
+    Q4_STREAM_RINGS(2, 1, false, false, GSH) Q4_STREAM_RINGS(2, 2, false, false, GSH)              \
+    Q4_STREAM_RINGS(2, 1, true, false, GSH) Q4_STREAM_RINGS(2, 2, true, false, GSH)
+Q4_STREAM_GS(0)
+Q4_STREAM_GS(1)
+Q4_STREAM_RINGS(1, 1, false, true, 0) Q4_STREAM_EXTERN(1, 1, false, 5, true, 0)
+Q4_STREAM_RINGS(1, 1, true, true, 0)
+#undef Q4_STREAM_GS
 #undef Q4_STREAM_RINGS
 #undef Q4_STREAM_EXTERN
 #endif
@@ -744,30 +748,33 @@ hipError_t launch_main(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 }
 
 
-template <int MR, int RW, bool PAIR, bool NORM>
+template <int MR, int RW, bool PAIR, bool NORM, int GSH>
 int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
                      size_t lds, int n_units, int items, hipStream_t st) {
-    const int per_cu = stream_blocks_per_cu<MR, RW, PAIR, NORM>(nwaves, lds);
+    const int per_cu = stream_blocks_per_cu<MR, RW, PAIR, NORM, GSH>(nwaves, lds);
     const int want = (n_units + nwaves - 1) / nwaves;
     const int cap = num_cus() * per_cu;                 // every workgroup resident at once
     const int grid = want < cap ? want : cap;
     // ring: a divisor of the unit's items (units change only between rings)
-    if (items % 4 == 0) return launch_stream_k<MR, RW, PAIR, 4, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+    if (items % 4 == 0)
+        return launch_stream_k<MR, RW, PAIR, 4, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
     if constexpr (MR == 1 && !PAIR)
         if (items % 5 == 0)
-            return launch_stream_k<MR, RW, PAIR, 5, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
-    if (items % 2 == 0) return launch_stream_k<MR, RW, PAIR, 2, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
-    return launch_stream_k<MR, RW, PAIR, 1, NORM>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+            return launch_stream_k<MR, RW, PAIR, 5, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+    if (items % 2 == 0)
+        return launch_stream_k<MR, RW, PAIR, 2, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+    return launch_stream_k<MR, RW, PAIR, 1, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
 }
 
-// NORM: the norm prologue (one row; one word of x per thread, so at least
+// GSH: group size 64 << GSH.  NORM: the norm prologue (group size 64; one
+// row; one word of x per thread, so at least
 // n_in / 512 waves -- n_in <= 8192).  Returns 0 if the shape does not fit.
-template <int MR, bool PAIR = false, bool NORM = false>
+template <int MR, bool PAIR = false, bool NORM = false, int GSH = 0>
 int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, const NormArgs& na = NormArgs{}) {
     static_assert(!NORM || MR == 1, "the norm prologue takes one row");
     constexpr int kWavesPerCu = stream_waves_per_cu<MR>();
     constexpr int rmax = NORM ? 1 : stream_max_rounds<MR>();
-    const int G = n_in / 64;
+    const int G = n_in / (64 << GSH);
     const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
     const int n_total = PAIR ? ml.n_out[0] : ml.row_begin[ml.count];
     const int cus = num_cus();
@@ -795,36 +802,45 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, c
     if (lds > kStreamLdsMax) return 0;
     const int items = (PAIR ? 2 : 1) * UB * C;
     if constexpr (NORM)
-        return rw == 1 ? launch_stream_rw<MR, 1, PAIR, true>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st)
-                       : 0;
+        return rw == 1 && GSH == 0
+                   ? launch_stream_rw<MR, 1, PAIR, true, 0>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st)
+                   : 0;
     switch (rw) {
-        case 1: return launch_stream_rw<MR, 1, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+        case 1: return launch_stream_rw<MR, 1, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
         case 2:
             if constexpr (rmax >= 2)
-                return launch_stream_rw<MR, 2, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+                return launch_stream_rw<MR, 2, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
             return 0;
         // (3 and 4 words per thread: the single-matrix launches of one row)
         case 3:
             if constexpr (rmax >= 3 && !PAIR)
-                return launch_stream_rw<MR, 3, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+                return launch_stream_rw<MR, 3, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
             return 0;
         case 4:
             if constexpr (rmax >= 4 && !PAIR)
-                return launch_stream_rw<MR, 4, PAIR, false>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+                return launch_stream_rw<MR, 4, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
             return 0;
         default: return 0;
     }
 }
 
-// The streaming path takes gs 64, x 16-byte aligned and at most 16 chunks
-// (n_in <= 32768).  Returns 1 if it launched, 0 if the call must take
-// the split path, <0 on error.
+// The streaming path takes gs 64 or 128, x 16-byte aligned and at most 16
+// chunks (n_in <= 32768).  Returns 1 if it launched, 0 if the call must
+// take the split path, <0 on error.
+bool stream_takes(const float* x, int n_in, int gs) {
+    if ((gs != 64 && gs != 128) || n_in == 0 || (reinterpret_cast<uintptr_t>(x) & 15)) return false;
+    return (n_in / 8 + kChunkWords - 1) / kChunkWords <= 16;
+}
+
+template <int MR, bool PAIR = false>
+int launch_stream_gs(const MatList& ml, const float* x, int n_in, int gs, hipStream_t st) {
+    return gs == 128 ? launch_stream<MR, PAIR, false, 1>(ml, x, n_in, st) : launch_stream<MR, PAIR, false, 0>(ml, x, n_in, st);
+}
+
 template <int MR>
 int try_fused(const MatList& ml, const float* x, int n_in, int gs, hipStream_t st) {
-    if (gs != 64 || n_in == 0 || (reinterpret_cast<uintptr_t>(x) & 15)) return 0;
-    const int C = (n_in / 8 + kChunkWords - 1) / kChunkWords;
-    if (C > 16) return 0;
-    return launch_stream<MR>(ml, x, n_in, st);
+    if (!stream_takes(x, n_in, gs)) return 0;
+    return launch_stream_gs<MR>(ml, x, n_in, gs, st);
 }
 
 // One or two rows: the streaming kernel's instance of that row count.
@@ -1459,9 +1475,9 @@ int q4_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const ui
             done = gemv_mfma(mt, true, xm, hm, mm, n_inter, n_in, gs, st, *ws);
             if (done < 0) return done;
         }
-        if (!done && mm <= 2 && gs == 64 && n_in > 0 && !(reinterpret_cast<uintptr_t>(xm) & 15) &&
-            (n_in / 8 + kChunkWords - 1) / kChunkWords <= 16) {
-            done = mm == 1 ? launch_stream<1, true>(ml, xm, n_in, st) : launch_stream<2, true>(ml, xm, n_in, st);
+        if (!done && mm <= 2 && stream_takes(xm, n_in, gs)) {
+            done = mm == 1 ? launch_stream_gs<1, true>(ml, xm, n_in, gs, st)
+                           : launch_stream_gs<2, true>(ml, xm, n_in, gs, st);
             if (done < 0) return done;
         }
         if (!done) {        // unfused: gate into h, up into the workspace, then SiLU * mul

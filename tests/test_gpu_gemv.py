@@ -341,3 +341,58 @@ def test_workspace_grown_after_capture_keeps_graph_valid(lib):
             g.replay()
         torch.cuda.synchronize()
         assert_bit_exact(out_s.cpu().numpy(), want_s, f"graph replay {rep}")
+
+
+@pytest.mark.parametrize("k_in,n_out", [(3584, 3584), (3584, 512), (18944, 3584), (3584, 18944)])
+def test_group_size_128_qwen_shapes(lib, k_in, n_out):
+    """Group size 128 (MLX's other common 4-bit layout) at the Qwen2.5-7B
+    projection shapes: 1 and 2 rows take the streaming kernel with 128-wide
+    groups, 3 and 4 rows the general path; bit-exact vs the oracle, and the
+    oracle vs the reference kernel compiled from source where it is built."""
+    import torch
+    o = oracle.Oracle()
+    w, s, b = synth.qlinear(900 + k_in + n_out, n_out, k_in, 128)
+    x = synth.activations(901, 4, k_in)
+    want = o.gemv_rows(w, s, b, x, 128)
+    if os.path.exists(oracle.ref_path(1)):
+        # the reference kernel compiled from source, on the first row
+        ref = np.empty(n_out, np.float32)
+        assert oracle.load_ref(1).q4_gemv(w.ctypes.data, s.ctypes.data, b.ctypes.data, x[0].ctypes.data,
+                                          ref.ctypes.data, n_out, k_in, 128, 8) == 0
+        assert_bit_exact(want[0], ref, "oracle vs reference kernel")
+    tw, ts, tb, tx = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16), x))
+    for m in (1, 2, 3, 4):
+        print(f"gs128 K={k_in} N={n_out} m={m}", flush=True)
+        got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
+        torch.cuda.synchronize()
+        assert_bit_exact(got.cpu().numpy(), want[:m], f"gs128 K={k_in} N={n_out} m={m}")
+
+
+def test_group_size_128_multi_and_gate_up(lib):
+    """Group size 128 through q4_gemv_multi_dev (q/k/v) and the gate/up
+    pair: the grouped outputs bit-exact vs the oracle, h bit-identical
+    between 2-row and 1-row launches and within 2e-6 of NumPy's float32
+    SiLU of the oracle's gate and up (exp may differ in the last place)."""
+    import torch
+    o = oracle.Oracle()
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    qkv = [synth.qlinear(910 + i, n, 3584, 128) for i, n in enumerate((3584, 512, 512))]
+    x = synth.activations(913, 2, 3584)
+    dev = [(t(w), t(s.view(np.int16)), t(b.view(np.int16))) for w, s, b in qkv]
+    for m in (1, 2):
+        print(f"gs128 q/k/v m={m}", flush=True)
+        outs = q4.gemv_multi_dev(dev, t(x[:m]))
+        torch.cuda.synchronize()
+        for (w, s, b), got in zip(qkv, outs):
+            assert_bit_exact(got.cpu().numpy(), o.gemv_rows(w, s, b, x[:m], 128), f"gs128 multi m={m} n={w.shape[0]}")
+    gate, up = synth.qlinear(920, 18944, 3584, 128), synth.qlinear(921, 18944, 3584, 128)
+    gd, ud = [(t(w), t(s.view(np.int16)), t(b.view(np.int16))) for w, s, b in (gate, up)]
+    print("gs128 gate/up", flush=True)
+    h2 = q4.gate_up_silu_dev(gd, ud, t(x)).cpu().numpy()
+    h1 = [q4.gate_up_silu_dev(gd, ud, t(x[r:r + 1])).cpu().numpy()[0] for r in range(2)]
+    torch.cuda.synchronize()
+    for r in range(2):
+        assert np.array_equal(h2[r].view(np.uint32), h1[r].view(np.uint32)), f"row {r}"
+        g, u = o.gemv(*gate, x[r], 128), o.gemv(*up, x[r], 128)
+        h_ref = (g / (np.float32(1.0) + np.exp(-g, dtype=np.float32)) * u).astype(np.float32)
+        assert oracle.normwise_rel(h2[r], h_ref) < 2e-6, f"row {r}"
