@@ -60,15 +60,15 @@ struct NormArgs {
     float eps;
 };
 
-// Row stride of the per-wave term table: a multiple of 4 floats (16-byte
-// reads) that is 4 mod 8 words, so lanes reading different rows spread over
-// the banks.
-__host__ __device__ inline int term_stride(int G) { return ((G + 3) & ~3) | 4; }
+// Row stride of the per-wave term table, which holds one chunk's group
+// terms (at most 32) per row: a multiple of 4 floats (16-byte reads) that is
+// 4 mod 8 words, so lanes reading different rows spread over the banks.
+constexpr int kTermStride = 36;
 
 // rw: words of x per thread and row (the register rounds of the x prologue).
 inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU, int rw) {
     (void)rw;
-    const size_t terms = static_cast<size_t>(nwaves) * mr * NU * term_stride(G) * 4;
+    const size_t terms = static_cast<size_t>(nwaves) * mr * NU * kTermStride * 4;
     return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
          + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
          + static_cast<size_t>(mr) * 16 * 4 + 16                         // amax per wave, counter
@@ -85,7 +85,17 @@ __device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
 // x[p] for a wave-uniform p in an SGPR, as scalar compare/selects in asm: a
 // select written in C++ is folded back into an indexed kernel-argument load,
 // which puts a scalar memory round trip in front of every weight load.
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
 __device__ __forceinline__ uint64_t sel4(int p, uint64_t a0, uint64_t a1, uint64_t a2, uint64_t a3) {
+    // uniform operands, kept in SGPRs (see the 32-bit form below)
+    a0 = uniform64(a0);
+    a1 = uniform64(a1);
+    a2 = uniform64(a2);
+    a3 = uniform64(a3);
     uint64_t r;
     asm volatile(
         "s_cmp_eq_u32 %1, 1\n\t"
@@ -206,19 +216,24 @@ __device__ __forceinline__ void load_item(Item& it, const UnitRows& ur, int unit
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// Sequential fp32 sum of n terms (ascending), four 16-byte LDS reads in flight.
-__device__ __forceinline__ float chain_sum(const float* tp, int n) {
+// acc + tp[0] + tp[1] + ... + tp[N-1], added in that order (fp32), all N
+// terms read from LDS at once.  The running sum of a row's groups goes
+// through this one chunk at a time: the same additions in the same order as
+// one pass over the row's groups.
+template <int N>
+__device__ __forceinline__ float chain_add(float acc, const float* tp) {
+    static_assert(N % 4 == 0, "whole float4 reads");
     const float4* t4 = reinterpret_cast<const float4*>(tp);
-    float acc = 0.0f;
-    int g = 0;
-    for (; g + 16 <= n; g += 16) {
-        const float4 a0 = t4[g / 4], a1 = t4[g / 4 + 1], a2 = t4[g / 4 + 2], a3 = t4[g / 4 + 3];
-        const float vals[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                                a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+    float4 v[N / 4];
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc = __fadd_rn(acc, vals[i]);
+    for (int i = 0; i < N / 4; i++) v[i] = t4[i];
+#pragma unroll
+    for (int i = 0; i < N / 4; i++) {
+        acc = __fadd_rn(acc, v[i].x);
+        acc = __fadd_rn(acc, v[i].y);
+        acc = __fadd_rn(acc, v[i].z);
+        acc = __fadd_rn(acc, v[i].w);
     }
-    for (; g < n; g++) acc = __fadd_rn(acc, tp[g]);
     return acc;
 }
 
@@ -263,7 +278,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     constexpr int WPG = 8 << GSH;                                 // packed words per group
     const int wpr = n_in >> 3, G = n_in >> (6 + GSH);
     const int C = (wpr + kChunkWords - 1) / kChunkWords;
-    const int Gr = (G + 3) & ~3, Ts = term_stride(G);
+    const int Gr = (G + 3) & ~3;
     const int tid = threadIdx.x, nt = blockDim.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);    // wave-uniform
@@ -273,7 +288,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     float* red = xsum_lds + MR * Gr;                              // [MR][16]
     const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
     int* claim_ctr = reinterpret_cast<int*>(red + MR * 16);       // units handed out past the first
-    float* Tw = red + MR * 16 + 4 + wave * (MR * NU * Ts);        // this wave: [MR][NU][Ts]
+    float* Tw = red + MR * 16 + 4 + wave * (MR * NU * kTermStride);   // this wave: [MR][NU][kTermStride]
 
     // ---- x loads: thread t owns words t, t + nt, ... of every row, 8 values
     //      each, through a resource over x (words at or past the row end read
@@ -475,13 +490,17 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     //      unconditional (exact waits).  After the wave's last unit the ring
     //      drains without loads.
     // one item: the integer dots of chunk c against row slot u, one fp32
-    // term per group written by the group's last lane
+    // term per group written by the group's last lane into the chunk's row of
+    // the term table -- +0.0 for a group past the row end: added to a running
+    // sum that starts at +0.0 (and so is never -0.0) it changes nothing
+    constexpr int GPC = kChunkWords / WPG;                        // groups per chunk
     auto consume = [&](const Item& itm, int c, int u) {
-        // group g = c * 32 + lane / 2: a uniform part and a lane part; the
-        // lead (last) lane of a group writes its term if the group is in the row
+        // group g = c * GPC + lane / lpg: a uniform part and a lane part
         const int lim = wpr - c * kChunkWords;                    // uniform
-        const bool lead = lane * 4 < lim && (lane & (lpg - 1)) == lpg - 1;
-        const int g = c * (kChunkWords / WPG) + (lane >> (1 + GSH));
+        const bool lead = (lane & (lpg - 1)) == lpg - 1;
+        const bool in_row = lane * 4 < lim;
+        const int gl = lane >> (1 + GSH);
+        const int g = c * GPC + gl;
         uint32_t xle[MR][4], xlo[MR][4], xhe[MR][4], xho[MR][4];
 #pragma unroll
         for (int m = 0; m < MR; m++)
@@ -511,24 +530,43 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
             }
             const int part = group_sum(static_cast<int>(static_cast<uint32_t>(ah) * 256u + al), lpg);
             if (lead) {
-                const float dot = __fmul_rn(xsc[m], static_cast<float>(part));
-                const float bx = __fmul_rn(bf, xsum_lds[m * Gr + g]);
-                Tw[(m * NU + u) * Ts + g] = __builtin_fmaf(sf, dot, bx);
+                float term = 0.0f;
+                if (in_row) {
+                    const float dot = __fmul_rn(xsc[m], static_cast<float>(part));
+                    const float bx = __fmul_rn(bf, xsum_lds[m * Gr + g]);
+                    term = __builtin_fmaf(sf, dot, bx);
+                }
+                Tw[(m * NU + u) * kTermStride + gl] = term;
             }
         }
     };
-    // a finished unit: one lane per (m, row) adds the row's terms in
-    // ascending group order
-    auto finish = [&](int unit) {
+    // lane L < MR * NU keeps the running sum of row slot L % NU of x row
+    // L / NU over the chunks done so far (kernel/q4gemv.c:286-293: the
+    // groups in ascending order); a chunk's terms are added as soon as its
+    // last row slot is consumed, so the end of a unit adds one chunk only
+    float row_acc = 0.0f;
+    auto chunk_done = [&]() {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (lane < MR * NU) row_acc = chain_add<GPC>(row_acc, Tw + lane * kTermStride);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    };
+    // a finished unit: its rows' sums are complete; one lane per (m, row)
+    // stores the row's output
+    auto finish = [&](int unit) {
+        // (m, uu) = (lane / UB, lane % UB); its sum sits in lane m * NU + uu
+        // (PAIR: the up row's in lane m * NU + UB + uu)
+        const int src = (lane / UB) * NU + (lane % UB);
+        const float acc = PAIR ? __shfl(row_acc, src & 63) : row_acc;
+        const float up = PAIR ? __shfl(row_acc, (src + UB) & 63) : 0.0f;
+        row_acc = 0.0f;
         if (lane < MR * UB) {
             const int m = lane / UB, uu = lane - m * UB, gr = unit * UB + uu;
             if (gr < n_total && m < ml.mrows) {
-                const float acc = chain_sum(Tw + (m * NU + uu) * Ts, G);
                 if constexpr (PAIR) {
-                    const float up = chain_sum(Tw + (m * NU + UB + uu) * Ts, G);
                     ml.out[0][static_cast<size_t>(m) * ml.n_out[0] + gr] = silu_mul(acc, up);
                 } else {
                     // the host picks UB dividing every n_out, so a unit
@@ -547,9 +585,6 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
                 }
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
     if (has_work) {                                               // uniform
         const int cyc_per_unit = items / RING;
@@ -575,12 +610,12 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
 #pragma unroll
             for (int d = 0; d < RING; d++) {
                 consume(ring[d], cu_c, cu_r);
-                if (++cu_r == NU) { cu_r = 0; ++cu_c; }
                 // the refill may not be scheduled above the consume of its
                 // slot, so that the slot keeps its registers
                 __builtin_amdgcn_sched_barrier(0);
                 load_item<PAIR, GSH>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, true);
                 if (++pf_r == NU) { pf_r = 0; ++pf_c; }
+                if (++cu_r == NU) { chunk_done(); cu_r = 0; ++cu_c; }
             }
             ++cyc_pf;
             if (++cyc_cu == cyc_per_unit) {                       // uniform: unit done
@@ -596,7 +631,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
 #pragma unroll
         for (int d = 0; d < RING; d++) {
             consume(ring[d], cu_c, cu_r);
-            if (++cu_r == NU) { cu_r = 0; ++cu_c; }
+            if (++cu_r == NU) { chunk_done(); cu_r = 0; ++cu_c; }
         }
         finish(cu_unit);
     }

@@ -27,7 +27,9 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev",
            "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev",
            # activation wire codec (include/q4wire.h)
-           "q4_wire_payload_bytes", "q4_wire_encode_dev", "q4_wire_decode_dev")
+           "q4_wire_payload_bytes", "q4_wire_encode_dev", "q4_wire_decode_dev",
+           # chained GEMV programs (include/q4chain.h)
+           "q4_chain_create", "q4_chain_run", "q4_chain_errors", "q4_chain_destroy")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
@@ -91,7 +93,22 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_wire_encode_dev.restype = _I
         lib.q4_wire_decode_dev.argtypes = [_VP, _I, _I, _I, _VP, _VP]
         lib.q4_wire_decode_dev.restype = _I
+    if hasattr(lib, "q4_chain_create"):
+        lib.q4_chain_create.argtypes = [ctypes.POINTER(ChainPhase), _I, ctypes.POINTER(_VP)]
+        lib.q4_chain_create.restype = _I
+        lib.q4_chain_run.argtypes = [_VP, _VP]
+        lib.q4_chain_run.restype = _I
+        lib.q4_chain_errors.argtypes = [_VP]
+        lib.q4_chain_errors.restype = _I
+        lib.q4_chain_destroy.argtypes = [_VP]
+        lib.q4_chain_destroy.restype = _I
     return lib
+
+
+class ChainPhase(ctypes.Structure):
+    """q4_chain_phase of include/q4chain.h."""
+    _fields_ = [("count", _I), ("pair", _I), ("w", _VP * 4), ("scales", _VP * 4), ("biases", _VP * 4),
+                ("out", _VP * 4), ("n_out", _I * 4), ("x", _VP), ("n_in", _I), ("gs", _I)]
 
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -277,6 +294,54 @@ def dequant_dev(w, scales, biases, row0=0, row1=None, out=None, bf16=False, stre
     rc = fn(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out), row0, row1, n_in, gs, _stream(stream))
     check(lib, rc, "q4_dequant_dev")
     return out
+
+
+class Chain:
+    """A chained GEMV program (include/q4chain.h): `phases` is a list of
+    (mats, x, outs, pair) with mats a list of (w, scales, biases) device
+    tensors sharing the one-row input x, outs their output tensors (pair:
+    gate/up, one output h = SiLU(gate x) * (up x)).  The phases run in order
+    in one launch; a phase may read the outputs of the phases before it."""
+
+    def __init__(self, phases, lib=None):
+        self.lib = lib or load()
+        self._keep = []
+        table = (ChainPhase * len(phases))()
+        for i, (mats, x, outs, pair) in enumerate(phases):
+            ph = table[i]
+            n_in = mats[0][0].shape[1] * 8
+            ph.count, ph.pair = len(mats), int(bool(pair))
+            ph.n_in, ph.gs = n_in, n_in // mats[0][1].shape[1]
+            ph.x = _ptr(x)
+            for k, (w, sc, b) in enumerate(mats):
+                ph.w[k], ph.scales[k], ph.biases[k] = _ptr(w), _ptr(sc), _ptr(b)
+                ph.n_out[k] = w.shape[0]
+                ph.out[k] = _ptr(outs[0] if pair else outs[k])
+            self._keep.append((mats, x, outs))
+        self._plan = _VP()
+        check(self.lib, self.lib.q4_chain_create(table, len(phases), ctypes.byref(self._plan)), "q4_chain_create")
+
+    def run(self, stream=None):
+        check(self.lib, self.lib.q4_chain_run(self._plan, _stream(stream)), "q4_chain_run")
+
+    def errors(self) -> int:
+        """Barrier waits that ran out of time since the last call (synchronises)."""
+        n = self.lib.q4_chain_errors(self._plan)
+        if n < 0:
+            check(self.lib, n, "q4_chain_errors")
+        return n
+
+    def close(self):
+        if self._plan:
+            self.lib.q4_chain_destroy(self._plan)
+            self._plan = _VP()
+        self._keep = []
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # ---- host-pointer calls (the reference's ABI) over NumPy arrays ----

@@ -1,0 +1,71 @@
+/* Chained GEMV programs on MI355X (gfx950): a sequence of dependent
+ * one-row GEMV phases -- the projections of a decode step, in order -- run
+ * as ONE persistent launch.
+ *
+ * No counterpart in the reference's kernel ABI (kernel/q4gemv.c): the
+ * reference's caller makes one q4_gemv call per projection per token
+ * (hetero/cpu_model.py:269-275, :291-292, :367), each one a full round trip.
+ * A phase here computes exactly what one q4_gemv_multi_dev (or, with `pair`,
+ * q4_gate_up_silu_dev) call of one row computes, bit for bit; phase p reads
+ * its x only after every workgroup has finished phase p-1, so a phase may
+ * read the outputs of the phases before it.  Within the launch each wave
+ * issues the weight loads of the next phase before it waits for that
+ * dependency, so the weight stream does not pause at each one.
+ *
+ * All pointers are device pointers on the device current at q4_chain_create.
+ * A plan holds its phase table and barrier state in device memory; it runs
+ * asynchronously on `stream` (a hipStream_t, NULL = the null stream), makes
+ * no allocation or memset when it runs, and can be captured in a HIP graph.
+ * One plan must not run on two streams at once (its barrier state is shared).
+ *
+ * Return codes as in q4gemv.h: 0 success, Q4_EHIP, Q4_ENOMEM, Q4_EARG (text in
+ * q4_last_error()).
+ */
+#ifndef Q4CHAIN_H
+#define Q4CHAIN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* One phase: out[k][0..n_out[k]) = W_k x for count (1..4) matrices sharing
+ * x[0..n_in), or with pair = 1 and count = 2 the gate/up pair,
+ * out[0][i] = SiLU((W_0 x)[i]) * (W_1 x)[i] (out[1] unused).  gs must be 64,
+ * n_in a multiple of 64 up to 24576, w and x 16-byte aligned. */
+typedef struct {
+    int count;
+    int pair;
+    const uint32_t *w[4];
+    const uint16_t *scales[4];
+    const uint16_t *biases[4];
+    float *out[4];
+    int n_out[4];
+    const float *x;
+    int n_in;
+    int gs;
+} q4_chain_phase;
+
+typedef struct q4_chain_plan q4_chain_plan;
+
+/* Check the phases, choose each one's launch shape and upload the table.
+ * Synchronous.  *plan is NULL on failure. */
+int q4_chain_create(const q4_chain_phase *phases, int n_phases, q4_chain_plan **plan);
+
+/* Run every phase, in order, in one launch on `stream`. */
+int q4_chain_run(q4_chain_plan *plan, void *stream);
+
+/* Synchronise the device and return how many barrier waits ran out of time
+ * since the last call (0 in a correct run; then clears the count and the
+ * barrier state).  A run with a nonzero count produced invalid outputs. */
+int q4_chain_errors(q4_chain_plan *plan);
+
+/* Synchronise the device and free the plan (NULL is a no-op). */
+int q4_chain_destroy(q4_chain_plan *plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q4CHAIN_H */

@@ -18,7 +18,7 @@ import pytest
 from hetero import q4
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("q4gemv.h", "q4decode.h", "q4wire.h")]
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("q4gemv.h", "q4decode.h", "q4wire.h", "q4chain.h")]
 
 
 def header_functions():
@@ -146,3 +146,40 @@ def test_wire_codec_argument_errors(lib):
     assert lib.q4_wire_decode_dev(p + 2, 1, 16, 1, p, None) == q4.Q4_EARG
     assert lib.q4_wire_encode_dev(None, 0, 16, 1, None, None) == 0                    # no rows: no-op
     assert lib.q4_wire_decode_dev(None, 0, 16, 1, None, None) == 0
+
+
+def test_chain_argument_errors(lib):
+    """q4_chain_create rejects bad phases with Q4_EARG before any device call."""
+    fake = 1 << 20                                       # 16-byte aligned, never dereferenced
+
+    def phase(**kw):
+        ph = q4.ChainPhase()
+        ph.count, ph.pair, ph.n_in, ph.gs, ph.x = 1, 0, 256, 64, fake
+        ph.w[0] = ph.scales[0] = ph.biases[0] = ph.out[0] = fake
+        ph.n_out[0] = 8
+        for k, v in kw.items():
+            setattr(ph, k, v)
+        return ph
+
+    def create(*phs):
+        arr = (q4.ChainPhase * len(phs))(*phs)
+        plan = ctypes.c_void_p()
+        return lib.q4_chain_create(arr, len(phs), ctypes.byref(plan)), plan
+
+    for bad in (dict(count=0), dict(count=5), dict(pair=1), dict(gs=128), dict(n_in=100), dict(n_in=0),
+                dict(n_in=24576 + 64), dict(x=fake + 4), dict(x=0)):
+        rc, plan = create(phase(**bad))
+        assert rc == q4.Q4_EARG and not plan.value, bad
+    ph = phase()
+    ph.w[0] = fake + 8                                   # misaligned weights
+    assert create(ph)[0] == q4.Q4_EARG
+    ph = phase(count=2, pair=1)                          # pair with unequal rows / a null matrix
+    ph.w[1] = ph.scales[1] = ph.biases[1] = ph.out[1] = fake
+    ph.n_out[1] = 16
+    assert create(ph)[0] == q4.Q4_EARG
+    ph.n_out[1], ph.w[1] = 8, 0
+    assert create(ph)[0] == q4.Q4_EARG
+    assert create(phase(), phase(n_in=96))[0] == q4.Q4_EARG      # any bad phase
+    assert lib.q4_chain_create(None, 1, ctypes.byref(ctypes.c_void_p())) == q4.Q4_EARG
+    assert lib.q4_chain_run(None, None) == q4.Q4_EARG
+    assert lib.q4_chain_destroy(None) == 0

@@ -1,0 +1,158 @@
+"""GPU parity of chained GEMV programs (include/q4chain.h): phases run in one
+persistent launch with a grid barrier between them.
+
+Bar: every phase output bit-exact against the oracle on the inputs the
+phase actually read (for gate/up: bit-identical to q4_gate_up_silu_dev, and
+within 2e-6 of NumPy's float32 SiLU of the oracle's gate and up, whose exp
+may differ in the last place); outputs of separate launches of the same
+projections bit-identical; no barrier wait ever runs out of time; graph
+replays equal to the eager run.
+"""
+import numpy as np
+import pytest
+
+from hetero import q4, synth
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(*arrays):
+    import torch
+    return [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrays]
+
+
+def mat(seed, n_out, n_in):
+    w, s, b = synth.qlinear(seed, n_out, n_in, 64)
+    return (w, s, b), tuple(dev(w, s.view(np.int16), b.view(np.int16)))
+
+
+def silu_np(g):
+    with np.errstate(over="ignore"):          # exp(-g) of a large negative g is inf: SiLU(g) = -0.0
+        return g / (np.float32(1.0) + np.exp(-g, dtype=np.float32))
+
+
+def bits(t):
+    return t.cpu().numpy().view(np.uint32)
+
+
+def test_dependent_qwen_layers_bit_exact():
+    """Two Qwen2.5-7B layers of projections, each phase reading the output of
+    the one before: q/k/v -> o -> gate/up -> down -> next layer."""
+    import torch
+    H, I = 3584, 18944
+    o = oracle.Oracle()
+    x0 = synth.activations(1000, 1, H)
+    tx0 = dev(x0)[0]
+    layers, phases, bufs = [], [], []
+    x = tx0
+    for l in range(2):
+        m = [mat(1010 + 10 * l + i, n, k) for i, (n, k) in
+             enumerate(((H, H), (512, H), (512, H), (H, H), (I, H), (I, H), (H, I)))]
+        layers.append(m)
+        q_, k_, v_, o_, h_, d_ = (torch.empty((1, n), device="cuda") for n in (H, 512, 512, H, I, H))
+        phases += [([m[0][1], m[1][1], m[2][1]], x, [q_, k_, v_], False), ([m[3][1]], q_, [o_], False),
+                   ([m[4][1], m[5][1]], o_, [h_], True), ([m[6][1]], h_, [d_], False)]
+        bufs.append((q_, k_, v_, o_, h_, d_))
+        x = d_
+    ch = q4.Chain(phases)
+    ch.run()
+    torch.cuda.synchronize()
+    assert ch.errors() == 0
+    xin = x0
+    for l, (m, (q_, k_, v_, o_, h_, d_)) in enumerate(zip(layers, bufs)):
+        print(f"layer {l}", flush=True)
+        for (wsb, _), got in zip(m[:3], (q_, k_, v_)):
+            assert np.array_equal(bits(got)[0], o.gemv(*wsb, xin[0], 64).view(np.uint32))
+        q_in = q_.cpu().numpy()
+        assert np.array_equal(bits(o_)[0], o.gemv(*m[3][0], q_in[0], 64).view(np.uint32))
+        o_in = o_.cpu().numpy()
+        g, u = o.gemv(*m[4][0], o_in[0], 64), o.gemv(*m[5][0], o_in[0], 64)
+        h = h_.cpu().numpy()[0]
+        assert oracle.normwise_rel(h, silu_np(g) * u) < 2e-6
+        sep = q4.gate_up_silu_dev(m[4][1], m[5][1], o_)
+        torch.cuda.synchronize()
+        assert np.array_equal(h.view(np.uint32), bits(sep)[0])
+        assert np.array_equal(bits(d_)[0], o.gemv(*m[6][0], h, 64).view(np.uint32))
+        xin = d_.cpu().numpy()
+    ch.close()
+
+
+@pytest.mark.parametrize("n_in,counts,pair", [
+    (512, (8,), False),                 # one chunk: ring 1
+    (832, (300, 40), False),            # 13 groups, partial chunk, two matrices
+    (3584, (96, 64, 8, 40), False),     # four matrices of uneven rows: ring 2
+    (6144, (200,), False),              # three chunks: ring 1
+    (18944, (3584,), False),            # ten chunks: ring 5
+    (24576, (64,), False),              # the longest row: twelve chunks
+    (2048, (1000, 1000), True),         # gate/up, one chunk: ring 2
+    (3584, (18944, 18944), True),       # gate/up, Qwen shape: ring 4
+    (320, (48, 48), True),              # gate/up, five groups
+])
+def test_phase_shapes_vs_separate_launches(n_in, counts, pair):
+    """One phase shape per ring size and row layout, run three times in one
+    chain (a dependency-free program, so the barrier is exercised with
+    identical phases), each bit-identical to the separate launch and, for
+    plain phases, to the oracle."""
+    import torch
+    o = oracle.Oracle()
+    mats = [mat(1100 + n_in + i + n, n, n_in) for i, n in enumerate(counts)]
+    x = synth.activations(1101 + n_in, 1, n_in)
+    tx = dev(x)[0]
+    n_outs = counts[:1] if pair else counts
+    outs = [[torch.full((1, n), float("nan"), device="cuda") for n in n_outs] for _ in range(3)]
+    ch = q4.Chain([([m[1] for m in mats], tx, outs[r], pair) for r in range(3)])
+    ch.run()
+    torch.cuda.synchronize()
+    assert ch.errors() == 0
+    if pair:
+        want = [q4.gate_up_silu_dev(mats[0][1], mats[1][1], tx)]
+    else:
+        want = q4.gemv_multi_dev([m[1] for m in mats], tx)
+    torch.cuda.synchronize()
+    for r in range(3):
+        for k, (got, ref) in enumerate(zip(outs[r], want)):
+            assert np.array_equal(bits(got), bits(ref)), f"repeat {r} matrix {k}"
+    if not pair:
+        for (wsb, _), got in zip(mats, outs[0]):
+            assert np.array_equal(bits(got)[0], o.gemv(*wsb, x[0], 64).view(np.uint32))
+    ch.close()
+
+
+def test_graph_replays_and_barrier_reset():
+    """A chain captured in a HIP graph: replays with eager work between them
+    equal the eager run (the barrier state returns to zero after every
+    launch), and the plan runs again eagerly afterwards."""
+    import torch
+    H = 3584
+    mats = [mat(1200 + i, H, H) for i in range(4)]
+    x = dev(synth.activations(1201, 1, H))[0]
+    bufs = [torch.empty((1, H), device="cuda") for _ in range(4)]
+    phases, xin = [], x
+    for m, b in zip(mats, bufs):
+        phases.append(([m[1]], xin, [b], False))
+        xin = b
+    ch = q4.Chain(phases)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        ch.run(st)
+    torch.cuda.synchronize()
+    want = [bits(b) for b in bufs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        ch.run(st)
+    for rep in range(3):
+        for b in bufs:
+            b.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert all(np.array_equal(bits(b), w) for b, w in zip(bufs, want)), f"replay {rep}"
+        y = q4.gemv_dev(*mats[0][1], x)          # eager work between replays
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(y), want[0])
+    ch.run()
+    torch.cuda.synchronize()
+    assert all(np.array_equal(bits(b), w) for b, w in zip(bufs, want))
+    assert ch.errors() == 0
+    ch.close()
