@@ -174,12 +174,14 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nwaves = nt >> 6;
-    uint4* xpl = lds4;                                            // [C*256] swizzled
-    float* xsum_lds = reinterpret_cast<float*>(xpl + C * 256);    // [Gr]
+    // the streaming kernel's LDS layout for one row (stream_lds_bytes)
+    float* xsum_lds = reinterpret_cast<float*>(lds4);             // [Gr]
     float* red = xsum_lds + Gr;                                   // [16]
-    const int NU = PAIR ? 2 * UB : UB;
     int* claim_ctr = reinterpret_cast<int*>(red + 16);
-    float* Tw = red + 16 + 4 + wave * (NU * kTermStride);         // this wave: [NU][kTermStride]
+    uint4* xpl = reinterpret_cast<uint4*>(red + 16 + 4 + 16);     // [C*256] swizzled
+    float* xstage = reinterpret_cast<float*>(xpl);                // [G][stage_stride(0)]: the prologue only
+    const int NU = PAIR ? 2 * UB : UB;
+    float* Tw = reinterpret_cast<float*>(xpl + C * 256) + wave * (NU * kTermStride);   // [NU][kTermStride]
     const int n_total = ph->n_total;
     const int n_units = (n_total + UB - 1) / UB;
     const int items = NU * C;
@@ -216,32 +218,28 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     // group sums in ascending order (kernel/q4gemv.c:244-248) and max |x|
     // (:258-259), as the streaming kernel computes them
     {
+        constexpr int SS = stage_stride(0);
         float amax = 0.0f;
-        const int sub = lane & (WPG - 1);
 #pragma unroll
         for (int r = 0; r < kChainRounds; r++) {
             if (r * nt + wave * 64 < wpr) {                       // uniform: the wave has words this round
                 const float4 a = wv[r][0], b = wv[r][1];
-                const float v8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
                 amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                                          fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
-                float acc = 0.0f;
-#pragma unroll
-                for (int step = 0; step < WPG; step++) {
-                    // lane 8k+step continues the chain of lane 8k+step-1
-                    float s = step == 0 ? 0.0f
-                                        : __int_as_float(__builtin_amdgcn_update_dpp(
-                                              0, __float_as_int(acc), 0x111, 0xF, 0xF, false));
-#pragma unroll
-                    for (int i = 0; i < 8; i++) s = __fadd_rn(s, v8[i]);
-                    acc = sub == step ? s : acc;
-                }
                 const int j = r * nt + tid;
-                if (sub == WPG - 1 && j < wpr) xsum_lds[j / WPG] = acc;
+                if (j < wpr) {
+                    float4* dst = reinterpret_cast<float4*>(xstage + (j / WPG) * SS + (j % WPG) * 8);
+                    dst[0] = a;
+                    dst[1] = b;
+                }
             }
         }
         amax = wave_max(amax);
         if (lane == 0) red[wave] = amax;
+        __syncthreads();
+        // one lane per group adds its 64 values in ascending order
+        for (int g = tid; g < G; g += nt)
+            xsum_lds[g] = chain_add<32>(chain_add<32>(0.0f, xstage + g * SS), xstage + g * SS + 32);
     }
     if (tid == 0) *claim_ctr = 0;
     __syncthreads();
@@ -510,7 +508,7 @@ int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) 
     if (!ring) return fail(Q4_EARG, "no ring size divides %d items", items);
     out.UB = UB;
     out.ring = ring;
-    const size_t need = 16 + stream_lds_bytes(1, C, G, kChainWaves, mult * UB, kChainRounds);
+    const size_t need = 16 + stream_lds_bytes(1, C, G, kChainWaves, mult * UB, kChainRounds, 0);
     if (need > lds) lds = need;
     return 0;
 }

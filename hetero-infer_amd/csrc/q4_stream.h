@@ -65,14 +65,22 @@ struct NormArgs {
 // 4 mod 8 words, so lanes reading different rows spread over the banks.
 constexpr int kTermStride = 36;
 
+// x staged for the group sums: one group's values per LDS row, padded by 4
+// floats so that lanes reading different groups spread over the banks.
+__host__ __device__ constexpr int stage_stride(int gsh) { return (64 << gsh) + 4; }
+
+// LDS of the streaming kernel: a header (group sums [mr][Gr], amax per wave
+// [mr][16], the unit counter, the norm prologue's wave sums [16]), then the
+// x planes and the per-wave term
+// tables -- where the prologue first stages one row of x in fp32.
 // rw: words of x per thread and row (the register rounds of the x prologue).
-inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU, int rw) {
+inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU, int rw, int gsh = 0) {
     (void)rw;
+    const size_t header = static_cast<size_t>(mr) * ((G + 3) & ~3) * 4 + static_cast<size_t>(mr) * 16 * 4 + 16 + 64;
+    const size_t planes = static_cast<size_t>(mr) * n_chunks * 256 * 16;
     const size_t terms = static_cast<size_t>(nwaves) * mr * NU * kTermStride * 4;
-    return static_cast<size_t>(mr) * n_chunks * 256 * 16                 // x planes
-         + static_cast<size_t>(mr) * ((G + 3) & ~3) * 4                  // group sums
-         + static_cast<size_t>(mr) * 16 * 4 + 16                         // amax per wave, counter
-         + terms;                                                        // term tables
+    const size_t stage = static_cast<size_t>(G) * stage_stride(gsh) * 4;
+    return header + (planes + terms > stage ? planes + terms : stage);
 }
 
 __device__ __forceinline__ int mat_of_row(const MatList& ml, int gr) {
@@ -283,12 +291,15 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);    // wave-uniform
     const int nwaves = nt >> 6;
-    uint4* xpl = lds4;                                            // [MR][C*256] swizzled
-    float* xsum_lds = reinterpret_cast<float*>(xpl + MR * C * 256);   // [MR][Gr]
+    float* xsum_lds = reinterpret_cast<float*>(lds4);             // [MR][Gr]
     float* red = xsum_lds + MR * Gr;                              // [MR][16]
-    const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
     int* claim_ctr = reinterpret_cast<int*>(red + MR * 16);       // units handed out past the first
-    float* Tw = red + MR * 16 + 4 + wave * (MR * NU * kTermStride);   // this wave: [MR][NU][kTermStride]
+    float* stage = red + MR * 16 + 4;                              // NORM: the wave sums [16]
+    uint4* xpl = reinterpret_cast<uint4*>(stage + 16);            // [MR][C*256] swizzled
+    float* xstage = reinterpret_cast<float*>(xpl);                // [G][stage_stride]: the prologue only
+    const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
+    float* Tw = reinterpret_cast<float*>(xpl + MR * C * 256) + wave * (MR * NU * kTermStride);
+                                                                  // this wave: [MR][NU][kTermStride]
 
     // ---- x loads: thread t owns words t, t + nt, ... of every row, 8 values
     //      each, through a resource over x (words at or past the row end read
@@ -358,11 +369,9 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
 
     // ---- group sums (kernel/q4gemv.c:244-248: the group's 64 values added
     //      in ascending order) and the running max |x| (:258-259,
-    //      NaN-skipping) per row.  A group is 8 consecutive words, so it
-    //      lies in 8 consecutive lanes of one wave: the wave chains its
-    //      groups itself, lane after lane (row_shr:1), while it waits for
-    //      the other waves' x -- every round's chain at once.
-    float* stage = red + MR * 16 + 4;                              // NORM: the wave sums
+    //      NaN-skipping) per row.  The row is staged in LDS with one group
+    //      per (padded) row, then one lane per group adds its values in
+    //      order: a sequential sum with no cross-lane chain.
     if constexpr (NORM) {
         // hetero/cpu_model.py:304-306 (x + delta) and :164-166 (RMSNorm); the
         // wave sums of squares go through the term tables' space (free until
@@ -400,44 +409,38 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
         wv[0][0][0] = make_float4(v[0], v[1], v[2], v[3]);
         wv[0][0][1] = make_float4(v[4], v[5], v[6], v[7]);
     }
+    constexpr int SS = stage_stride(GSH);                         // staged floats per group
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-        // one chain per round, the rounds' chains independent (interleaved
-        // by the scheduler); words past the row end are 0 and store nothing
-        float v8[RW][8], acc[RW];
         float amax = 0.0f;
 #pragma unroll
         for (int r = 0; r < RW; r++) {
             const float4 a = wv[m][r][0], b = wv[m][r][1];
-            v8[r][0] = a.x; v8[r][1] = a.y; v8[r][2] = a.z; v8[r][3] = a.w;
-            v8[r][4] = b.x; v8[r][5] = b.y; v8[r][6] = b.z; v8[r][7] = b.w;
-            acc[r] = 0.0f;
             amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
                                      fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
         }
-        const int sub = lane & (WPG - 1);
-        if (wave * 64 < wpr) {                                    // uniform: the wave has words
-#pragma unroll
-            for (int step = 0; step < WPG; step++) {
-#pragma unroll
-                for (int r = 0; r < RW; r++) {
-                    // lane 8k+step continues the chain of lane 8k+step-1
-                    float a = step == 0 ? 0.0f
-                                        : __int_as_float(__builtin_amdgcn_update_dpp(
-                                              0, __float_as_int(acc[r]), 0x111, 0xF, 0xF, false));
-#pragma unroll
-                    for (int i = 0; i < 8; i++) a = __fadd_rn(a, v8[r][i]);
-                    acc[r] = sub == step ? a : acc[r];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < RW; r++) {
-                const int j = r * nt + tid;
-                if (sub == WPG - 1 && j < wpr) xsum_lds[m * Gr + j / WPG] = acc[r];
-            }
-        }
         amax = wave_max(amax);
         if (lane == 0) red[m * 16 + wave] = amax;
+        // row m staged in fp32, one group per LDS row: word j of group g at
+        // xstage[g * SS + (j % WPG) * 8] (row m-1's sums are read first)
+        if (m > 0) __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            const int j = r * nt + tid;
+            if (r * nt + wave * 64 < wpr && j < wpr) {            // the wave's round has words; this one
+                float4* dst = reinterpret_cast<float4*>(xstage + (j / WPG) * SS + (j % WPG) * 8);
+                dst[0] = wv[m][r][0];
+                dst[1] = wv[m][r][1];
+            }
+        }
+        __syncthreads();
+        // one lane per group adds its 64 << GSH values in ascending order
+        for (int g = tid; g < G; g += nt) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int h = 0; h < (64 << GSH) / 32; h++) acc = chain_add<32>(acc, xstage + g * SS + h * 32);
+            xsum_lds[m * Gr + g] = acc;
+        }
     }
 #pragma unroll
     for (int d = kE; d < RING; d++) {

@@ -798,7 +798,7 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, c
     if (nwaves < minw) nwaves = minw;
     if (nwaves > kWavesPerCu) nwaves = kWavesPerCu;
     const int rw = (C * kChunkWords + 64 * nwaves - 1) / (64 * nwaves);
-    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB, rw);
+    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB, rw, GSH);
     if (lds > kStreamLdsMax) return 0;
     const int items = (PAIR ? 2 : 1) * UB * C;
     if constexpr (NORM)
