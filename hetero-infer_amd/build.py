@@ -6,7 +6,8 @@ hetero/cpu_model.py here loads it the same way.
 
 csrc/q4gemv.hip (host code, C-ABI and the other kernels), csrc/q4_decode.hip
 (the decode-step kernels of include/q4decode.h), csrc/q4_chain.hip (the
-chained GEMV programs of include/q4chain.h) and the instances of the
+chained GEMV programs of include/q4chain.h), csrc/q4_gemm.hip (the prefill
+GEMM) and the instances of the
 streaming GEMV kernel (csrc/q4_stream_inst.hip, once per activation rows x
 gate/up pair x ring size) are compiled as separate objects in parallel, then
 linked into one shared library.
@@ -27,6 +28,7 @@ SRC = os.path.join(CSRC, "q4gemv.hip")
 DECODE = os.path.join(CSRC, "q4_decode.hip")
 WIRE = os.path.join(CSRC, "q4_wire.hip")
 CHAIN = os.path.join(CSRC, "q4_chain.hip")
+GEMM = os.path.join(CSRC, "q4_gemm.hip")
 INST = os.path.join(CSRC, "q4_stream_inst.hip")
 OUT = os.path.join(HERE, "kernel", "libq4gemv.so")
 
@@ -68,7 +70,8 @@ def build(verbose: bool = False, jobs: int | None = None, out: str = OUT, define
     jobs = jobs or min(16, os.cpu_count() or 4)
     with tempfile.TemporaryDirectory(prefix="q4build") as tmpd:
         units = [(SRC, os.path.join(tmpd, "q4gemv.o"), []), (DECODE, os.path.join(tmpd, "q4_decode.o"), []),
-                 (WIRE, os.path.join(tmpd, "q4_wire.o"), []), (CHAIN, os.path.join(tmpd, "q4_chain.o"), [])]
+                 (WIRE, os.path.join(tmpd, "q4_wire.o"), []), (CHAIN, os.path.join(tmpd, "q4_chain.o"), []),
+                 (GEMM, os.path.join(tmpd, "q4_gemm.o"), [])]
         for mr, pair, ring, gsh in STREAM_INSTANCES:
             obj = os.path.join(tmpd, f"stream_m{mr}_p{pair}_r{ring}_g{gsh}.o")
             units.append((INST, obj, [f"-DQ4_MR={mr}", f"-DQ4_PAIR={pair}", f"-DQ4_RING={ring}", f"-DQ4_GSH={gsh}"]))

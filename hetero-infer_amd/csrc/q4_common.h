@@ -128,6 +128,12 @@ __device__ __forceinline__ uint4 quant_word(const float (&v)[8], float inv, bool
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int num_cus();
 
+// The prefill GEMM (q4_gemm.hip): out (+ z M ldo for split z) = bf16 x .
+// dequant W^T over the N-blocks [nb0, nb0 + nblocks) of 256 columns, tile
+// height bm (256 or 128), S splits of kt_split K steps.
+int gemm_w4(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, int M, int N,
+            int K, int bm, int S, int kt_split, int nb0, int nblocks, int ldo, hipStream_t st);
+
 // Dynamic LDS above 64 KiB needs the kernel's limit raised on each device
 // that runs it.  `done` holds one bit per device already raised (0..63; a
 // higher device id raises it on every call).

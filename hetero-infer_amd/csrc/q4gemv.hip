@@ -369,23 +369,12 @@ __global__ __launch_bounds__(256) void dequant_kernel(
 // ------------------------------------------------ prefill GEMM (bf16 MFMA) --
 //
 // out[M][N] = x[M][K] . W^T for the prompt (M > 16 rows), the contraction the
-// reference hands to BLAS after q4_dequant (hetero/cpu_model.py:119-136).
-// W is dequantised to bf16 inside the B-tile load (fma(q, scale, bias) in
-// fp32, rounded to nearest even: exactly q4_dequant_bf16), x is rounded to
-// bf16 in the A-tile load, and v_mfma_f32_32x32x16_bf16 accumulates in fp32.
-//   * tile BM x BN x 64 (one quantisation group per k-step, so each B row of
-//     a tile has one scale/bias pair), 4 waves as 2 x 2, each wave owning a
-//     (BM/2) x (BN/2) block of 32 x 32 MFMA tiles;
-//   * LDS double-buffered; the next tile's global loads are in flight while
-//     the current tile is multiplied;
-//   * blockIdx.x walks the M blocks: with 4 M blocks and WGs dealt round-robin
-//     to the 8 XCDs, each XCD keeps one M block of x in its L2 and the W tile
-//     of a column of workgroups is read by them back to back.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-constexpr int kGemmLdsK = 72;            // LDS row stride in bf16 (64 + 8 pad: conflict-free)
-
+// reference hands to BLAS after q4_dequant (hetero/cpu_model.py:119-136): x
+// is rounded to bf16 once per call (x_to_bf16_kernel), W stays 4-bit up to
+// the matrix cores (gemm_w4_kernel, q4_gemm.hip), where it becomes
+// bf16(fma(q, scale, bias)) -- exactly q4_dequant_bf16 -- and
+// v_mfma_f32_32x32x16_bf16 accumulates in fp32; split-K partials are added
+// in split order (splitk_sum_kernel).
 // a in the low half, b in the high half, each rounded to nearest even: one
 // v_cvt_pk_bf16_f32 (two scalar conversions became a conversion each plus
 // shifts and ors)
@@ -409,199 +398,6 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
         o.w = pack_bf16x2(b.z, b.w);
         xb[i] = o;
     }
-}
-
-// Prefill GEMM: out[M][N] = bf16(x)[M][K] . bf16(dequant W)[N][K]^T, fp32
-// accumulation on v_mfma_f32_32x32x16_bf16.  Tile BM x BN x 64 (one group
-// of K per step, so each B row has one scale/bias pair per step); 4 waves
-// (2 x 2), each (BM/2) x (BN/2).  A is the bf16 copy of x; B is dequantised
-// while it is stored to LDS (v_cvt_f32_ubyte -> fma with the fp16
-// scale/bias -> RNE to bf16: the value of q4_dequant_bf16_dev).
-// Pipeline: D register slots of loads in flight (step k + D is issued while
-// step k is multiplied), LDS double-buffered; every load goes through a
-// buffer resource bounded to the tile's rows, so rows past M or N and steps
-// past the workgroup's K range read 0 and cost no access.  Split-K:
-// blockIdx.z takes steps [z*kt_split, (z+1)*kt_split) and writes its
-// partial sums to out + z*M*N.
-// EVENG (an even number of groups per row): the scales and biases come in
-// 32-bit words of two consecutive steps, the step's half picked when it is
-// dequantised.  16-bit loads were packed in pairs into one register right
-// after they were issued, which made the compiler wait for every load in
-// flight, the whole prefetch ring included.
-template <int BM, int BN, int D, bool EVENG>
-__global__ __launch_bounds__(256) void gemm_q4_bf16_kernel(
-    const uint16_t* __restrict__ xb, const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
-    const uint16_t* __restrict__ bi, float* __restrict__ out, int M, int N, int K, int kt_split, int nb0, int ldo) {
-    static_assert(D % 2 == 0, "the LDS buffer of a step is its slot parity");
-    extern __shared__ uint4 gemm_lds[];
-    uint16_t* As = reinterpret_cast<uint16_t*>(gemm_lds);          // [2][BM][72]
-    uint16_t* Bs = As + 2 * BM * kGemmLdsK;                        // [2][BN][72]
-    constexpr int TM = BM / 64, TN = BN / 64;                      // 32x32 tiles per wave
-    constexpr int A_PER = BM * 8 / 256;                            // uint4 (8 bf16) of x per thread and step
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);       // wave-uniform
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.x * BM, n0 = (blockIdx.y + nb0) * BN;
-    const int G = K >> 6, wpr = K >> 3;
-    const int kt0 = blockIdx.z * kt_split;
-    const int nk = G - kt0 < kt_split ? G - kt0 : kt_split;
-    const int mrows = M - m0 < BM ? M - m0 : BM, nrows = N - n0 < BN ? N - n0 : BN;
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(xb + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows * K) * 2u);
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(w + static_cast<size_t>(n0) * wpr, static_cast<uint32_t>(nrows * wpr) * 4u);
-    const __amdgpu_buffer_rsrc_t sr = buf_rsrc(sc + static_cast<size_t>(n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
-    const __amdgpu_buffer_rsrc_t br = buf_rsrc(bi + static_cast<size_t>(n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
-    // B: 256 / BN threads per row, WPT words (8 nibbles each) per thread
-    constexpr int QPR = 256 / BN, WPT = 8 / QPR;
-    static_assert(WPT == 8 || WPT == 4 || WPT == 2, "BN is 64, 128 or 256");
-    const int brow = tid / QPR, bq = tid % QPR;
-    struct BVec {
-        uint32_t v[WPT];
-    };
-
-    uint4 ra[D][A_PER];
-    BVec rb[D];
-    using SB = typename std::conditional<EVENG, uint32_t, uint16_t>::type;
-    SB rs[D], rbb[D];
-    // issue the loads of step `it` (relative to kt0) into slot j
-    // the lanes' offsets inside a step; a step adds a uniform offset, or an
-    // offset past every range when it is past the K range (reads 0).  An
-    // add, not a select: a select on the offsets became branches around
-    // duplicated loads, after which every wait on the ring was a full one.
-    uint32_t a_off[A_PER];
-#pragma unroll
-    for (int i = 0; i < A_PER; i++) {
-        const int idx = tid + 256 * i, row = idx >> 3, c = idx & 7;
-        a_off[i] = static_cast<uint32_t>(row * K + c * 8) * 2u;
-    }
-    const uint32_t w_off = static_cast<uint32_t>(brow * wpr + bq * WPT) * 4u;
-    const uint32_t g_off = static_cast<uint32_t>(brow * G) * 2u;
-    auto load = [&](uint4 (&a)[A_PER], BVec& bw, SB& s16, SB& b16, int it) {
-        const int kt = kt0 + it;
-        const uint32_t dead = __builtin_amdgcn_readfirstlane(it < nk ? 0u : kOutOfRange);
-        const uint32_t sa = static_cast<uint32_t>(kt) * 128u + dead;     // 64 bf16 of x per step
-        const uint32_t sw = static_cast<uint32_t>(kt) * 32u + dead;      // 8 words of w per step
-        const uint32_t sg = (EVENG ? static_cast<uint32_t>(kt >> 1) * 4u : static_cast<uint32_t>(kt) * 2u) + dead;
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < A_PER; i++)
-            a[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, a_off[i] + sa, 0, 0));
-        const uint32_t wo = w_off + sw;
-        const uint32_t go = g_off + sg;
-        if constexpr (WPT >= 4) {
-#pragma unroll
-            for (int q = 0; q < WPT / 4; q++) {
-                const uint4 t = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo + 16 * q, 0, 2));
-                bw.v[4 * q] = t.x; bw.v[4 * q + 1] = t.y; bw.v[4 * q + 2] = t.z; bw.v[4 * q + 3] = t.w;
-            }
-        } else {
-            const uint2 t = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(wr, wo, 0, 2));
-            bw.v[0] = t.x; bw.v[1] = t.y;
-        }
-        if constexpr (EVENG) {
-            s16 = __builtin_amdgcn_raw_buffer_load_b32(sr, go, 0, 0);
-            b16 = __builtin_amdgcn_raw_buffer_load_b32(br, go, 0, 0);
-        } else {
-            s16 = __builtin_amdgcn_raw_buffer_load_b16(sr, go, 0, 0);
-            b16 = __builtin_amdgcn_raw_buffer_load_b16(br, go, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // store step `it` (relative to kt0), held in slot (a, bw, s16, b16), into LDS buffer `buf`
-    auto store = [&](const uint4 (&a)[A_PER], const BVec& bw, SB s16, SB b16, int buf, int it) {
-#pragma unroll
-        for (int i = 0; i < A_PER; i++) {
-            const int idx = tid + 256 * i, row = idx >> 3, c = idx & 7;
-            *reinterpret_cast<uint4*>(As + (buf * BM + row) * kGemmLdsK + 8 * c) = a[i];
-        }
-        {
-            const int sh = EVENG ? 16 * ((kt0 + it) & 1) : 0;              // uniform
-            const float sf = h2f(static_cast<uint16_t>(s16 >> sh)), bf = h2f(static_cast<uint16_t>(b16 >> sh));
-            const uint32_t* wd = bw.v;
-#pragma unroll
-            for (int t = 0; t < WPT; t++) {
-                // even values in the bytes of lo, odd ones in hi; v_cvt_f32_ubyteN
-                // turns each byte into a float in one instruction
-                const uint32_t lo = wd[t] & 0x0F0F0F0Fu, hi = (wd[t] >> 4) & 0x0F0F0F0Fu;
-                float v[8];
-#pragma unroll
-                for (int n = 0; n < 4; n++) {
-                    v[2 * n] = __builtin_fmaf(static_cast<float>((lo >> (8 * n)) & 0xFFu), sf, bf);
-                    v[2 * n + 1] = __builtin_fmaf(static_cast<float>((hi >> (8 * n)) & 0xFFu), sf, bf);
-                }
-                uint4 pk;
-                pk.x = pack_bf16x2(v[0], v[1]); pk.y = pack_bf16x2(v[2], v[3]);
-                pk.z = pack_bf16x2(v[4], v[5]); pk.w = pack_bf16x2(v[6], v[7]);
-                *reinterpret_cast<uint4*>(Bs + (buf * BN + brow) * kGemmLdsK + 8 * WPT * bq + 8 * t) = pk;
-            }
-        }
-    };
-
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
-
-#pragma unroll
-    for (int j = 0; j < D; j++) load(ra[j], rb[j], rs[j], rbb[j], j);
-    store(ra[0], rb[0], rs[0], rbb[0], 0, 0);
-    __syncthreads();
-    const int ngroups = (nk + D - 1) / D;
-    for (int g = 0; g < ngroups; g++) {
-#pragma unroll
-        for (int j = 0; j < D; j++) {
-            const int it = g * D + j;
-            const int cur = j & 1;
-            // slot j held step `it` (already in LDS): refill it with step it + D,
-            // then store step it + 1 (loaded D - 1 steps ago) into the other
-            // buffer.  Steps past the K range multiply zeros (their loads read
-            // 0), so the multiply needs no branch.
-            auto mfma_step = [&]() {
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++) {
-                    bf16x8 av[TM], bv[TN];
-#pragma unroll
-                    for (int i = 0; i < TM; i++) {
-                        const int row = wm * (BM / 2) + i * 32 + (lane & 31);
-                        av[i] = *reinterpret_cast<const bf16x8*>(As + (cur * BM + row) * kGemmLdsK + 16 * ks +
-                                                                 8 * (lane >> 5));
-                    }
-#pragma unroll
-                    for (int jj = 0; jj < TN; jj++) {
-                        const int row = wn * (BN / 2) + jj * 32 + (lane & 31);
-                        bv[jj] = *reinterpret_cast<const bf16x8*>(Bs + (cur * BN + row) * kGemmLdsK + 16 * ks +
-                                                                  8 * (lane >> 5));
-                    }
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-#pragma unroll
-                        for (int jj = 0; jj < TN; jj++)
-                            acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[jj], acc[i][jj], 0, 0, 0);
-                }
-            };
-            load(ra[j], rb[j], rs[j], rbb[j], it + D);
-            mfma_step();
-            store(ra[(j + 1) % D], rb[(j + 1) % D], rs[(j + 1) % D], rbb[(j + 1) % D], cur ^ 1, it + 1);
-            __syncthreads();
-        }
-    }
-    // C tile layout: lane l, register v holds row 8*(v/4) + 4*(l/32) + v%4, column l%32
-    // out: this split's [M][ldo] block, whose column 0 is column nb0 * BN of the
-    // product (nb0 = 0 and ldo = N: the whole output)
-    float* o = out + static_cast<size_t>(blockIdx.z) * M * ldo;
-    const int c0 = nb0 * BN;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
-                if (row < M && col < N) o[static_cast<size_t>(row) * ldo + (col - c0)] = acc[i][j][v];
-            }
 }
 
 // out[r][c0 + c] = sum over the S split-K partials part[s][r][c] (r < M,
@@ -1148,35 +944,6 @@ int dequant_launch(const uint32_t* w, const uint16_t* s, const uint16_t* b, void
 }
 
 
-template <int BM, int BN, bool EVENG, int D = 4>      // D: steps in flight
-int launch_gemm(const uint32_t* w, const uint16_t* s, const uint16_t* b, const uint16_t* xb, float* out,
-                int M, int N, int K, int S, int kt_split, hipStream_t st, int nb0 = 0, int nblocks = -1, int ldo = -1) {
-    auto kern = gemm_q4_bf16_kernel<BM, BN, D, EVENG>;
-    const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
-    static std::atomic<uint64_t> lds_raised{0};
-    if (int rc = q4k::raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
-    dim3 grid((M + BM - 1) / BM, nblocks < 0 ? (N + BN - 1) / BN : nblocks, S);
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, xb, w, s, b, out, M, N, K, kt_split, nb0, ldo < 0 ? N : ldo);
-    HIP_TRY(hipGetLastError());
-    return 0;
-}
-
-// Workgroups of the prefill GEMM resident per CU (its LDS decides it).
-template <int BM, int BN>
-int gemm_blocks_per_cu() {
-    static int cached = 0;
-    if (!cached) {
-        const size_t lds = static_cast<size_t>(2) * (BM + BN) * kGemmLdsK * 2;
-        auto kern = gemm_q4_bf16_kernel<BM, BN, 4, true>;
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(lds));
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, 256, lds) != hipSuccess || n < 1) n = 1;
-        cached = n;
-    }
-    return cached;
-}
-
 // The arguments of the norm-prologue entry points: gs 64, n_in in
 // [64, 8192], the vectors 16-byte aligned, x_out overlapping neither input.
 int check_norm_args(const char* who, const float* x, const float* delta, const float* norm_w, const float* x_out,
@@ -1596,77 +1363,51 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
         if ((rc = current_device(&dev))) return rc;
         ws = &g_dev[dev].ws[st];
     }
-    // tiles: 128 x 128 when split-K (up to 8) can fill the CUs with them,
-    // else 128 x 64.  The A tile (x) is read once per N-block, so the wider
-    // tile halves the bytes of x read (down at M=512: 1.1 GB per call with
-    // 64 columns).  Split K in two while the workgroups do not fill the CUs
-    // twice and every split keeps at least 8 groups of K.
+    // Tile height and split-K from a cost model of the W4 kernel measured at
+    // M = 512: a K step of a 256 x 256 tile takes about 2.3 us, of a
+    // 128 x 256 tile 2.0 us, plus about two steps of pipeline fill per
+    // workgroup; the workgroups run in rounds of one per CU; split partials
+    // cost a write and a read of M x N floats each (about 4.5 TB/s) plus the
+    // sum launch.  Every split keeps at least 2 steps of K.
     const int cus = num_cus();
-    const long tiles128 = static_cast<long>((m + 127) / 128) * ((n_out + 127) / 128);
-    const int BN = tiles128 * 8 >= cus ? 128 : 64;
-    const long tiles = static_cast<long>((m + 127) / 128) * ((n_out + BN - 1) / BN);
     const int G = n_in / 64;
-    int S = 1;
-    while (S < 8 && tiles * S < 2L * cus && G / (2 * S) >= 8) S *= 2;
-    const int kt_split = (G + S - 1) / S;
-    S = (G + kt_split - 1) / kt_split;
-    // A last round of resident workgroups that is at most half full gets its
-    // tiles (the last N-blocks) in a launch of its own, split along K to fill
-    // the round: gate/up at M=512 are 592 tiles of 128 x 128 on 512 slots.
-    const int MB = (m + 127) / 128, NB = (n_out + BN - 1) / BN;
-    int main_nb = NB, rem_nb = 0, S2 = 1, kt2 = G;
-    if (S == 1) {
-        const long P = static_cast<long>(cus) * (BN == 128 ? gemm_blocks_per_cu<128, 128>() : gemm_blocks_per_cu<128, 64>());
-        const long full = (tiles / P) * P;
-        if (full > 0 && tiles > full && tiles - full <= P / 2) {
-            const int nb = static_cast<int>(full / MB);
-            int s2 = static_cast<int>(P / (static_cast<long>(MB) * (NB - nb)));
-            if (s2 > 8) s2 = 8;
-            while (s2 > 1 && G / s2 < 8) --s2;
-            if (s2 >= 2) {
-                main_nb = nb;
-                rem_nb = NB - nb;
-                kt2 = (G + s2 - 1) / s2;
-                S2 = (G + kt2 - 1) / kt2;
+    int bm = 256, S = 1;
+    double best = 1e30;
+    for (int cand_bm : {256, 128}) {
+        const long tiles = static_cast<long>((m + cand_bm - 1) / cand_bm) * ((n_out + 255) / 256);
+        const double t_step = cand_bm == 256 ? 2.3 : 2.0;
+        for (int cand_s = 1; cand_s <= 16 && G / cand_s >= 2; cand_s++) {
+            const int kts = (G + cand_s - 1) / cand_s;
+            const int sn = (G + kts - 1) / kts;                   // splits actually used
+            if (sn != cand_s) continue;
+            const long rounds = (tiles * sn + cus - 1) / cus;
+            const double est = static_cast<double>(rounds) * (kts + 2) * t_step +
+                               (sn > 1 ? static_cast<double>(sn) * m * n_out * 8.0 / 4.5e6 + 3.0 : 0.0);
+            if (est < best) {
+                best = est;
+                bm = cand_bm;
+                S = sn;
             }
         }
     }
-    const int W = rem_nb ? (n_out - main_nb * BN < rem_nb * BN ? n_out - main_nb * BN : rem_nb * BN) : 0;
+    const int kt_split = (G + S - 1) / S;
     const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * n_out;
     if ((rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
-    const size_t part_bytes = S > 1 ? S * mn * 4 : static_cast<size_t>(S2) * m * W * 4;
-    if (part_bytes && (rc = grow(*ws, ws->part, kWsPart, part_bytes, st, "prefill"))) return rc;
+    if (S > 1 && (rc = grow(*ws, ws->part, kWsPart, S * mn * 4, st, "prefill"))) return rc;
     const long n8 = static_cast<long>(mk / 8);
     hipLaunchKernelGGL(x_to_bf16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, st, x,
                        static_cast<uint4*>(ws->xbf), n8);
     HIP_TRY(hipGetLastError());
     const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
-    float* part = static_cast<float*>(ws->part);
-    auto gemm = [&](float* dst, int splits, int kts, int nb0, int nblocks, int ldo) {
-        if (G % 2 == 0)
-            return BN == 128 ? launch_gemm<128, 128, true>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
-                                                           nb0, nblocks, ldo)
-                             : launch_gemm<128, 64, true>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
-                                                          nb0, nblocks, ldo);
-        return BN == 128 ? launch_gemm<128, 128, false>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
-                                                        nb0, nblocks, ldo)
-                         : launch_gemm<128, 64, false>(w, scales, biases, xb, dst, m, n_out, n_in, splits, kts, st,
-                                                       nb0, nblocks, ldo);
-    };
-    auto ksum = [&](int width, int c0, int splits) -> int {
-        const long n = static_cast<long>(m) * width;
-        hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
-                           static_cast<const float*>(part), out, m, width, n_out, c0, splits);
-        HIP_TRY(hipGetLastError());
-        return 0;
-    };
-    if (rem_nb) {
-        if ((rc = gemm(out, 1, G, 0, main_nb, n_out))) return rc;
-        if ((rc = gemm(part, S2, kt2, main_nb, rem_nb, W))) return rc;
-        return ksum(W, main_nb * BN, S2);
-    }
-    if ((rc = gemm(S > 1 ? part : out, S, kt_split, 0, NB, n_out)) || S == 1) return rc;
-    return ksum(n_out, 0, S);
+    float* dst = S > 1 ? static_cast<float*>(ws->part) : out;
+    if ((rc = gemm_w4(xb, w, scales, biases, dst, m, n_out, n_in, bm, S, kt_split, 0, (n_out + 255) / 256, n_out, st)))
+        return rc;
+    if (S == 1) return 0;
+    const long n = static_cast<long>(mn);
+    hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const float*>(ws->part), out, m, n_out, n_out, 0, S);
+    HIP_TRY(hipGetLastError());
+    return 0;
 }
 
 int q4_dequant_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,

@@ -153,8 +153,32 @@ def test_attention(torch, lib, nh, nkv):
     q_np = rng.normal(0, 1, nh * d).astype(np.float32)
     kc, vc, tq = (torch.from_numpy(a).to(dev) for a in (kc_np, vc_np, q_np))
     out = torch.empty(nh * d, device=dev)
-    scratch = torch.empty(lib.q4_attention_scratch_floats(nh, d, cap), device=dev)
+    scratch = torch.zeros(lib.q4_attention_scratch_floats(nh, d, cap), device=dev)
     for p in (0, 5, 63, 64, 65, 127, 128, cap - 1):
+        pos = torch.tensor([p], dtype=torch.int64, device=dev)
+        rc = lib.q4_attention_dev(tq.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(),
+                                  scratch.data_ptr(), nh, nkv, d, cap, float(scale), sp(torch))
+        assert rc == 0, q4.last_error(lib)
+        ref = attention_ref(q_np, kc_np, vc_np, p, nh, nkv, float(scale))
+        assert oracle.normwise_rel(out.cpu().numpy(), ref) < ATTN_TOL, p
+
+
+def test_attention_long_context(torch, lib):
+    """Contexts past the combine's prefetch (32 chunks of 64 positions per
+    part) and past one chunk per thread for m and l (256 chunks would be the
+    next step): up to 79 chunks, the ones beyond the prefetch merged by the
+    combine's fallback loop, against the fp64 reference."""
+    rng = np.random.default_rng(9)
+    nh, nkv, d, cap = 28, 4, 128, 5000
+    scale = np.float32(d ** -0.5)
+    dev = torch.device("cuda")
+    kc_np = rng.normal(0, 1, (nkv, cap, d)).astype(np.float16)
+    vc_np = rng.normal(0, 1, (nkv, cap, d)).astype(np.float16)
+    q_np = rng.normal(0, 1, nh * d).astype(np.float32)
+    kc, vc, tq = (torch.from_numpy(a).to(dev) for a in (kc_np, vc_np, q_np))
+    out = torch.empty(nh * d, device=dev)
+    scratch = torch.zeros(lib.q4_attention_scratch_floats(nh, d, cap), device=dev)
+    for p in (2559, 2560, 2561, 4095, 4096, cap - 1):
         pos = torch.tensor([p], dtype=torch.int64, device=dev)
         rc = lib.q4_attention_dev(tq.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(),
                                   scratch.data_ptr(), nh, nkv, d, cap, float(scale), sp(torch))
@@ -181,7 +205,7 @@ def test_attention_rope_matches_separate_calls(torch, lib, nh, nkv):
     kc_b, vc_b = kc_a.clone(), vc_a.clone()
     q_rot = torch.empty(nh * d, device=dev)
     out_a, out_b = torch.empty(nh * d, device=dev), torch.empty(nh * d, device=dev)
-    scratch = torch.empty(lib.q4_attention_scratch_floats(nh, d, cap), device=dev)
+    scratch = torch.zeros(lib.q4_attention_scratch_floats(nh, d, cap), device=dev)
     for p in (0, 1, 2, 62, 63, 64, 65, 100, 127, 128, cap - 1, cap, cap + 5):
         q, k, v = (torch.from_numpy(rng.normal(0, 1, n * d).astype(np.float32)).to(dev) for n in (nh, nkv, nkv))
         pos = torch.tensor([p], dtype=torch.int64, device=dev)

@@ -29,10 +29,11 @@ def bf16_round(a):
     return b.astype(np.uint32).view(np.float32)
 
 
-# (500, 16600, 1024) and (512, 18944, 3584) have more 128 x 128 tiles than one
-# round of resident workgroups holds, so their last tiles take the launch of
-# their own split along K (a partial last tile in the first of them);
-# (512, 3584, 18944) is down_proj of a 512-token prompt, split along K
+# Shapes that take each tile height and split: (37, 200, 512) and
+# (130, 96, 1024) partial 128-row and 256-column tiles; (512, 3584, 3584) and
+# (512, 512, 3584) split along K; (500, 16600, 1024) a partial last tile of
+# both kinds; (512, 18944, 3584) gate/up of a 512-token prompt unsplit;
+# (512, 3584, 18944) and (64, 3584, 18944) down_proj, split along K
 @pytest.mark.parametrize("m,n_out,n_in", [(37, 200, 512), (130, 96, 1024), (512, 3584, 3584),
                                           (512, 512, 3584), (64, 3584, 18944), (500, 16600, 1024),
                                           (512, 18944, 3584), (512, 3584, 18944)])
