@@ -134,6 +134,14 @@ int num_cus();
 int gemm_w4(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, int M, int N,
             int K, int bm, int S, int kt_split, int nb0, int nblocks, int ldo, hipStream_t st);
 
+// Stream-K form of the prefill GEMM: P workgroups in nx XCD groups (256 x
+// 256 tiles; P a multiple of nx, and P / nx at least a group's tile count,
+// ceil(tiles / nx)), out [M][N].  part: P x 256 x 256 floats of partial
+// sums; flags: 32 P words, zero on entry and on return; errors: a counter of
+// partials that did not arrive in time (their tiles are NaN).
+int gemm_w4_sk(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, float* part,
+               unsigned* flags, unsigned* errors, int M, int N, int K, int P, int nx, hipStream_t st);
+
 // Dynamic LDS above 64 KiB needs the kernel's limit raised on each device
 // that runs it.  `done` holds one bit per device already raised (0..63; a
 // higher device id raises it on every call).

@@ -92,63 +92,90 @@ __device__ __forceinline__ void w4_issue(char* st, __amdgpu_buffer_rsrc_t xr, __
     }
 }
 
-// NW waves as 2 x NW/2: each wave (BM/2) x (512/NW) columns.
-template <int BM, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __restrict__ xb, const uint32_t* __restrict__ w,
-                                                          const uint16_t* __restrict__ sc,
-                                                          const uint16_t* __restrict__ bi, float* __restrict__ out,
-                                                          int M, int N, int K, int kt_split, int nb0, int ldo) {
-    constexpr int BN = 256, WN = NW / 2, WC = BN / WN;             // waves along N, columns per wave
-    constexpr int TM = BM / 64, TN = WC / 32;                      // 32 x 32 tiles per wave
-    constexpr int A_DMA = BM / (8 * NW), B_DMA = 8 / NW;
-    constexpr int PER_STEP = A_DMA + B_DMA + (NW == 4 ? 2 : 1);    // copies per wave and step
-    constexpr int STAGE = w4_stage_bytes(BM);
-    extern __shared__ uint4 w4_lds[];
-    char* lds = reinterpret_cast<char*>(w4_lds);
-    const int tid = threadIdx.x, lane = tid & 63, hb = lane >> 5;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-    const int m0 = blockIdx.x * BM, n0 = (blockIdx.y + nb0) * BN;
-    const int G = K >> 6, wpr = K >> 3;
-    const int kt0 = blockIdx.z * kt_split;
-    const int nk = G - kt0 < kt_split ? G - kt0 : kt_split;
-    const int mrows = M - m0 < BM ? M - m0 : BM, nrows = N - n0 < BN ? N - n0 : BN;
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(xb + static_cast<size_t>(m0) * K, static_cast<uint32_t>(mrows * K) * 2u);
-    const __amdgpu_buffer_rsrc_t wr = buf_rsrc(w + static_cast<size_t>(n0) * wpr, static_cast<uint32_t>(nrows * wpr) * 4u);
-    const __amdgpu_buffer_rsrc_t sr = buf_rsrc(sc + static_cast<size_t>(n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
-    const __amdgpu_buffer_rsrc_t br = buf_rsrc(bi + static_cast<size_t>(n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
+// The operands of one tile (M block mt, N block nt): buffer resources over
+// its rows of x, W, scales and biases.
+struct W4Tile {
+    __amdgpu_buffer_rsrc_t xr, wr, sr, br;
+    int m0, n0;
+};
 
-    // per-lane source offsets of the step's copies (step kt adds kt * 128,
-    // kt * 32 and kt * 2 bytes).  A: copy i of wave w moves rows
-    // 8 (w A_DMA + i) .. + 8, lane -> (row, 16-byte chunk c), reading chunk
-    // c ^ (row & 7) of the row: the stage holds row r's chunk c at
-    // r * 128 + (c ^ (r & 7)) * 16.  B: copy q moves rows 32 (B_DMA w + q) ..
-    // + 32, two lanes per row.  Scales / biases: one row per lane, a
-    // zero-extended word each.
-    uint32_t a_src[A_DMA];
+template <int BM>
+__device__ __forceinline__ W4Tile w4_tile(const uint16_t* xb, const uint32_t* w, const uint16_t* sc, const uint16_t* bi,
+                                          int M, int N, int K, int mt, int nt) {
+    constexpr int BN = 256;
+    W4Tile t;
+    t.m0 = mt * BM;
+    t.n0 = nt * BN;
+    const int G = K >> 6, wpr = K >> 3;
+    const int mrows = M - t.m0 < BM ? M - t.m0 : BM, nrows = N - t.n0 < BN ? N - t.n0 : BN;
+    t.xr = buf_rsrc(xb + static_cast<size_t>(t.m0) * K, static_cast<uint32_t>(mrows * K) * 2u);
+    t.wr = buf_rsrc(w + static_cast<size_t>(t.n0) * wpr, static_cast<uint32_t>(nrows * wpr) * 4u);
+    t.sr = buf_rsrc(sc + static_cast<size_t>(t.n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
+    t.br = buf_rsrc(bi + static_cast<size_t>(t.n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
+    return t;
+}
+
+// Per-lane source offsets of a step's copies (step kt adds kt * 128, kt * 32
+// and kt * 2 bytes).  A: copy i of wave w moves rows 8 (w A_DMA + i) .. + 8,
+// lane -> (row, 16-byte chunk c), reading chunk c ^ (row & 7) of the row:
+// the stage holds row r's chunk c at r * 128 + (c ^ (r & 7)) * 16.  B: copy
+// q moves rows 32 (B_DMA w + q) .. + 32, two lanes per row.  Scales /
+// biases: one row per lane, a zero-extended word each.
+template <int BM, int NW>
+struct W4Src {
+    uint32_t a[BM / (8 * NW)];
+    uint32_t b[8 / NW];
+    uint32_t g;
+};
+
+template <int BM, int NW>
+__device__ __forceinline__ void w4_src(W4Src<BM, NW>& src, int K, int wave, int lane) {
+    constexpr int A_DMA = BM / (8 * NW), B_DMA = 8 / NW;
+    const int G = K >> 6, wpr = K >> 3;
 #pragma unroll
     for (int i = 0; i < A_DMA; i++) {
         const int r = (wave * A_DMA + i) * 8 + (lane >> 3), c = lane & 7;
-        a_src[i] = static_cast<uint32_t>(r * K + (c ^ (r & 7)) * 8) * 2u;
+        src.a[i] = static_cast<uint32_t>(r * K + (c ^ (r & 7)) * 8) * 2u;
     }
-    uint32_t b_src[B_DMA];
 #pragma unroll
     for (int q = 0; q < B_DMA; q++) {
         const int r = (B_DMA * wave + q) * 32 + (lane >> 1);
-        b_src[q] = static_cast<uint32_t>(r * wpr + (lane & 1) * 4) * 4u;
+        src.b[q] = static_cast<uint32_t>(r * wpr + (lane & 1) * 4) * 4u;
     }
-    const uint32_t g_src = static_cast<uint32_t>(((NW == 4 ? wave : wave & 3) * 64 + lane) * G) * 2u;
+    src.g = static_cast<uint32_t>(((NW == 4 ? wave : wave & 3) * 64 + lane) * G) * 2u;
+}
 
-    gemm_f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
+// How NW waves split a BM x 256 tile: WM x WN waves of RW rows x WC
+// columns, TM x TN MFMA tiles of 32 x 32 each.  256-row tiles: 1 x 4 waves
+// of 256 x 64 -- each weight word is dequantised once and feeds 8 MFMAs
+// (a 2 x 2 split dequantises every word twice and measured 12% slower per
+// K step); 128-row tiles: 2 x 4 waves of 64 x 64.
+template <int BM, int NW>
+struct W4Layout {
+    static constexpr int WN = BM == 256 ? NW : NW / 2, WM = NW / WN;
+    static constexpr int RW = BM / WM, WC = 256 / WN;
+    static constexpr int TM = RW / 32, TN = WC / 32;
+};
 
-    w4_issue<BM, NW>(lds, xr, wr, sr, br, a_src, b_src, g_src, kt0, 0 < nk, wave);
-    w4_issue<BM, NW>(lds + STAGE, xr, wr, sr, br, a_src, b_src, g_src, kt0 + 1, 1 < nk, wave);
+template <int BM, int NW>
+using W4Acc = gemm_f32x16[W4Layout<BM, NW>::TM][W4Layout<BM, NW>::TN];
+
+// K steps [k0, k0 + nk) of one tile into acc (which it adds to): the copy
+// pipeline starts and drains inside, and on return every wave is past its
+// last LDS read and no copy is in flight, so the next segment may reuse the
+// ring.
+template <int BM, int NW>
+__device__ __forceinline__ void w4_segment(W4Acc<BM, NW>& acc, char* lds, const W4Tile& t, const W4Src<BM, NW>& src,
+                                           int k0, int nk, int wave, int lane) {
+    using L = W4Layout<BM, NW>;
+    constexpr int WN = L::WN, WC = L::WC, RW = L::RW, TM = L::TM, TN = L::TN;
+    constexpr int A_DMA = BM / (8 * NW), B_DMA = 8 / NW;
+    constexpr int PER_STEP = A_DMA + B_DMA + (NW == 4 ? 2 : 1);    // copies per wave and step
+    constexpr int STAGE = w4_stage_bytes(BM);
+    const int hb = lane >> 5;
+    const int wm = wave / WN, wn = wave % WN;
+    w4_issue<BM, NW>(lds, t.xr, t.wr, t.sr, t.br, src.a, src.b, src.g, k0, 0 < nk, wave);
+    w4_issue<BM, NW>(lds + STAGE, t.xr, t.wr, t.sr, t.br, src.a, src.b, src.g, k0 + 1, 1 < nk, wave);
     for (int it = 0; it < nk; it++) {
         // step it's copies are done (only step it + 1's may be in flight)
         __builtin_amdgcn_s_waitcnt(0x0F70 | PER_STEP);
@@ -156,8 +183,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
         // wave is past step it - 1, whose stage step it + 2 refills (a fence
         // would also wait for the copies of step it + 1)
         __builtin_amdgcn_s_barrier();
-        w4_issue<BM, NW>(lds + ((it + 2) % 3) * STAGE, xr, wr, sr, br, a_src, b_src, g_src, kt0 + it + 2, it + 2 < nk,
-                         wave);
+        w4_issue<BM, NW>(lds + ((it + 2) % 3) * STAGE, t.xr, t.wr, t.sr, t.br, src.a, src.b, src.g, k0 + it + 2,
+                         it + 2 < nk, wave);
         const char* st = lds + (it % 3) * STAGE;
         const uint16_t* As = reinterpret_cast<const uint16_t*>(st);
         const uint32_t* Bs = reinterpret_cast<const uint32_t*>(st + BM * 128);
@@ -180,7 +207,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
             }
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                const int row = wm * (BM / 2) + i * 32 + (lane & 31);
+                const int row = wm * RW + i * 32 + (lane & 31);
                 const int c = (2 * ks + hb) ^ (row & 7);
                 av[i] = *reinterpret_cast<const gemm_bf16x8*>(As + row * 64 + c * 8);
             }
@@ -191,24 +218,273 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
     }
-    // C tile: lane l, register v holds row 8 (v / 4) + 4 (l / 32) + v % 4,
-    // column l % 32.  out: this split's [M][ldo] block, whose column 0 is
-    // column nb0 * BN of the product
-    float* o = out + static_cast<size_t>(blockIdx.z) * M * ldo;
-    const int c0 = nb0 * BN;
+    // the last copies issued (past the segment) read nothing; wait for them,
+    // and for every wave's last LDS reads
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+}
+
+// C tile: lane l, register v holds row 8 (v / 4) + 4 (l / 32) + v % 4,
+// column l % 32.  o: a [M][ldo] block whose column 0 is column c0 of the
+// product.
+template <int BM, int NW>
+__device__ __forceinline__ void w4_store(const W4Acc<BM, NW>& acc, float* o, const W4Tile& t, int M, int N, int ldo,
+                                         int c0, int wave, int lane) {
+    using L = W4Layout<BM, NW>;
+    constexpr int WN = L::WN, WC = L::WC, RW = L::RW, TM = L::TM, TN = L::TN;
+    const int hb = lane >> 5, wm = wave / WN, wn = wave % WN;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (v >> 2) + 4 * hb + (v & 3);
-                const int col = n0 + wn * WC + j * 32 + (lane & 31);
+                const int row = t.m0 + wm * RW + i * 32 + 8 * (v >> 2) + 4 * hb + (v & 3);
+                const int col = t.n0 + wn * WC + j * 32 + (lane & 31);
                 if (row < M && col < N) o[static_cast<size_t>(row) * ldo + (col - c0)] = acc[i][j][v];
             }
-    // the last copies issued (past the K range) read nothing; wait for them
-    // before the workgroup's LDS is released
-    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// Part h of NP of w4_store's tiles (i TN + j in [h TM TN / NP, (h + 1) TM TN
+// / NP)), into a [M][N] output; NaN in place of every value if `poison`.
+template <int BM, int NW, int NP>
+__device__ __forceinline__ void w4_store_rows(const W4Acc<BM, NW>& acc, float* o, const W4Tile& t, int M, int N, int h,
+                                              bool poison, int wave, int lane) {
+    using L = W4Layout<BM, NW>;
+    constexpr int WN = L::WN, WC = L::WC, RW = L::RW, TM = L::TM, TN = L::TN;
+    const int hb = lane >> 5, wm = wave / WN, wn = wave % WN;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            if ((i * TN + j) / (TM * TN / NP) != h) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = t.m0 + wm * RW + i * 32 + 8 * (v >> 2) + 4 * hb + (v & 3);
+                const int col = t.n0 + wn * WC + j * 32 + (lane & 31);
+                if (row < M && col < N)
+                    o[static_cast<size_t>(row) * N + col] = poison ? __builtin_nanf("") : acc[i][j][v];
+            }
+        }
+}
+
+template <int BM, int NW>
+__device__ __forceinline__ void w4_zero(W4Acc<BM, NW>& acc) {
+    constexpr int TM = W4Layout<BM, NW>::TM, TN = W4Layout<BM, NW>::TN;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
+}
+
+// Data-parallel: workgroup (mt, nt - nb0, z) computes K steps
+// [z kt_split, (z+1) kt_split) of tile (mt, nt) into out + z M ldo.
+template <int BM, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __restrict__ xb, const uint32_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ sc,
+                                                          const uint16_t* __restrict__ bi, float* __restrict__ out,
+                                                          int M, int N, int K, int kt_split, int nb0, int ldo) {
+    extern __shared__ uint4 w4_lds[];
+    char* lds = reinterpret_cast<char*>(w4_lds);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = K >> 6;
+    const int kt0 = blockIdx.z * kt_split;
+    const int nk = G - kt0 < kt_split ? G - kt0 : kt_split;
+    const W4Tile t = w4_tile<BM>(xb, w, sc, bi, M, N, K, blockIdx.x, blockIdx.y + nb0);
+    W4Src<BM, NW> src;
+    w4_src<BM, NW>(src, K, wave, lane);
+    W4Acc<BM, NW> acc;
+    w4_zero<BM, NW>(acc);
+    w4_segment<BM, NW>(acc, lds, t, src, kt0, nk, wave, lane);
+    w4_store<BM, NW>(acc, out + static_cast<size_t>(blockIdx.z) * M * ldo, t, M, N, ldo, nb0 * 256, wave, lane);
+}
+
+// Stream-K: the tiles (m block major) are split into nx contiguous groups,
+// one per XCD, and each group's T = tiles x G (tile, K step) iterations,
+// tile-major and K-minor, into P equal contiguous ranges, one per workgroup
+// of that XCD.  A range is at most G iterations long (the host launches at
+// least as many workgroups per group as the group has tiles), so it covers
+// at most two segments, a tile's tail and the next tile's head; the
+// workgroup runs the head first.  A segment that does not reach its tile's
+// end is a partial: it goes to the workgroup's slot in `part` at device
+// scope, then its flag is raised.  The segment that ends a tile (its
+// owner's) adds the partials of the workgroups before it in its group that
+// cover the rest of the tile, nearest first, and stores the tile.  Waits
+// point only to lower-numbered workgroups, which are dispatched first, and
+// a partial is a workgroup's first segment whenever it has two, so an
+// owner, which reaches its tail last, rarely waits.  The owner lowers the
+// flags it consumed: they are zero again for the next launch.
+//
+// A slot holds 256 x 256 floats as [block b][quad q][thread] of 16 bytes,
+// block b = i TN + j of the accumulators, quad q = v / 4: every store and
+// LDS read of a wave is 1 KiB contiguous.  The owner cannot add a whole
+// partial in registers (the accumulators live in AGPRs, which VALU adds do
+// not read), so it brings each quarter of a slot into the drained LDS ring by
+// global->LDS copies and adds it from there, storing each quarter of the
+// tile once its partials are in.
+constexpr int kSkParts = 4;                                        // the owner adds a slot in 4 parts
+constexpr int kSkFlagStride = 32;                                  // flags 128 bytes apart
+constexpr long long kSkSpinTicks = 20000000;                       // 200 ms at 100 MHz
+
+// A workgroup's stream-K group: the tiles [t0, t0 + T / G) of XCD `xcd`
+// (tiles m-block major, split into nx contiguous groups; workgroup i runs
+// on XCD i mod nx, so an XCD's L2 holds only its group's rows of x), run
+// by the P workgroups xcd, xcd + nx, .. (slots 0 .. P - 1).
+struct SkGroup {
+    long T;
+    int P, slot, xcd, nx, t0;
+    __device__ int phys(int s) const { return xcd + nx * s; }
+};
+
+// Segment [it, stop) of a stream-K range (stop at most its tile's end).
+template <int BM, int NW>
+__device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, const uint32_t* w, const uint16_t* sc,
+                                              const uint16_t* bi, float* out, float* part, unsigned* flags,
+                                              unsigned* errors, int M, int N, int K, const SkGroup& gp, long it,
+                                              long stop, const W4Src<BM, NW>& src, int tid, int wave, int lane) {
+    typedef __attribute__((address_space(3))) void* lds_ptr;
+    constexpr int TM = W4Layout<BM, NW>::TM, TN = W4Layout<BM, NW>::TN, NB = TM * TN;
+    constexpr int NT = 64 * NW;
+    constexpr int kDevice = 16;                                    // sc1: device-coherent
+    constexpr uint32_t kSlotBytes = 256u * 256u * 4u;
+    using u32x4 = unsigned int __attribute__((__vector_size__(16)));
+    const int G = K >> 6, NTL = (N + 255) / 256;
+    const long T = gp.T;
+    const int P = gp.P, wg = gp.slot;
+    W4Acc<BM, NW> acc;
+    const int k0 = static_cast<int>(it % G);
+    const int nk = static_cast<int>(stop - it);
+    const long tile_start = it - k0;                               // in the group's iterations
+    const int tile = gp.t0 + static_cast<int>(it / G);
+    const W4Tile t = w4_tile<BM>(xb, w, sc, bi, M, N, K, tile / NTL, tile % NTL);
+    w4_zero<BM, NW>(acc);
+    w4_segment<BM, NW>(acc, lds, t, src, k0, nk, wave, lane);
+    if (stop < tile_start + G) {
+        const __amdgpu_buffer_rsrc_t pr =
+            buf_rsrc(part + static_cast<size_t>(gp.phys(wg)) * (kSlotBytes / 4), kSlotBytes);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int v = 0; v < 16; v += 4) {
+                    // by value: a bit cast of a vector element would read element 0
+                    const u32x4 q = {__float_as_uint(acc[i][j][v]), __float_as_uint(acc[i][j][v + 1]),
+                                     __float_as_uint(acc[i][j][v + 2]), __float_as_uint(acc[i][j][v + 3])};
+                    const uint32_t o = static_cast<uint32_t>(((i * TN + j) * 4 + v / 4) * NT + tid) * 16u;
+                    __builtin_amdgcn_raw_buffer_store_b128(q, pr, o, 0, kDevice);
+                }
+        __builtin_amdgcn_s_waitcnt(0x0F70);                    // this thread's stores have landed
+        __syncthreads();
+        if (tid == 0)
+            __hip_atomic_store(flags + gp.phys(wg) * kSkFlagStride, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        // the partials of workgroups wg - 1, wg - 2, .. j1, whose ranges
+        // end inside this tile
+        int j1 = wg;
+        while (j1 > 0 && T * j1 / P > tile_start) j1--;
+        int missing = 0;
+        if (tid == 0) {
+            for (int j = wg - 1; j >= j1; j--) {
+                if (T * (j + 1) / P == T * j / P) continue;        // an empty range
+                const long long t0 = __builtin_amdgcn_s_memrealtime();
+                while (__hip_atomic_load(flags + gp.phys(j) * kSkFlagStride, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) ==
+                       0u) {
+                    if (__builtin_amdgcn_s_memrealtime() - t0 > kSkSpinTicks) {
+                        __hip_atomic_fetch_add(errors, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        missing = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+                __hip_atomic_store(flags + gp.phys(j) * kSkFlagStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        // a tile whose partials did not all arrive is stored as NaN
+        const bool poison = __syncthreads_or(missing) != 0;
+        // the partials, not stale cache lines (only when there are any: the
+        // invalidate also drops the operand lines the XCD's other
+        // workgroups are streaming)
+        if (j1 < wg) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        // part h of the tile (blocks h NB / kSkParts ..): each partial's part
+        // in turn through LDS, then the part is stored, so only a quarter of
+        // the accumulators is ever live in VGPRs
+        constexpr int PB = NB / kSkParts;                          // blocks per part
+        constexpr int PCH = PB * 16;                               // 1 KiB chunks per part
+#pragma unroll
+        for (int h = 0; h < kSkParts; h++) {
+            for (int j = wg - 1; j >= j1; j--) {
+                if (T * (j + 1) / P == T * j / P) continue;
+                const __amdgpu_buffer_rsrc_t pr =
+                    buf_rsrc(part + static_cast<size_t>(gp.phys(j)) * (kSlotBytes / 4), kSlotBytes);
+#pragma unroll
+                for (int c = 0; c < PCH / NW; c++) {
+                    const int chunk = wave * (PCH / NW) + c;
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        pr, (lds_ptr)(lds + chunk * 1024), 16, static_cast<uint32_t>(lane) * 16u,
+                        static_cast<uint32_t>((h * PCH + chunk) * 1024), 0, kDevice);
+                }
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+                const float4* hp = reinterpret_cast<const float4*>(lds);
+#pragma unroll
+                for (int b = 0; b < PB; b++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int blk = h * PB + b, i = blk / TN, jj = blk % TN;
+                        const float4 p4 = hp[(b * 4 + q) * NT + tid];
+                        acc[i][jj][4 * q] = __fadd_rn(acc[i][jj][4 * q], p4.x);
+                        acc[i][jj][4 * q + 1] = __fadd_rn(acc[i][jj][4 * q + 1], p4.y);
+                        acc[i][jj][4 * q + 2] = __fadd_rn(acc[i][jj][4 * q + 2], p4.z);
+                        acc[i][jj][4 * q + 3] = __fadd_rn(acc[i][jj][4 * q + 3], p4.w);
+                    }
+                __syncthreads();                               // before the next copies overwrite LDS
+            }
+            w4_store_rows<BM, NW, kSkParts>(acc, out, t, M, N, h, poison, wave, lane);
+        }
+    }
+}
+
+template <int BM, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __restrict__ xb,
+                                                             const uint32_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ sc,
+                                                             const uint16_t* __restrict__ bi, float* __restrict__ out,
+                                                             float* __restrict__ part, unsigned* __restrict__ flags,
+                                                             unsigned* __restrict__ errors, int M, int N, int K,
+                                                             int nx) {
+    static_assert(BM == 256 && NW == 4, "stream-K slots assume 256 x 256 tiles of 4 waves");
+    extern __shared__ uint4 w4_lds[];
+    char* lds = reinterpret_cast<char*>(w4_lds);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = K >> 6;
+    const int tiles = ((M + BM - 1) / BM) * ((N + 255) / 256);
+    SkGroup gp;
+    gp.xcd = blockIdx.x % nx;
+    gp.nx = nx;
+    gp.slot = blockIdx.x / nx;
+    gp.P = gridDim.x / nx;
+    gp.t0 = tiles * gp.xcd / nx;
+    gp.T = static_cast<long>(tiles * (gp.xcd + 1) / nx - gp.t0) * G;
+    const long begin = gp.T * gp.slot / gp.P, end = gp.T * (gp.slot + 1) / gp.P;
+    if (begin >= end) return;
+    W4Src<BM, NW> src;
+    w4_src<BM, NW>(src, K, wave, lane);
+    const long cut = (begin / G + 1) * G;                         // end of the first tile
+    if (end > cut) {
+        w4_sk_segment<BM, NW>(lds, xb, w, sc, bi, out, part, flags, errors, M, N, K, gp, cut, end, src, tid, wave,
+                              lane);
+        w4_sk_segment<BM, NW>(lds, xb, w, sc, bi, out, part, flags, errors, M, N, K, gp, begin, cut, src, tid, wave,
+                              lane);
+    } else {
+        w4_sk_segment<BM, NW>(lds, xb, w, sc, bi, out, part, flags, errors, M, N, K, gp, begin, end, src, tid, wave,
+                              lane);
+    }
 }
 
 template <int BM, int NW>
@@ -230,12 +506,31 @@ int launch_w4(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const ui
     return 0;
 }
 
+template <int BM, int NW>
+int launch_w4_sk(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, float* part,
+                 unsigned* flags, unsigned* errors, int M, int N, int K, int P, int nx, hipStream_t st) {
+    auto kern = gemm_w4_sk_kernel<BM, NW>;
+    const size_t lds = w4_lds_bytes<BM, NW>();
+    static_assert(256 * 256 * 4 / kSkParts <= 3 * w4_stage_bytes(BM), "a part of a slot fits the LDS ring");
+    static std::atomic<uint64_t> lds_raised{0};
+    if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
+    hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, w, s, b, out, part, flags, errors, M, N, K, nx);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q4_EHIP, "prefill gemm (stream-K) launch: %s", hipGetErrorString(e));
+    return 0;
+}
+
 int gemm_w4(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, int M, int N,
             int K, int bm, int S, int kt_split, int nb0, int nblocks, int ldo, hipStream_t st) {
-    // 256-row tiles: 4 waves of 128 x 128 (a dequantised weight word feeds 4
+    // 256-row tiles: 4 waves of 256 x 64 (a dequantised weight word feeds 8
     // MFMAs); 128-row tiles: 8 waves of 64 x 64
     return bm == 256 ? launch_w4<256, 4>(xb, w, s, b, out, M, N, K, S, kt_split, nb0, nblocks, ldo, st)
                      : launch_w4<128, 8>(xb, w, s, b, out, M, N, K, S, kt_split, nb0, nblocks, ldo, st);
+}
+
+int gemm_w4_sk(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, float* part,
+               unsigned* flags, unsigned* errors, int M, int N, int K, int P, int nx, hipStream_t st) {
+    return launch_w4_sk<256, 4>(xb, w, s, b, out, part, flags, errors, M, N, K, P, nx, st);
 }
 
 }  // namespace q4k

@@ -30,8 +30,10 @@
 // Everything is compiled with -ffp-contract=off: the only fused multiply-adds
 // are the explicit fmaf calls that mirror the reference's own contractions.
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <type_traits>
@@ -428,8 +430,8 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
 bool pow2_gs(int gs) { return gs >= 64 && gs <= 2048 && (gs & (gs - 1)) == 0; }
 
 // Per-stream workspace: the x prologue's outputs (byte planes, group sums,
-// scales), the unfused MLP's up rows, and the prefill's bf16 copy of x and
-// split-K partial sums.  Buffers only grow.  A buffer that a call used while
+// scales), the unfused MLP's up rows, and the prefill's bf16 copy of x,
+// partial sums and stream-K flags.  Buffers only grow.  A buffer that a call used while
 // its stream was being captured may be baked into a graph, so when it has to
 // grow later it is retired -- kept allocated until the process ends --
 // instead of freed; a buffer no graph holds is freed once the stream has
@@ -441,13 +443,14 @@ struct Workspace {
     float* xscale = nullptr;
     float* tmp = nullptr;                       // up-projection rows of the unfused MLP
     void* xbf = nullptr;                        // prefill: bf16 copy of x
-    void* part = nullptr;                       // prefill: split-K partial sums
-    size_t cap[6] = {0, 0, 0, 0, 0, 0};         // bytes, in the order above
-    bool in_graph[6] = {false, false, false, false, false, false};
+    void* part = nullptr;                       // prefill: split-K / stream-K partial sums
+    unsigned* sk = nullptr;                     // prefill: stream-K flags, then its error counter
+    size_t cap[7] = {0, 0, 0, 0, 0, 0, 0};      // bytes, in the order above
+    bool in_graph[7] = {false, false, false, false, false, false, false};
     bool fixed = false;
     std::vector<void*> retired;
 };
-enum WsBuf { kWsPlanes, kWsXsum, kWsXscale, kWsTmp, kWsXbf, kWsPart };
+enum WsBuf { kWsPlanes, kWsXsum, kWsXscale, kWsTmp, kWsXbf, kWsPart, kWsSk };
 
 // Make buffer `which` (pointer p) of the workspace hold `bytes`.  Growing is
 // refused while the stream is captured (an allocation cannot be recorded).
@@ -1007,6 +1010,90 @@ int scratch_workspace(Workspace* ws) {
     return 0;
 }
 
+// The prefill GEMM's plan: data-parallel tiles of height bm (256 or 128)
+// with K split S ways (S > 1: partial planes and a sum launch), or, when
+// sk_p > 0, stream-K over sk_p workgroups of 256 x 256 tiles.
+struct PrefillPlan {
+    int bm = 256, S = 1, sk_p = 0, sk_nx = 1;
+};
+
+// XCD groups of a stream-K launch of P workgroups over `tiles` tiles: one per
+// XCD when P spreads evenly over 8 of them and there are tiles for each.
+int sk_groups(int P, long tiles) { return P % 8 == 0 && tiles >= 8 ? 8 : 1; }
+
+bool sk_ok(int P, long tiles, long T, int cus) {
+    const int nx = sk_groups(P, tiles);
+    return P >= 1 && P <= cus && P <= T && P / nx >= (tiles + nx - 1) / nx;
+}
+
+// From a cost model of the kernels measured at M = 512: a K step of a
+// 256 x 256 tile takes about 2.3 us, of a 128 x 256 tile 2.0 us, plus about
+// two steps of pipeline fill per workgroup; data-parallel workgroups run in
+// rounds of one per CU, and split partials cost a write and a read of
+// M x N floats each (about 4.5 TB/s) plus the sum launch.  Stream-K keeps
+// every CU busy, where a step takes about 2.7 us (the clock drops), and a
+// tile's owner adds one 256 KiB partial per range before it in the tile
+// (about 5 us each, serially), plus about 20 us of partial stores, restarts
+// and imbalance: it wins only where each tile has one or two ranges
+// (gate/up of a 512-token prompt: 124 us against 132 us).
+// Q4_GEMM_PLAN="dp:<bm>:<S>" or "sk:<P>" sets the plan instead (for tests
+// and measurement).
+int plan_prefill(int m, int n_out, int n_in, PrefillPlan* out) {
+    const int cus = num_cus();
+    const int G = n_in / 64;
+    const long tiles256 = static_cast<long>((m + 255) / 256) * ((n_out + 255) / 256);
+    const long T = tiles256 * G;
+    auto splits_ok = [&](int S) { return S >= 1 && S <= G && (G + (G + S - 1) / S - 1) / ((G + S - 1) / S) == S; };
+    if (const char* env = getenv("Q4_GEMM_PLAN")) {
+        PrefillPlan p;
+        char tail = 0;
+        if (sscanf(env, "sk:%d%c", &p.sk_p, &tail) == 1) {
+            if (!sk_ok(p.sk_p, tiles256, T, cus))
+                return fail(Q4_EARG, "Q4_GEMM_PLAN=%s: P must lie in [%ld, %ld] here, with P / 8 >= %ld when P is "
+                            "a multiple of 8", env, tiles256, std::min<long>(cus, T), (tiles256 + 7) / 8);
+            p.sk_nx = sk_groups(p.sk_p, tiles256);
+        } else if (sscanf(env, "dp:%d:%d%c", &p.bm, &p.S, &tail) == 2) {
+            if ((p.bm != 256 && p.bm != 128) || !splits_ok(p.S))
+                return fail(Q4_EARG, "Q4_GEMM_PLAN=%s: bm is 128 or 256, and S splits of %d K steps must all be "
+                                     "non-empty", env, G);
+        } else {
+            return fail(Q4_EARG, "Q4_GEMM_PLAN=%s: expected dp:<bm>:<S> or sk:<P>", env);
+        }
+        *out = p;
+        return 0;
+    }
+    PrefillPlan best_plan;
+    double best = 1e30;
+    for (int bm : {256, 128}) {
+        const long tiles = static_cast<long>((m + bm - 1) / bm) * ((n_out + 255) / 256);
+        const double t_step = bm == 256 ? 2.3 : 2.0;
+        for (int S = 1; S <= 16 && G / S >= 2; S++) {
+            if (!splits_ok(S)) continue;
+            const int kts = (G + S - 1) / S;
+            const long rounds = (tiles * S + cus - 1) / cus;
+            const double est = static_cast<double>(rounds) * (kts + 2) * t_step +
+                               (S > 1 ? static_cast<double>(S) * m * n_out * 8.0 / 4.5e6 + 3.0 : 0.0);
+            if (est < best) {
+                best = est;
+                best_plan = PrefillPlan{bm, S, 0};
+            }
+        }
+    }
+    for (int P = 8; P <= cus; P += 8) {
+        if (!sk_ok(P, tiles256, T, cus) || sk_groups(P, tiles256) != 8) continue;
+        const long Tg = (tiles256 + 7) / 8 * G, Pg = P / 8;
+        const long L = (Tg + Pg - 1) / Pg, Lmin = Tg / Pg;
+        const long partials = (G + Lmin - 1) / Lmin - 1;            // per owner, at most
+        const double est = static_cast<double>(L + 4) * 2.7 + static_cast<double>(partials) * 5.0 + 20.0;
+        if (est < best) {
+            best = est;
+            best_plan = PrefillPlan{256, 1, P, 8};
+        }
+    }
+    *out = best_plan;
+    return 0;
+}
+
 }  // namespace
 
 // ================================================================ C-ABI ====
@@ -1363,44 +1450,40 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
         if ((rc = current_device(&dev))) return rc;
         ws = &g_dev[dev].ws[st];
     }
-    // Tile height and split-K from a cost model of the W4 kernel measured at
-    // M = 512: a K step of a 256 x 256 tile takes about 2.3 us, of a
-    // 128 x 256 tile 2.0 us, plus about two steps of pipeline fill per
-    // workgroup; the workgroups run in rounds of one per CU; split partials
-    // cost a write and a read of M x N floats each (about 4.5 TB/s) plus the
-    // sum launch.  Every split keeps at least 2 steps of K.
-    const int cus = num_cus();
-    const int G = n_in / 64;
-    int bm = 256, S = 1;
-    double best = 1e30;
-    for (int cand_bm : {256, 128}) {
-        const long tiles = static_cast<long>((m + cand_bm - 1) / cand_bm) * ((n_out + 255) / 256);
-        const double t_step = cand_bm == 256 ? 2.3 : 2.0;
-        for (int cand_s = 1; cand_s <= 16 && G / cand_s >= 2; cand_s++) {
-            const int kts = (G + cand_s - 1) / cand_s;
-            const int sn = (G + kts - 1) / kts;                   // splits actually used
-            if (sn != cand_s) continue;
-            const long rounds = (tiles * sn + cus - 1) / cus;
-            const double est = static_cast<double>(rounds) * (kts + 2) * t_step +
-                               (sn > 1 ? static_cast<double>(sn) * m * n_out * 8.0 / 4.5e6 + 3.0 : 0.0);
-            if (est < best) {
-                best = est;
-                bm = cand_bm;
-                S = sn;
-            }
-        }
-    }
-    const int kt_split = (G + S - 1) / S;
+    PrefillPlan plan;
+    if ((rc = plan_prefill(m, n_out, n_in, &plan))) return rc;
     const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * n_out;
     if ((rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
-    if (S > 1 && (rc = grow(*ws, ws->part, kWsPart, S * mn * 4, st, "prefill"))) return rc;
+    if (plan.sk_p > 0) {
+        const size_t flag_words = static_cast<size_t>(num_cus()) * 32 + 32;
+        if ((rc = grow(*ws, ws->part, kWsPart, static_cast<size_t>(plan.sk_p) * 256 * 256 * 4, st, "prefill")))
+            return rc;
+        const size_t cap_before = ws->cap[kWsSk];
+        if ((rc = grow(*ws, ws->sk, kWsSk, flag_words * 4, st, "prefill"))) return rc;
+        if (ws->cap[kWsSk] != cap_before) {
+            // flags start at zero once; every launch leaves them at zero
+            const long n = static_cast<long>(ws->cap[kWsSk] / 4);
+            hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st,
+                               reinterpret_cast<float*>(ws->sk), n);
+            HIP_TRY(hipGetLastError());
+        }
+    } else if (plan.S > 1 && (rc = grow(*ws, ws->part, kWsPart, plan.S * mn * 4, st, "prefill"))) {
+        return rc;
+    }
     const long n8 = static_cast<long>(mk / 8);
     hipLaunchKernelGGL(x_to_bf16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, st, x,
                        static_cast<uint4*>(ws->xbf), n8);
     HIP_TRY(hipGetLastError());
     const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
+    if (plan.sk_p > 0) {
+        const size_t words = ws->cap[kWsSk] / 4;
+        return gemm_w4_sk(xb, w, scales, biases, out, static_cast<float*>(ws->part), ws->sk, ws->sk + words - 1, m,
+                          n_out, n_in, plan.sk_p, plan.sk_nx, st);
+    }
+    const int S = plan.S, kt_split = (n_in / 64 + S - 1) / S;
     float* dst = S > 1 ? static_cast<float*>(ws->part) : out;
-    if ((rc = gemm_w4(xb, w, scales, biases, dst, m, n_out, n_in, bm, S, kt_split, 0, (n_out + 255) / 256, n_out, st)))
+    if ((rc = gemm_w4(xb, w, scales, biases, dst, m, n_out, n_in, plan.bm, S, kt_split, 0, (n_out + 255) / 256, n_out,
+                      st)))
         return rc;
     if (S == 1) return 0;
     const long n = static_cast<long>(mn);

@@ -68,3 +68,95 @@ def test_gemm_bf16_dequant_matches_bf16_dequant_kernel():
     deq = q4.dequant_dev(tw, ts, tb, bf16=True).float()
     torch.cuda.synchronize()
     assert torch.equal(got.t().contiguous(), deq)
+
+
+def _plan(monkeypatch, plan):
+    if plan is None:
+        monkeypatch.delenv("Q4_GEMM_PLAN", raising=False)
+    else:
+        monkeypatch.setenv("Q4_GEMM_PLAN", plan)
+
+
+def _operands(seed, m, n_out, n_in):
+    import torch
+    w, s, b = synth.qlinear(seed, n_out, n_in, 64)
+    x = synth.activations(seed + 1, m, n_in)
+    dev = [torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16), x)]
+    exact = bf16_round(x).astype(np.float64) @ bf16_round(oracle.dequant_np(w, s, b, 64)).astype(np.float64).T
+    return dev, exact
+
+
+# Stream-K plans: P workgroups over tiles x G iterations, in 8 XCD groups
+# when P is a multiple of 8 and there are at least 8 tiles (one group
+# otherwise).  P = tiles gives every workgroup one whole tile (no partials);
+# P = tiles + 1 cuts every range across two tiles (a partial and an owner
+# segment each); the largest P gives ranges of one or two K steps, so an
+# owner adds many partials (up to G - 1 of them).  (300, 600, 1024) and
+# (500, 16600, 1024): ragged last tiles in both dimensions; the latter's 130
+# tiles split 16/17 over the groups.  (512, 3584, 18944): 37-step ranges in
+# 296-step tiles, 8 partials per owner.
+@pytest.mark.parametrize("m,n_out,n_in,ps", [(37, 200, 512, (1, 3, 8)),
+                                             (300, 600, 1024, (6, 7, 50, 96)),
+                                             (512, 3584, 3584, (28, 29, 200, 256)),
+                                             (500, 16600, 1024, (136, 256)),
+                                             (512, 3584, 18944, (224,)),
+                                             (512, 18944, 3584, (148, 256))])
+def test_gemm_bf16_stream_k(monkeypatch, m, n_out, n_in, ps):
+    import torch
+    (tw, ts, tb, tx), exact = _operands(720 + m, m, n_out, n_in)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for p in ps:
+        p = min(p, cus)
+        print(f"stream-K m={m} n={n_out} k={n_in} P={p}", flush=True)
+        _plan(monkeypatch, f"sk:{p}")
+        a = q4.gemm_bf16_dev(tw, ts, tb, tx)
+        b2 = q4.gemm_bf16_dev(tw, ts, tb, tx)
+        torch.cuda.synchronize()
+        got = a.cpu().numpy()
+        assert np.isfinite(got).all(), "a tile's partials did not arrive"
+        assert oracle.normwise_rel(got, exact) < EXACT_OPERAND_TOL
+        assert torch.equal(a, b2), "stream-K sums in a fixed order: runs agree bit for bit"
+    _plan(monkeypatch, None)
+
+
+def test_gemm_bf16_stream_k_graph_replays(monkeypatch):
+    """Owners lower the flags they consume, so a captured stream-K launch
+    replays correctly: every replay equals the eager result bit for bit."""
+    import torch
+    m, n_out, n_in = 512, 3584, 3584
+    (tw, ts, tb, tx), exact = _operands(760, m, n_out, n_in)
+    _plan(monkeypatch, "sk:200")
+    eager = q4.gemm_bf16_dev(tw, ts, tb, tx)            # workspace sized before capture
+    torch.cuda.synchronize()
+    out = torch.full_like(eager, float("nan"))
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        q4.gemm_bf16_dev(tw, ts, tb, tx, out=out, stream=s)   # this stream's workspace
+        s.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            q4.gemm_bf16_dev(tw, ts, tb, tx, out=out, stream=s)
+    for r in range(4):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+        q4.gemm_bf16_dev(tw, ts, tb, tx)                # eager work between replays
+    assert oracle.normwise_rel(eager.cpu().numpy(), exact) < EXACT_OPERAND_TOL
+    _plan(monkeypatch, None)
+
+
+@pytest.mark.parametrize("plan", ["sk:0", "sk:100000", "dp:64:1", "dp:256:3", "splitk"])
+def test_gemm_bf16_plan_override_rejected(monkeypatch, plan):
+    """A plan the shape cannot take is an error, not a silent fallback."""
+    import torch
+    (tw, ts, tb, tx), _ = _operands(770, 64, 512, 512)   # one tile of G = 8 K steps
+    _plan(monkeypatch, plan)
+    if plan == "dp:256:3":
+        q4.gemm_bf16_dev(tw, ts, tb, tx)                # splits of 3, 3 and 2 steps: valid
+        torch.cuda.synchronize()
+    else:
+        with pytest.raises(RuntimeError, match="Q4_GEMM_PLAN"):
+            q4.gemm_bf16_dev(tw, ts, tb, tx)
+    _plan(monkeypatch, None)
