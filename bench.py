@@ -889,6 +889,30 @@ def main():
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
     calls_ms = float("nan") if args.sweep_only else timed(step_calls, max(3, args.steps // 2), 1)[0]
 
+    # the same sweep as one chained GEMV program (include/q4chain.h): one
+    # launch, a grid barrier between phases, each phase's first weights
+    # requested before its barrier
+    chained = None
+    if not args.sweep_only:
+        phases = []
+        for q, k, v, o, g, u, d in layers:
+            phases += [([q, k, v], xs[3584], [gouts[3584][0], gouts[512][1], gouts[512][2]], False),
+                       ([o], xs[3584], [outs[3584]], False),
+                       ([g, u], xs[3584], [gouts[18944][0], gouts[18944][1]], False),
+                       ([d], xs[18944], [outs[3584]], False)]
+        phases.append(([head], xs[3584], [outs[152064]], False))
+        chain = q4.Chain(phases, lib=lib)
+
+        def step_chain():
+            chain.run(stream=stream)
+
+        chain_ms = timed(step_chain, args.steps, args.warmup)[0]
+        chain_errors = chain.errors()
+        chain.close()
+        chained = {"ms_per_step": round(chain_ms, 4), "GB_s": round(sweep_bytes / (chain_ms * 1e-3) / 1e9, 1),
+                   "frac_peak": round(sweep_bytes / (chain_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "phases": len(phases), "barrier_timeouts": chain_errors}
+
     if args.calibrate:
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -955,6 +979,7 @@ def main():
         "one_call_per_projection": {"ms_per_step": round(calls_ms, 4),
                                     "GB_s": round(sweep_bytes / (calls_ms * 1e-3) / 1e9, 1),
                                     "launches_per_step": LAYERS * len(LAYER_SHAPES) + 1},
+        "chained": chained,
     }
     if args.sweep_only:
         args.no_prefill = args.no_cpu_baseline = args.no_decode = args.no_small_m = args.no_wire = True
