@@ -124,15 +124,31 @@ class WeightIndex:
     def tied(self) -> bool:
         return bool(self.config.get("tie_word_embeddings", False))
 
-    def owns(self, name: str, spec: ShardSpec) -> bool:
-        """hetero/shard.py:96-105."""
-        if name.startswith("model.layers."):
-            return spec.start <= int(name.split(".")[2]) < spec.end
+    # ---- ownership and byte accounting (hetero/shard.py:96-134) ----
+    # Every tensor falls in one class: a decoder layer's (by layer number),
+    # the embedding table, or the head's (lm_head, final norm).  A stage owns
+    # the layers of its range, the embedding when it is the first stage (or,
+    # with tied weights, the head stage too), and the head's tensors when it
+    # is the last.
+
+    @staticmethod
+    def _tensor_class(name: str) -> Tuple[str, int]:
+        parts = name.split(".")
+        if parts[:2] == ["model", "layers"]:
+            return "layer", int(parts[2])
         if name.startswith("model.embed_tokens"):
-            return spec.embed or (self.tied and spec.head)
+            return "embed", -1
         if name.startswith("lm_head") or name == "model.norm.weight":
-            return spec.head
+            return "head", -1
         raise KeyError(f"unclassified tensor {name}")
+
+    def owns(self, name: str, spec: ShardSpec) -> bool:
+        cls, layer = self._tensor_class(name)
+        if cls == "layer":
+            return layer in range(spec.start, spec.end)
+        if cls == "embed":
+            return spec.embed or (spec.head and self.tied)
+        return spec.head
 
     def names(self) -> List[str]:
         return list(self.entries)
@@ -140,27 +156,29 @@ class WeightIndex:
     def nbytes(self, name: str) -> int:
         return self.entries[name][3]
 
+    def _class_bytes(self, cls: str) -> int:
+        return sum(self.nbytes(n) for n in self.entries if self._tensor_class(n)[0] == cls)
+
     def layer_bytes(self) -> List[int]:
-        n = int(self.config["num_hidden_layers"])
-        out = [0] * n
-        for name, (_, _, _, nb) in self.entries.items():
-            if name.startswith("model.layers."):
-                out[int(name.split(".")[2])] += nb
-        return out
+        per_layer = [0] * int(self.config["num_hidden_layers"])
+        for n in self.entries:
+            cls, layer = self._tensor_class(n)
+            if cls == "layer":
+                per_layer[layer] += self.nbytes(n)
+        return per_layer
 
     def embed_bytes(self) -> int:
-        return sum(nb for n, (_, _, _, nb) in self.entries.items() if n.startswith("model.embed_tokens"))
+        return self._class_bytes("embed")
 
     def head_bytes(self) -> int:
-        b = sum(nb for n, (_, _, _, nb) in self.entries.items()
-                if n.startswith("lm_head") or n == "model.norm.weight")
-        return b + (self.embed_bytes() if self.tied else 0)
+        """The head stage's bytes; with tied weights it also holds the embedding."""
+        return self._class_bytes("head") + (self._class_bytes("embed") if self.tied else 0)
 
     def total_bytes(self) -> int:
-        return sum(nb for _, _, _, nb in self.entries.values())
+        return sum(self.nbytes(n) for n in self.entries)
 
     def shard_bytes(self, spec: ShardSpec) -> int:
-        return sum(nb for n, (_, _, _, nb) in self.entries.items() if self.owns(n, spec))
+        return sum(self.nbytes(n) for n in self.owned(spec))
 
     def owned(self, spec: ShardSpec) -> List[str]:
         return [n for n in self.entries if self.owns(n, spec)]
