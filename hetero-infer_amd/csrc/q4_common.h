@@ -128,19 +128,36 @@ __device__ __forceinline__ uint4 quant_word(const float (&v)[8], float inv, bool
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int num_cus();
 
-// The prefill GEMM (q4_gemm.hip): out (+ z M ldo for split z) = bf16 x .
-// dequant W^T over the N-blocks [nb0, nb0 + nblocks) of 256 columns, tile
-// height bm (256 or 128), S splits of kt_split K steps.
-int gemm_w4(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, int M, int N,
-            int K, int bm, int S, int kt_split, int nb0, int nblocks, int ldo, hipStream_t st);
+// The matrices of one prefill launch (q4_gemm.hip), up to 4 sharing x:
+// matrix k's 256-column blocks are blocks nb0[k] .. nb0[k+1] - 1 of the
+// launch (a block never holds two matrices), its columns are columns
+// col0[k] .. col0[k] + n_out[k] - 1 of the split-K partials.
+struct GemmMats {
+    const uint32_t* w[4];
+    const uint16_t* s[4];
+    const uint16_t* b[4];
+    float* out[4];
+    int n_out[4];
+    int nb0[5];
+    int col0[4];
+    int count;
+};
+
+// The prefill GEMM (q4_gemm.hip), data-parallel: tiles of height bm (256 or
+// 128) over every block of gm, S splits of kt_split K steps.  part null:
+// each matrix's output directly; else split z into part + z M ldp at the
+// matrix's columns.
+int gemm_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K, int bm, int S, int kt_split, int ldp,
+            hipStream_t st);
 
 // Stream-K form of the prefill GEMM: P workgroups in nx XCD groups (256 x
 // 256 tiles; P a multiple of nx, and P / nx at least a group's tile count,
-// ceil(tiles / nx)), out [M][N].  part: P x 256 x 256 floats of partial
-// sums; flags: 32 P words, zero on entry and on return; errors: a counter of
-// partials that did not arrive in time (their tiles are NaN).
-int gemm_w4_sk(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, float* part,
-               unsigned* flags, unsigned* errors, int M, int N, int K, int P, int nx, hipStream_t st);
+// ceil(tiles / nx)), each matrix's output directly.  part: P x 256 x 256
+// floats of partial sums; flags: 32 P words, zero on entry and on return;
+// errors: a counter of partials that did not arrive in time (their tiles
+// are NaN).
+int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* errors, int M, int K,
+               int P, int nx, hipStream_t st);
 
 // Dynamic LDS above 64 KiB needs the kernel's limit raised on each device
 // that runs it.  `done` holds one bit per device already raised (0..63; a

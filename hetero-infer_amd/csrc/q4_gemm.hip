@@ -279,13 +279,21 @@ __device__ __forceinline__ void w4_zero(W4Acc<BM, NW>& acc) {
             for (int v = 0; v < 16; v++) acc[i][j][v] = 0.0f;
 }
 
-// Data-parallel: workgroup (mt, nt - nb0, z) computes K steps
-// [z kt_split, (z+1) kt_split) of tile (mt, nt) into out + z M ldo.
+// The matrix of launch block nt (uniform).
+__device__ __forceinline__ int gm_mat(const GemmMats& gm, int nt) {
+    int k = 0;
+#pragma unroll
+    for (int i = 1; i < 4; i++) k += (i < gm.count && nt >= gm.nb0[i]) ? 1 : 0;
+    return __builtin_amdgcn_readfirstlane(k);
+}
+
+// Data-parallel: workgroup (mt, nt, z) computes K steps [z kt_split,
+// (z+1) kt_split) of tile (mt, nt): into its matrix's output, or (part)
+// into part + z M ldp at the matrix's columns.
 template <int BM, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __restrict__ xb, const uint32_t* __restrict__ w,
-                                                          const uint16_t* __restrict__ sc,
-                                                          const uint16_t* __restrict__ bi, float* __restrict__ out,
-                                                          int M, int N, int K, int kt_split, int nb0, int ldo) {
+__global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __restrict__ xb, GemmMats gm,
+                                                          float* __restrict__ part, int M, int K, int kt_split,
+                                                          int ldp) {
     extern __shared__ uint4 w4_lds[];
     char* lds = reinterpret_cast<char*>(w4_lds);
     const int lane = threadIdx.x & 63;
@@ -293,13 +301,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
     const int G = K >> 6;
     const int kt0 = blockIdx.z * kt_split;
     const int nk = G - kt0 < kt_split ? G - kt0 : kt_split;
-    const W4Tile t = w4_tile<BM>(xb, w, sc, bi, M, N, K, blockIdx.x, blockIdx.y + nb0);
+    const int k = gm_mat(gm, blockIdx.y);
+    const int N = gm.n_out[k];
+    const W4Tile t = w4_tile<BM>(xb, gm.w[k], gm.s[k], gm.b[k], M, N, K, blockIdx.x, blockIdx.y - gm.nb0[k]);
     W4Src<BM, NW> src;
     w4_src<BM, NW>(src, K, wave, lane);
     W4Acc<BM, NW> acc;
     w4_zero<BM, NW>(acc);
     w4_segment<BM, NW>(acc, lds, t, src, kt0, nk, wave, lane);
-    w4_store<BM, NW>(acc, out + static_cast<size_t>(blockIdx.z) * M * ldo, t, M, N, ldo, nb0 * 256, wave, lane);
+    if (part)
+        w4_store<BM, NW>(acc, part + static_cast<size_t>(blockIdx.z) * M * ldp + gm.col0[k], t, M, N, ldp, 0, wave,
+                         lane);
+    else
+        w4_store<BM, NW>(acc, gm.out[k], t, M, N, N, 0, wave, lane);
 }
 
 // Stream-K: the tiles (m block major) are split into nx contiguous groups,
@@ -341,17 +355,17 @@ struct SkGroup {
 
 // Segment [it, stop) of a stream-K range (stop at most its tile's end).
 template <int BM, int NW>
-__device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, const uint32_t* w, const uint16_t* sc,
-                                              const uint16_t* bi, float* out, float* part, unsigned* flags,
-                                              unsigned* errors, int M, int N, int K, const SkGroup& gp, long it,
-                                              long stop, const W4Src<BM, NW>& src, int tid, int wave, int lane) {
+__device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, const GemmMats& gm, float* part,
+                                              unsigned* flags, unsigned* errors, int M, int K, const SkGroup& gp,
+                                              long it, long stop, const W4Src<BM, NW>& src, int tid, int wave,
+                                              int lane) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
     constexpr int TM = W4Layout<BM, NW>::TM, TN = W4Layout<BM, NW>::TN, NB = TM * TN;
     constexpr int NT = 64 * NW;
     constexpr int kDevice = 16;                                    // sc1: device-coherent
     constexpr uint32_t kSlotBytes = 256u * 256u * 4u;
     using u32x4 = unsigned int __attribute__((__vector_size__(16)));
-    const int G = K >> 6, NTL = (N + 255) / 256;
+    const int G = K >> 6, NTL = gm.nb0[gm.count];
     const long T = gp.T;
     const int P = gp.P, wg = gp.slot;
     W4Acc<BM, NW> acc;
@@ -359,7 +373,10 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
     const int nk = static_cast<int>(stop - it);
     const long tile_start = it - k0;                               // in the group's iterations
     const int tile = gp.t0 + static_cast<int>(it / G);
-    const W4Tile t = w4_tile<BM>(xb, w, sc, bi, M, N, K, tile / NTL, tile % NTL);
+    const int nt = tile % NTL, mk = gm_mat(gm, nt);
+    const int N = gm.n_out[mk];
+    float* const out = gm.out[mk];
+    const W4Tile t = w4_tile<BM>(xb, gm.w[mk], gm.s[mk], gm.b[mk], M, N, K, tile / NTL, nt - gm.nb0[mk]);
     w4_zero<BM, NW>(acc);
     w4_segment<BM, NW>(acc, lds, t, src, k0, nk, wave, lane);
     if (stop < tile_start + G) {
@@ -450,20 +467,16 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
 }
 
 template <int BM, int NW>
-__global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __restrict__ xb,
-                                                             const uint32_t* __restrict__ w,
-                                                             const uint16_t* __restrict__ sc,
-                                                             const uint16_t* __restrict__ bi, float* __restrict__ out,
+__global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __restrict__ xb, GemmMats gm,
                                                              float* __restrict__ part, unsigned* __restrict__ flags,
-                                                             unsigned* __restrict__ errors, int M, int N, int K,
-                                                             int nx) {
+                                                             unsigned* __restrict__ errors, int M, int K, int nx) {
     static_assert(BM == 256 && NW == 4, "stream-K slots assume 256 x 256 tiles of 4 waves");
     extern __shared__ uint4 w4_lds[];
     char* lds = reinterpret_cast<char*>(w4_lds);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = K >> 6;
-    const int tiles = ((M + BM - 1) / BM) * ((N + 255) / 256);
+    const int tiles = ((M + BM - 1) / BM) * gm.nb0[gm.count];
     SkGroup gp;
     gp.xcd = blockIdx.x % nx;
     gp.nx = nx;
@@ -477,13 +490,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __r
     w4_src<BM, NW>(src, K, wave, lane);
     const long cut = (begin / G + 1) * G;                         // end of the first tile
     if (end > cut) {
-        w4_sk_segment<BM, NW>(lds, xb, w, sc, bi, out, part, flags, errors, M, N, K, gp, cut, end, src, tid, wave,
-                              lane);
-        w4_sk_segment<BM, NW>(lds, xb, w, sc, bi, out, part, flags, errors, M, N, K, gp, begin, cut, src, tid, wave,
-                              lane);
+        w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, M, K, gp, cut, end, src, tid, wave, lane);
+        w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, M, K, gp, begin, cut, src, tid, wave, lane);
     } else {
-        w4_sk_segment<BM, NW>(lds, xb, w, sc, bi, out, part, flags, errors, M, N, K, gp, begin, end, src, tid, wave,
-                              lane);
+        w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, M, K, gp, begin, end, src, tid, wave, lane);
     }
 }
 
@@ -493,44 +503,44 @@ size_t w4_lds_bytes() {
 }
 
 template <int BM, int NW>
-int launch_w4(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, int M, int N,
-              int K, int S, int kt_split, int nb0, int nblocks, int ldo, hipStream_t st) {
+int launch_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K, int S, int kt_split, int ldp,
+              hipStream_t st) {
     auto kern = gemm_w4_kernel<BM, NW>;
     const size_t lds = w4_lds_bytes<BM, NW>();
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
-    hipLaunchKernelGGL(kern, dim3((M + BM - 1) / BM, nblocks, S), dim3(64 * NW), lds, st, xb, w, s, b, out, M, N, K,
-                       kt_split, nb0, ldo);
+    hipLaunchKernelGGL(kern, dim3((M + BM - 1) / BM, gm.nb0[gm.count], S), dim3(64 * NW), lds, st, xb, gm, part, M, K,
+                       kt_split, ldp);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "prefill gemm launch: %s", hipGetErrorString(e));
     return 0;
 }
 
 template <int BM, int NW>
-int launch_w4_sk(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, float* part,
-                 unsigned* flags, unsigned* errors, int M, int N, int K, int P, int nx, hipStream_t st) {
+int launch_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* errors, int M, int K,
+                 int P, int nx, hipStream_t st) {
     auto kern = gemm_w4_sk_kernel<BM, NW>;
     const size_t lds = w4_lds_bytes<BM, NW>();
     static_assert(256 * 256 * 4 / kSkParts <= 3 * w4_stage_bytes(BM), "a part of a slot fits the LDS ring");
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
-    hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, w, s, b, out, part, flags, errors, M, N, K, nx);
+    hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, gm, part, flags, errors, M, K, nx);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "prefill gemm (stream-K) launch: %s", hipGetErrorString(e));
     return 0;
 }
 
-int gemm_w4(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, int M, int N,
-            int K, int bm, int S, int kt_split, int nb0, int nblocks, int ldo, hipStream_t st) {
+int gemm_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K, int bm, int S, int kt_split, int ldp,
+            hipStream_t st) {
     // 256-row tiles: 4 waves of 256 x 64 (a dequantised weight word feeds 8
     // MFMAs); 128-row tiles: 8 waves of 64 x 64
-    return bm == 256 ? launch_w4<256, 4>(xb, w, s, b, out, M, N, K, S, kt_split, nb0, nblocks, ldo, st)
-                     : launch_w4<128, 8>(xb, w, s, b, out, M, N, K, S, kt_split, nb0, nblocks, ldo, st);
+    return bm == 256 ? launch_w4<256, 4>(xb, gm, part, M, K, S, kt_split, ldp, st)
+                     : launch_w4<128, 8>(xb, gm, part, M, K, S, kt_split, ldp, st);
 }
 
-int gemm_w4_sk(const uint16_t* xb, const uint32_t* w, const uint16_t* s, const uint16_t* b, float* out, float* part,
-               unsigned* flags, unsigned* errors, int M, int N, int K, int P, int nx, hipStream_t st) {
-    return launch_w4_sk<256, 4>(xb, w, s, b, out, part, flags, errors, M, N, K, P, nx, st);
+int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* errors, int M, int K,
+               int P, int nx, hipStream_t st) {
+    return launch_w4_sk<256, 4>(xb, gm, part, flags, errors, M, K, P, nx, st);
 }
 
 }  // namespace q4k

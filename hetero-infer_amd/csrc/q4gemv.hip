@@ -402,17 +402,21 @@ __global__ __launch_bounds__(256) void x_to_bf16_kernel(const float* __restrict_
     }
 }
 
-// out[r][c0 + c] = sum over the S split-K partials part[s][r][c] (r < M,
-// c < W), in split order; out has row stride ldo.
-__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ part, float* __restrict__ out,
-                                                         int M, int W, int ldo, int c0, int S) {
+// The S split-K partials part[s][r][c] (r < M, c < W: the matrices' columns
+// side by side) summed in split order into the output of column c's
+// matrix.
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ part, GemmMats gm, int M, int W,
+                                                         int S) {
     const long n = static_cast<long>(M) * W;
     const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
     if (i < n) {
         float a = part[i];
         for (int s = 1; s < S; s++) a = __fadd_rn(a, part[static_cast<long>(s) * n + i]);
         const long r = i / W;
-        out[r * ldo + c0 + (i - r * W)] = a;
+        const int c = static_cast<int>(i - r * W);
+        int k = 0;
+        for (int j = 1; j < gm.count; j++) k += c >= gm.col0[j] ? 1 : 0;
+        gm.out[k][r * gm.n_out[k] + (c - gm.col0[k])] = a;
     }
 }
 
@@ -1038,10 +1042,11 @@ bool sk_ok(int P, long tiles, long T, int cus) {
 // (gate/up of a 512-token prompt: 124 us against 132 us).
 // Q4_GEMM_PLAN="dp:<bm>:<S>" or "sk:<P>" sets the plan instead (for tests
 // and measurement).
-int plan_prefill(int m, int n_out, int n_in, PrefillPlan* out) {
+// nblocks: 256-column blocks of the launch; ncols: its columns.
+int plan_prefill(int m, int nblocks, int ncols, int n_in, PrefillPlan* out) {
     const int cus = num_cus();
     const int G = n_in / 64;
-    const long tiles256 = static_cast<long>((m + 255) / 256) * ((n_out + 255) / 256);
+    const long tiles256 = static_cast<long>((m + 255) / 256) * nblocks;
     const long T = tiles256 * G;
     auto splits_ok = [&](int S) { return S >= 1 && S <= G && (G + (G + S - 1) / S - 1) / ((G + S - 1) / S) == S; };
     if (const char* env = getenv("Q4_GEMM_PLAN")) {
@@ -1065,14 +1070,14 @@ int plan_prefill(int m, int n_out, int n_in, PrefillPlan* out) {
     PrefillPlan best_plan;
     double best = 1e30;
     for (int bm : {256, 128}) {
-        const long tiles = static_cast<long>((m + bm - 1) / bm) * ((n_out + 255) / 256);
+        const long tiles = static_cast<long>((m + bm - 1) / bm) * nblocks;
         const double t_step = bm == 256 ? 2.3 : 2.0;
         for (int S = 1; S <= 16 && G / S >= 2; S++) {
             if (!splits_ok(S)) continue;
             const int kts = (G + S - 1) / S;
             const long rounds = (tiles * S + cus - 1) / cus;
             const double est = static_cast<double>(rounds) * (kts + 2) * t_step +
-                               (S > 1 ? static_cast<double>(S) * m * n_out * 8.0 / 4.5e6 + 3.0 : 0.0);
+                               (S > 1 ? static_cast<double>(S) * m * ncols * 8.0 / 4.5e6 + 3.0 : 0.0);
             if (est < best) {
                 best = est;
                 best_plan = PrefillPlan{bm, S, 0};
@@ -1426,21 +1431,45 @@ int q4_mlp_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* g
 }
 
 
-int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
-                     const float* x, float* out, int m, int n_out, int n_in, int gs, void* stream) {
-    int rc = check_gemv_shape(n_out, n_in, gs);
-    if (rc) return rc;
-    if (gs != 64) return fail(Q4_EARG, "q4_gemm_bf16_dev takes gs = 64 (got %d)", gs);
+int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* const* scales,
+                           const uint16_t* const* biases, float* const* out, const int* n_out, const float* x,
+                           int m, int n_in, int gs, void* stream) {
+    if (count < 1 || count > 4) return fail(Q4_EARG, "count=%d (1..4)", count);
+    if (!w || !scales || !biases || !out || !n_out) return fail(Q4_EARG, "null array");
+    int rc;
+    for (int k = 0; k < count; k++)
+        if ((rc = check_gemv_shape(n_out[k], n_in, gs))) return rc;
+    if (gs != 64) return fail(Q4_EARG, "the prefill GEMM takes gs = 64 (got %d)", gs);
     if (m < 0) return fail(Q4_EARG, "m=%d", m);
-    if (m == 0 || n_out == 0) return 0;
-    if (!w || !scales || !biases || !x || !out) return fail(Q4_EARG, "null pointer");
-    if ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15)
-        return fail(Q4_EARG, "w and x must be 16-byte aligned");
+    GemmMats gm{};
+    int ncols = 0, nblocks = 0;
+    for (int k = 0; k < count; k++) {
+        if (n_out[k] == 0) continue;                          // a matrix of no rows takes no block
+        gm.w[gm.count] = w[k];
+        gm.s[gm.count] = scales[k];
+        gm.b[gm.count] = biases[k];
+        gm.out[gm.count] = out[k];
+        gm.n_out[gm.count] = n_out[k];
+        gm.nb0[gm.count] = nblocks;
+        gm.col0[gm.count] = ncols;
+        nblocks += (n_out[k] + 255) / 256;
+        ncols += n_out[k];
+        ++gm.count;
+    }
+    gm.nb0[gm.count] = nblocks;
+    if (m == 0 || gm.count == 0) return 0;
+    for (int k = 0; k < gm.count; k++) {
+        if (!gm.w[k] || !gm.s[k] || !gm.b[k] || !gm.out[k]) return fail(Q4_EARG, "null pointer");
+        if (reinterpret_cast<uintptr_t>(gm.w[k]) & 15) return fail(Q4_EARG, "w and x must be 16-byte aligned");
+    }
+    if (!x || (reinterpret_cast<uintptr_t>(x) & 15)) return fail(Q4_EARG, "w and x must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (n_in == 0) {
-        const long n = static_cast<long>(m) * n_out;
-        hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st, out, n);
-        HIP_TRY(hipGetLastError());
+        for (int k = 0; k < gm.count; k++) {
+            const long n = static_cast<long>(m) * gm.n_out[k];
+            hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st, gm.out[k], n);
+            HIP_TRY(hipGetLastError());
+        }
         return 0;
     }
     Workspace* ws;
@@ -1451,8 +1480,8 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
         ws = &g_dev[dev].ws[st];
     }
     PrefillPlan plan;
-    if ((rc = plan_prefill(m, n_out, n_in, &plan))) return rc;
-    const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * n_out;
+    if ((rc = plan_prefill(m, nblocks, ncols, n_in, &plan))) return rc;
+    const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * ncols;
     if ((rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
     if (plan.sk_p > 0) {
         const size_t flag_words = static_cast<size_t>(num_cus()) * 32 + 32;
@@ -1477,20 +1506,23 @@ int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* 
     const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
     if (plan.sk_p > 0) {
         const size_t words = ws->cap[kWsSk] / 4;
-        return gemm_w4_sk(xb, w, scales, biases, out, static_cast<float*>(ws->part), ws->sk, ws->sk + words - 1, m,
-                          n_out, n_in, plan.sk_p, plan.sk_nx, st);
+        return gemm_w4_sk(xb, gm, static_cast<float*>(ws->part), ws->sk, ws->sk + words - 1, m, n_in, plan.sk_p,
+                          plan.sk_nx, st);
     }
     const int S = plan.S, kt_split = (n_in / 64 + S - 1) / S;
-    float* dst = S > 1 ? static_cast<float*>(ws->part) : out;
-    if ((rc = gemm_w4(xb, w, scales, biases, dst, m, n_out, n_in, plan.bm, S, kt_split, 0, (n_out + 255) / 256, n_out,
-                      st)))
-        return rc;
+    float* part = S > 1 ? static_cast<float*>(ws->part) : nullptr;
+    if ((rc = gemm_w4(xb, gm, part, m, n_in, plan.bm, S, kt_split, ncols, st))) return rc;
     if (S == 1) return 0;
     const long n = static_cast<long>(mn);
     hipLaunchKernelGGL(splitk_sum_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, st,
-                       static_cast<const float*>(ws->part), out, m, n_out, n_out, 0, S);
+                       static_cast<const float*>(ws->part), gm, m, ncols, S);
     HIP_TRY(hipGetLastError());
     return 0;
+}
+
+int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                     const float* x, float* out, int m, int n_out, int n_in, int gs, void* stream) {
+    return q4_gemm_bf16_multi_dev(1, &w, &scales, &biases, &out, &n_out, x, m, n_in, gs, stream);
 }
 
 int q4_dequant_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* out,

@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
 
 EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
            "q4_last_error", "q4_gemv_dev", "q4_gemv_noalloc_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
-           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_dequant_dev", "q4_dequant_bf16_dev",
+           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_gemm_bf16_multi_dev", "q4_dequant_dev", "q4_dequant_bf16_dev",
            # decode-step kernels (include/q4decode.h)
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
            "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev",
@@ -63,6 +63,8 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_mlp_dev.restype = _I
         lib.q4_gemm_bf16_dev.argtypes = [_VP] * 5 + [_I] * 4 + [_VP]
         lib.q4_gemm_bf16_dev.restype = _I
+        lib.q4_gemm_bf16_multi_dev.argtypes = [_I] + [_VP] * 6 + [_I] * 3 + [_VP]
+        lib.q4_gemm_bf16_multi_dev.restype = _I
         lib.q4_dequant_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
         lib.q4_dequant_dev.restype = _I
         lib.q4_dequant_bf16_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
@@ -278,6 +280,26 @@ def gemm_bf16_dev(w, scales, biases, x, out=None, stream=None, lib=None):
                               x2.shape[0], n_out, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gemm_bf16_dev")
     return out
+
+
+def gemm_bf16_multi_dev(mats, x, outs=None, stream=None, lib=None):
+    """Prefill for several (w, scales, biases) sharing x in one launch; returns the outputs."""
+    import torch
+    lib = lib or load()
+    n_in = mats[0][0].shape[1] * 8
+    gs = n_in // mats[0][1].shape[1]
+    x2 = x.reshape(-1, n_in)
+    m = x2.shape[0]
+    if outs is None:
+        outs = [torch.empty((m, w.shape[0]), dtype=torch.float32, device=x.device) for w, _, _ in mats]
+    k = len(mats)
+    arr = lambda vals: (ctypes.c_void_p * k)(*vals)
+    rc = lib.q4_gemm_bf16_multi_dev(k, arr([_ptr(a[0]) for a in mats]), arr([_ptr(a[1]) for a in mats]),
+                                    arr([_ptr(a[2]) for a in mats]), arr([_ptr(o) for o in outs]),
+                                    (ctypes.c_int * k)(*[a[0].shape[0] for a in mats]),
+                                    _ptr(x2), m, n_in, gs, _stream(stream))
+    check(lib, rc, "q4_gemm_bf16_multi_dev")
+    return outs
 
 
 def dequant_dev(w, scales, biases, row0=0, row1=None, out=None, bf16=False, stream=None, lib=None):

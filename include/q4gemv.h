@@ -148,6 +148,19 @@ int q4_gemm_bf16_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *
                      const float *x, float *out, int m, int n_out, int n_in, int gs,
                      void *stream);
 
+/* Up to four prefill contractions that share x (q/k/v, gate/up) in one
+ * launch: out[k] is [m][n_out[k]] = x . W_k^T, each as q4_gemm_bf16_dev
+ * computes it (the tiling may differ, so the fp32 sums may differ from a
+ * separate call's in the last place).  x is rounded to bf16 once, and the
+ * matrices' 256-column tile blocks share one tile space, so small matrices
+ * fill the CUs together.  w, scales, biases, out and n_out are host arrays
+ * of `count` device pointers / sizes.  No counterpart in the reference,
+ * whose caller makes one QLinear._gemm call per projection
+ * (hetero/cpu_model.py:119-136, :269-275, :291-292). */
+int q4_gemm_bf16_multi_dev(int count, const uint32_t *const *w, const uint16_t *const *scales,
+                           const uint16_t *const *biases, float *const *out, const int *n_out,
+                           const float *x, int m, int n_in, int gs, void *stream);
+
 /* Device q4_dequant: rows [row0,row1) to fp32 [row1-row0][n_in]. */
 int q4_dequant_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
                    float *out, int row0, int row1, int n_in, int gs, void *stream);

@@ -183,3 +183,27 @@ def test_chain_argument_errors(lib):
     assert lib.q4_chain_create(None, 1, ctypes.byref(ctypes.c_void_p())) == q4.Q4_EARG
     assert lib.q4_chain_run(None, None) == q4.Q4_EARG
     assert lib.q4_chain_destroy(None) == 0
+
+
+def test_gemm_multi_argument_errors(lib):
+    """q4_gemm_bf16_multi_dev checks its arguments before any device call:
+    count, group size, shapes; a call with no rows or no columns is a no-op."""
+    fake = 1 << 20                                       # 16-byte aligned, never dereferenced
+    vp = ctypes.c_void_p
+
+    def call(count, n_out, n_in=256, gs=64, m=4, x=fake, w=fake):
+        k = max(count, 1)
+        arr = lambda v: (vp * k)(*([v] * k))
+        return lib.q4_gemm_bf16_multi_dev(count, arr(w), arr(fake), arr(fake), arr(fake),
+                                          (ctypes.c_int * k)(*([n_out] * k)), x, m, n_in, gs, None)
+
+    assert call(0, 8) == q4.Q4_EARG
+    assert call(5, 8) == q4.Q4_EARG
+    assert call(2, 8, gs=128) == q4.Q4_EARG                 # the prefill GEMM takes gs 64
+    assert call(2, 8, n_in=100) != 0                          # n_in not a multiple of gs: the shape code
+    assert call(2, -1) != 0
+    assert call(2, 8, m=-1) == q4.Q4_EARG
+    assert call(2, 8, m=0, x=None) == 0                       # nothing to compute
+    assert call(2, 0, x=None) == 0
+    assert call(2, 8, x=fake + 4) == q4.Q4_EARG               # misaligned x
+    assert call(2, 8, w=fake + 8) == q4.Q4_EARG               # misaligned weights

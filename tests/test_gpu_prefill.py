@@ -160,3 +160,41 @@ def test_gemm_bf16_plan_override_rejected(monkeypatch, plan):
         with pytest.raises(RuntimeError, match="Q4_GEMM_PLAN"):
             q4.gemm_bf16_dev(tw, ts, tb, tx)
     _plan(monkeypatch, None)
+
+
+# Several matrices sharing x in one launch: q/k/v and gate/up of the Qwen
+# shapes at M=512, and a ragged set -- 300 rows (a partial block), a matrix
+# of no rows and 700 rows -- at M=200, under the default plan and forced
+# data-parallel, split-K and stream-K plans.  Each output against its own
+# exact-operand product; two runs agree bit for bit.
+@pytest.mark.parametrize("m,n_in,n_outs,plans", [
+    (512, 3584, (3584, 512, 512), (None, "dp:128:4", "sk:40")),
+    (512, 3584, (18944, 18944), (None, "dp:256:1")),
+    (200, 1024, (300, 0, 700), (None, "dp:256:3", "sk:8", "sk:5")),
+])
+def test_gemm_bf16_multi(monkeypatch, m, n_in, n_outs, plans):
+    import torch
+    mats, exacts = [], []
+    x = synth.activations(780 + m, m, n_in)
+    xr = bf16_round(x).astype(np.float64)
+    for i, n in enumerate(n_outs):
+        w, s, b = synth.qlinear(781 + i + n, max(n, 1), n_in, 64)
+        w, s, b = w[:n], s[:n], b[:n]
+        mats.append(tuple(torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (w, s.view(np.int16), b.view(np.int16))))
+        exacts.append(xr @ bf16_round(oracle.dequant_np(w, s, b, 64)).astype(np.float64).T if n else None)
+    tx = torch.from_numpy(x).cuda()
+    for plan in plans:
+        print(f"multi m={m} k={n_in} n={n_outs} plan={plan}", flush=True)
+        _plan(monkeypatch, plan)
+        a = q4.gemm_bf16_multi_dev(mats, tx)
+        b2 = q4.gemm_bf16_multi_dev(mats, tx)
+        torch.cuda.synchronize()
+        for n, got, again, exact in zip(n_outs, a, b2, exacts):
+            assert got.shape == (m, n)
+            if n == 0:
+                continue
+            g = got.cpu().numpy()
+            assert np.isfinite(g).all()
+            assert oracle.normwise_rel(g, exact) < EXACT_OPERAND_TOL, (plan, n)
+            assert torch.equal(got, again), (plan, n)
+    _plan(monkeypatch, None)
