@@ -160,11 +160,15 @@ def group128_bench(torch, lib, dev, reps=5):
 
 def prefill_bench(torch, lib, layers, dev, reps=3):
     """M=512 prompt over the 28 layers' projections: bf16 MFMA GEMM with the
-    dequant fused into the weight-tile load (q4_gemm_bf16_dev)."""
+    dequant fused into the weight-tile load.  Two launch patterns over the
+    same work: one q4_gemm_bf16_dev per projection, and the grouped form
+    (q4_gemm_bf16_multi_dev over [q, k, v] and over [gate, up], which share
+    their input, then o_proj and down_proj alone)."""
     from hetero import q4
     m = 512
     xs = {k: torch.randn((m, k), device=dev) for k in (3584, 18944)}
     outs = {n: torch.empty((m, n), device=dev) for n in (512, 3584, 18944)}
+    gouts = [torch.empty((m, n), device=dev) for n in (3584, 512, 512, 18944, 18944)]
     # the weights and x come from the default stream; the GEMMs run on a
     # non-blocking one
     torch.cuda.synchronize()
@@ -180,26 +184,38 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
                 if rc != 0:
                     raise RuntimeError(f"q4_gemm_bf16_dev rc={rc}: {q4.last_error(lib)}")
 
+    def step_grouped():
+        for layer in layers:
+            q4.gemm_bf16_multi_dev(layer[0:3], xs[3584], outs=gouts[0:3], stream=stream, lib=lib)
+            q4.gemm_bf16_dev(*layer[3], xs[3584], out=outs[3584], stream=stream, lib=lib)
+            q4.gemm_bf16_multi_dev(layer[4:6], xs[3584], outs=gouts[3:5], stream=stream, lib=lib)
+            q4.gemm_bf16_dev(*layer[6], xs[18944], out=outs[3584], stream=stream, lib=lib)
+
+    def timed(fn):
+        with torch.cuda.stream(stream):
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+        with torch.cuda.stream(stream):
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
     for layer in layers:
         for w, _, _ in layer:
             flops += 2 * m * w.shape[0] * w.shape[1] * 8
-    with torch.cuda.stream(stream):
-        step()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
-        step()
-    with torch.cuda.stream(stream):
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            g.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+    ms = timed(step)
+    ms_grouped = timed(step_grouped)
     tf = flops / (ms * 1e-3) / 1e12
+    tf_grouped = flops / (ms_grouped * 1e-3) / 1e12
     # error vs the reference contraction, fp32 dequant-matmul (hetero/cpu_model.py:119-136), on
     # each projection shape of layer 0: max |err| / max |ref| and norm-wise
     errs = {}
@@ -216,6 +232,9 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
     return {"workload": "M=512 prompt, 28 layers x 7 projections (K/N of the decode sweep), "
                         "group-64 dequant to bf16 fused into the weight-tile load, MFMA GEMM",
             "ms": round(ms, 3), "tflops": round(tf, 1), "frac_mfma_peak": round(tf / 2500.0, 4),
+            "grouped": {"ms": round(ms_grouped, 3), "tflops": round(tf_grouped, 1),
+                        "frac_mfma_peak": round(tf_grouped / 2500.0, 4),
+                        "launches_per_layer": 4},
             "peak_tflops_bf16_dense": 2500.0, "flops": flops,
             "max_rel_err_vs_fp32_dequant_matmul": round(worst, 6),
             "err_per_shape": {k: {kk: round(vv, 7) for kk, vv in v.items()} for k, v in errs.items()}}
