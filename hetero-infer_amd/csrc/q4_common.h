@@ -124,6 +124,35 @@ __device__ __forceinline__ uint4 quant_word(const float (&v)[8], float inv, bool
     return make_uint4(le, lo, he, ho);
 }
 
+// NumPy's argmax order (hetero/backends.py:106-109, z.argmax()): NaN counts
+// as the largest value, so the first NaN wins; otherwise the largest value,
+// the first index of it on ties.  (v, i) replaces (bv, bi) when it comes
+// first in that order -- a total order, so any reduction tree gives the
+// same result.
+__device__ __forceinline__ void argmax_better(float& bv, int& bi, float v, int i) {
+    const bool vn = v != v, bn = bv != bv;
+    const bool take = vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)));
+    if (take) { bv = v; bi = i; }
+}
+constexpr int kArgmaxNone = 0x7FFFFFFF;   // the index of "no value yet"
+constexpr int kGreedyMaxParts = 4096;     // workgroups of a launch that takes the greedy token
+
+// The greedy token of a one-matrix, one-row GEMV, taken in the GEMV's own
+// launch: each workgroup reduces the rows it stored to (value, index) in
+// part[blockIdx.x] and counts itself in *count; the last to arrive reduces
+// the parts and does the decode step's bookkeeping (*tok = the index,
+// hist[*pos - s0] = *tok when in [0, hist_len), *pos += 1) and sets *count
+// back to 0.  part null: no greedy token.
+struct GreedyArgs {
+    float2* part;
+    unsigned* count;
+    int64_t* tok;
+    int64_t* hist;
+    int64_t* pos;
+    int64_t s0;
+    int hist_len;
+};
+
 // host side, defined in q4gemv.hip
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int num_cus();

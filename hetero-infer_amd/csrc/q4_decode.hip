@@ -518,12 +518,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const float* __restri
 // step's bookkeeping.
 constexpr int kArgmaxParts = 256;
 
-// (v, i) replaces (bv, bi) when it comes first in NumPy's order
-__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
-    const bool vn = v != v, bn = bv != bv;
-    const bool take = vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)));
-    if (take) { bv = v; bi = i; }
-}
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) { argmax_better(bv, bi, v, i); }
 
 // wave and workgroup reduction of (value, index); the result in thread 0
 __device__ __forceinline__ void argmax_reduce(float& bv, int& bi, float* rv, int* ri) {

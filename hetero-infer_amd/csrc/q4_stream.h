@@ -58,6 +58,7 @@ struct NormArgs {
     const float* w;
     float* x_out;
     float eps;
+    GreedyArgs greedy;   // one matrix, one row, no pair: the greedy token of the outputs
 };
 
 // Row stride of the per-wave term table, which holds one chunk's group
@@ -275,6 +276,65 @@ __host__ __device__ constexpr int stream_waves_per_cu() { return MR >= 8 ? 8 : 1
 // packed words, 2 << GSH lanes of an item.
 // Host guarantees: chunks * 256 <= RW * blockDim.x, n_in % (64 << GSH) == 0,
 // x 16-byte aligned.
+// The greedy token's end of a launch (GreedyArgs): (bv, bi) is the lane's
+// best stored row.  The wave's and then the workgroup's best go to
+// g.part[blockIdx.x] through a device-coherent store; once the store is
+// complete the workgroup counts itself, and the one that finds every other
+// workgroup counted reduces the parts.  rv / ri: nwaves free LDS words each.
+// Every thread of the workgroup calls it.
+__device__ __forceinline__ void greedy_tail(float bv, int bi, const GreedyArgs& g, float* rv, int* ri, int lane,
+                                            int wave, int nwaves) {
+    constexpr int kCoherent = 16;                                 // cache policy sc1: device scope
+    auto wave_best = [&](float& v, int& i) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(v, o);
+            const int oi = __shfl_xor(i, o);
+            argmax_better(v, i, ov, oi);
+        }
+    };
+    wave_best(bv, bi);                                            // every lane: the wave's best
+    if (lane == 0) {
+        rv[wave] = bv;
+        ri[wave] = bi;
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    for (int w = 1; w < nwaves; w++) argmax_better(bv, bi, rv[w], ri[w]);
+    const uint32_t parts = gridDim.x;
+    const __amdgpu_buffer_rsrc_t pr = buf_rsrc(g.part, parts * 8u);
+    using u32x2 = unsigned int __attribute__((ext_vector_type(2)));
+    int last = 0;
+    if (lane == 0) {
+        const u32x2 v = {__float_as_uint(bv), static_cast<uint32_t>(bi)};
+        __builtin_amdgcn_raw_buffer_store_b64(v, pr, blockIdx.x * 8u, 0, kCoherent);
+        __builtin_amdgcn_s_waitcnt(0x0F70);                       // vmcnt(0): the part is stored
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        last = __hip_atomic_fetch_add(g.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == parts - 1;
+    }
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    float fv = -__builtin_inff();
+    int fi = kArgmaxNone;
+    for (uint32_t k = lane; k < parts; k += 64) {
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, k * 8u, 0, kCoherent));
+        argmax_better(fv, fi, __uint_as_float(v.x), static_cast<int>(v.y));
+    }
+    wave_best(fv, fi);
+    if (lane == 0) {
+        // hetero/backends.py:106-109 and the decode loop's bookkeeping
+        // (hetero/cpu_model.py:357-368): the token, its history slot, the
+        // next position
+        const int best = fi == kArgmaxNone ? 0 : fi;
+        *g.tok = best;
+        const int64_t p = *g.pos;
+        const int64_t k = p - g.s0;
+        if (k >= 0 && k < g.hist_len) g.hist[k] = best;
+        *g.pos = p + 1;
+        __hip_atomic_store(g.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 template <int MR, int RW, bool PAIR, int RING, bool NORM, int GSH>
 __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_kernel(MatList ml,
                                                                                      const float* __restrict__ x,
@@ -557,6 +617,10 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
+    // GreedyArgs (one row, no pair): the lane's best stored row so far
+    const bool greedy = MR == 1 && !PAIR && na.greedy.part != nullptr;   // uniform
+    float g_bv = -__builtin_inff();
+    int g_bi = kArgmaxNone;
     // a finished unit: its rows' sums are complete; one lane per (m, row)
     // stores the row's output
     auto finish = [&](int unit) {
@@ -585,6 +649,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
                         buf_rsrc(pick(ml.out, p), static_cast<uint32_t>(MR * no) * 4u);
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc), ro,
                                                           (m * no + (gr - rb)) * 4, 0, 0);
+                    if (greedy) argmax_better(g_bv, g_bi, acc, gr - rb);
                 }
             }
         }
@@ -638,6 +703,9 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
         }
         finish(cu_unit);
     }
+    // the prologue's amax and wave-sum slots are free past its last barrier
+    if constexpr (MR == 1 && !PAIR)
+        if (greedy) greedy_tail(g_bv, g_bi, na.greedy, red, reinterpret_cast<int*>(stage), lane, wave, nwaves);
 }
 
 // Workgroups of the kernel resident per CU (the ring-4 instance: the most
@@ -653,6 +721,8 @@ int stream_blocks_per_cu(int nwaves, size_t lds) {
 template <int MR, int RW, bool PAIR, int RING, bool NORM, int GSH>
 int launch_stream_k(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
                     size_t lds, int grid, hipStream_t st) {
+    if (na.greedy.part && (MR != 1 || PAIR || grid > kGreedyMaxParts))
+        return fail(Q4_EARG, "greedy token: one matrix, one row and at most %d workgroups", kGreedyMaxParts);
     auto kern = gemv_stream_kernel<MR, RW, PAIR, RING, NORM, GSH>;
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), kStreamLdsMax, lds_raised)) return rc;

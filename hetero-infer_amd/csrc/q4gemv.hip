@@ -988,6 +988,16 @@ static __device__ __align__(256) uint4 scratch[kScrPlanes + (kScrXsum + kScrXsca
 std::mutex g_scr_mu;
 void* g_scr_ptr[64] = {};
 
+// q4_norm_gemv_argmax_dev's per-workgroup (value, index) parts and arrival
+// counter: fixed arrays in device memory, one per GPU (zero at load; the
+// last workgroup of each launch sets the counter back to zero), so calls
+// that overlap in time on one GPU race.
+static __device__ __align__(256) float2 greedy_part[kGreedyMaxParts];
+static __device__ __align__(256) unsigned greedy_count[64];
+std::mutex g_greedy_mu;
+void* g_greedy_part[64] = {};
+void* g_greedy_count[64] = {};
+
 int scratch_workspace(Workspace* ws) {
     int dev;
     HIP_TRY(hipGetDevice(&dev));
@@ -1386,6 +1396,51 @@ int q4_norm_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
     const NormArgs na{delta, norm_w, x_out, eps};
     rc = launch_stream<1, false, true>(ml, x, n_in, static_cast<hipStream_t>(stream), na);
     if (rc == 0) return fail(Q4_EARG, "q4_norm_gemv_multi_dev: n_in = %d does not fit the norm prologue", n_in);
+    return rc < 0 ? rc : 0;
+}
+
+int q4_norm_gemv_argmax_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* logits,
+                            int n_out, const float* x, const float* delta, const float* norm_w, float eps,
+                            float* x_out, int n_in, int gs, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0,
+                            int hist_len, void* stream) {
+    int rc = check_gemv_shape(n_out, n_in, gs);
+    if (rc) return rc;
+    if (n_out == 0) return fail(Q4_EARG, "q4_norm_gemv_argmax_dev: no output rows");
+    if (!w || !scales || !biases || !logits || !tok || !pos || (hist_len > 0 && !hist))
+        return fail(Q4_EARG, "q4_norm_gemv_argmax_dev: null pointer");
+    if (reinterpret_cast<uintptr_t>(w) & 15) return fail(Q4_EARG, "w must be 16-byte aligned");
+    if ((rc = check_norm_args("q4_norm_gemv_argmax_dev", x, delta, norm_w, x_out, n_in, gs))) return rc;
+    int dev;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return fail(Q4_EARG, "device %d: the greedy-token arrays are kept for devices 0..63", dev);
+    void *part, *count;
+    {
+        std::lock_guard<std::mutex> lock(g_greedy_mu);
+        if (!g_greedy_part[dev]) {
+            void *a = nullptr, *b = nullptr;
+            HIP_TRY(hipGetSymbolAddress(&a, HIP_SYMBOL(greedy_part)));
+            HIP_TRY(hipGetSymbolAddress(&b, HIP_SYMBOL(greedy_count)));
+            if (!a || !b) return fail(Q4_EHIP, "hipGetSymbolAddress(greedy arrays) gave a null address");
+            g_greedy_part[dev] = a;
+            g_greedy_count[dev] = b;
+        }
+        part = g_greedy_part[dev];
+        count = g_greedy_count[dev];
+    }
+    MatList ml{};
+    for (int k = 0; k < kMaxMats; k++) {
+        ml.w[k] = w; ml.s[k] = scales; ml.b[k] = biases; ml.out[k] = logits;
+        ml.n_out[k] = k == 0 ? n_out : 0;
+    }
+    ml.row_begin[0] = 0;
+    for (int k = 0; k < kMaxMats; k++) ml.row_begin[k + 1] = ml.row_begin[k] + ml.n_out[k];
+    ml.count = 1;
+    ml.mrows = 1;
+    NormArgs na{delta, norm_w, x_out, eps};
+    na.greedy = GreedyArgs{static_cast<float2*>(part), static_cast<unsigned*>(count), tok, hist, pos, s0,
+                           hist_len > 0 ? hist_len : 0};
+    rc = launch_stream<1, false, true>(ml, x, n_in, static_cast<hipStream_t>(stream), na);
+    if (rc == 0) return fail(Q4_EARG, "q4_norm_gemv_argmax_dev: n_in = %d does not fit the norm prologue", n_in);
     return rc < 0 ? rc : 0;
 }
 

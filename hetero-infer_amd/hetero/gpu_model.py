@@ -7,12 +7,13 @@ and every operation a kernel of libq4gemv.so:
     launch, o_proj, the fused gate/up/SiLU*mul launch, down and lm_head --
     every GEMV result is the reference q4_gemv's bit for bit given the same
     input.  Each residual add and RMSNorm is folded into the prologue of the
-    GEMV that follows it (q4_norm_gemv_multi_dev for q/k/v and lm_head,
-    q4_norm_gate_up_silu_dev for gate/up; include/q4decode.h);
-  * the rest from include/q4decode.h: the embedding row (q4_embed_dev), bias
-    + RoPE + the fp16 KV-cache write fused with GQA attention split over the
-    context (q4_attention_rope_dev) and the greedy argmax with the step's
-    bookkeeping (q4_argmax_dev).
+    GEMV that follows it (q4_norm_gemv_multi_dev for q/k/v,
+    q4_norm_gate_up_silu_dev for gate/up; include/q4decode.h), and lm_head
+    takes the greedy argmax with the step's bookkeeping in its own launch
+    (q4_norm_gemv_argmax_dev);
+  * the rest from include/q4decode.h: the embedding row (q4_embed_dev) and
+    bias + RoPE + the fp16 KV-cache write fused with GQA attention split over
+    the context (q4_attention_rope_dev).
 The token id and the position live in device tensors and attention covers
 positions [0, pos] of a fixed-size cache, so one decode step is
 position-independent and is captured once as a HIP graph; generating n
@@ -168,11 +169,11 @@ class GpuStage:
             cur, other = other, cur
             q4.gemv_dev(*L["down"], self.hbuf, out=self.mlp_out, lib=lib)
             delta = self.mlp_out
-        # x = x + mlp; lm_head of the final norm (cpu_model.py:367)
-        q4.norm_gemv_multi_dev([self.lm_head], cur, delta, self.norm_w, self.eps, outs=[self.logits], lib=lib)
-        # greedy token (backends.py:106-109), history slot, position + 1
-        ck(lib.q4_argmax_dev(P(self.logits), self.logits.shape[1], P(self.tok), P(self.hist), P(self.pos),
-                             self.s0, self.hist.numel(), st), "argmax")
+        # x = x + mlp; lm_head of the final norm (cpu_model.py:367), and in the
+        # same launch the greedy token (backends.py:106-109), its history
+        # slot and position + 1
+        q4.norm_gemv_argmax_dev(self.lm_head, cur, delta, self.norm_w, self.eps, self.tok, self.pos,
+                                hist=self.hist, s0=self.s0, logits=self.logits, lib=lib)
 
     # -- driving --------------------------------------------------------------
     def _eager_step(self):

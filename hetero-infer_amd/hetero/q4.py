@@ -25,7 +25,7 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            # decode-step kernels (include/q4decode.h)
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
            "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev",
-           "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev",
+           "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev", "q4_norm_gemv_argmax_dev",
            # activation wire codec (include/q4wire.h)
            "q4_wire_payload_bytes", "q4_wire_encode_dev", "q4_wire_decode_dev",
            # chained GEMV programs (include/q4chain.h)
@@ -88,6 +88,9 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_norm_gate_up_silu_dev.restype = _I
         lib.q4_argmax_dev.argtypes = [_VP, _I, _VP, _VP, _VP, ctypes.c_int64, _I, _VP]
         lib.q4_argmax_dev.restype = _I
+        lib.q4_norm_gemv_argmax_dev.argtypes = ([_VP] * 4 + [_I] + [_VP] * 3 + [_F, _VP, _I, _I] + [_VP] * 3
+                                                + [ctypes.c_int64, _I, _VP])
+        lib.q4_norm_gemv_argmax_dev.restype = _I
     if hasattr(lib, "q4_wire_encode_dev"):
         lib.q4_wire_payload_bytes.argtypes = [_I] * 3
         lib.q4_wire_payload_bytes.restype = ctypes.c_longlong
@@ -216,6 +219,25 @@ def norm_gemv_multi_dev(mats, x, delta, norm_w, eps, x_out=None, outs=None, stre
                                     _stream(stream))
     check(lib, rc, "q4_norm_gemv_multi_dev")
     return outs
+
+
+def norm_gemv_argmax_dev(mat, x, delta, norm_w, eps, tok, pos, hist=None, s0=0, x_out=None, logits=None,
+                         stream=None, lib=None):
+    """norm_gemv_multi_dev of one matrix plus the greedy token: *tok = argmax
+    of the logits (NumPy's rule), hist[*pos - s0] = *tok when in range, *pos
+    += 1 -- all in the GEMV's launch.  Returns the logits."""
+    import torch
+    lib = lib or load()
+    w, s, b = mat
+    n_out, n_in = w.shape[0], w.shape[1] * 8
+    gs = n_in // s.shape[1]
+    if logits is None:
+        logits = torch.empty((1, n_out), dtype=torch.float32, device=x.device)
+    rc = lib.q4_norm_gemv_argmax_dev(_ptr(w), _ptr(s), _ptr(b), _ptr(logits), n_out, _ptr(x), _ptr_or_null(delta),
+                                     _ptr(norm_w), eps, _ptr_or_null(x_out), n_in, gs, _ptr(tok), _ptr_or_null(hist),
+                                     _ptr(pos), s0, 0 if hist is None else hist.numel(), _stream(stream))
+    check(lib, rc, "q4_norm_gemv_argmax_dev")
+    return logits
 
 
 def norm_gate_up_silu_dev(gate, up, x, delta, norm_w, eps, x_out=None, h=None, stream=None, lib=None):

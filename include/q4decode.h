@@ -100,6 +100,21 @@ int q4_attention_rope_dev(const float* q, const float* k, const float* v, const 
                           const float* sin_t, const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache, float* out,
                           float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream);
 
+/* The final norm, the vocabulary projection and the greedy token in one
+ * launch: logits as q4_norm_gemv_multi_dev computes them for the one matrix
+ * (lm_head after the final norm, hetero/cpu_model.py:355 and :367), then
+ * *tok, hist and *pos exactly as q4_argmax_dev(logits, n_out, ...) sets them
+ * (hetero/backends.py:106-109).  Each workgroup reduces the rows it stored
+ * and the last one to finish reduces those parts, through fixed arrays of
+ * the library in device memory (one per GPU): calls that overlap in time on
+ * one GPU, with each other or with another launch of this entry point,
+ * race.  The same arguments as q4_norm_gemv_multi_dev with count 1, plus
+ * q4_argmax_dev's. */
+int q4_norm_gemv_argmax_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* logits,
+                            int n_out, const float* x, const float* delta, const float* norm_w, float eps,
+                            float* x_out, int n_in, int gs, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0,
+                            int hist_len, void* stream);
+
 /* Greedy token (hetero/backends.py:106-109, NumpyBackend.sample: NumPy's
  * argmax, which takes NaN as the largest value -- the first NaN if there is
  * one, else the first index of the maximum) and the step's bookkeeping:

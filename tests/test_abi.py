@@ -207,3 +207,27 @@ def test_gemm_multi_argument_errors(lib):
     assert call(2, 0, x=None) == 0
     assert call(2, 8, x=fake + 4) == q4.Q4_EARG               # misaligned x
     assert call(2, 8, w=fake + 8) == q4.Q4_EARG               # misaligned weights
+
+
+def test_norm_gemv_argmax_argument_errors(lib):
+    """q4_norm_gemv_argmax_dev checks its arguments before any device call:
+    the GEMV shape, the norm-prologue limits, and the token, position and
+    history pointers."""
+    fake = 1 << 20                                       # 16-byte aligned, never dereferenced
+
+    def call(n_out=1000, n_in=512, gs=64, w=fake, x=fake, norm_w=fake, tok=fake, pos=fake, hist=fake, hist_len=4):
+        return lib.q4_norm_gemv_argmax_dev(w, fake, fake, fake, n_out, x, None, norm_w, 1e-6, None, n_in, gs,
+                                           tok, hist, pos, 0, hist_len, None)
+
+    assert call(n_out=0) == q4.Q4_EARG                  # no logits, no token
+    assert call(n_out=-1) != 0
+    assert call(tok=None) == q4.Q4_EARG
+    assert call(pos=None) == q4.Q4_EARG
+    assert call(hist=None) == q4.Q4_EARG                # hist_len > 0 needs the history
+    assert call(w=fake + 8) == q4.Q4_EARG
+    assert call(x=None) == q4.Q4_EARG
+    assert call(x=fake + 4) == q4.Q4_EARG
+    assert call(norm_w=None) == q4.Q4_EARG
+    assert call(gs=128, n_in=512) == q4.Q4_EARG          # the norm prologue takes gs 64
+    assert call(n_in=16384) == q4.Q4_EARG                # past the norm prologue's 8192
+    assert call(n_in=100) != 0                           # not a multiple of gs

@@ -104,3 +104,65 @@ def test_norm_gemv_argument_errors():
         (_, big) = mats(731, 64, 8256)
         xb = torch.zeros(8256, device="cuda")
         q4.norm_gemv_multi_dev([big], xb, None, xb, EPS, lib=lib)
+
+
+# The greedy token taken in lm_head's own launch (q4_norm_gemv_argmax_dev)
+# against q4_norm_gemv_multi_dev followed by q4_argmax_dev (whose NumPy
+# argmax rule other tests pin): logits bit for bit, token, history slot and
+# position.  Planted: nothing; a tie (the argmax row copied to a lower row:
+# the first index wins); NaN rows (fp16 NaN scales: the first NaN wins).
+# Shapes: the Qwen vocabulary, and vocabularies that leave workgroups with
+# no row.  Three calls in a row check that the arrival counter starts at 0
+# each launch.
+@pytest.mark.parametrize("n_in,n_out", [(3584, 152064), (512, 1000), (256, 37)])
+def test_norm_gemv_argmax_matches_two_launches(n_in, n_out):
+    import torch
+    print(f"norm gemv argmax n_in={n_in} n_out={n_out}", flush=True)
+    lib = q4.load()
+    rng = np.random.default_rng(n_out)
+    (w, s, b), _ = mats(900, n_out, n_in)
+    x, d, nw = tensors(rng.normal(0, 1, n_in).astype(np.float32), rng.normal(0, 1, n_in).astype(np.float32),
+                       rng.normal(1, 0.2, n_in).astype(np.float32))
+    st = torch.cuda.current_stream().cuda_stream
+
+    def state():
+        return (torch.zeros(1, dtype=torch.int64, device="cuda"), torch.full((4,), -1, dtype=torch.int64, device="cuda"),
+                torch.tensor([11], dtype=torch.int64, device="cuda"))
+
+    def two_launches(mat):
+        lg = q4.norm_gemv_multi_dev([mat], x, d, nw, EPS, lib=lib)[0]
+        tok, hist, pos = state()
+        rc = lib.q4_argmax_dev(lg.data_ptr(), n_out, tok.data_ptr(), hist.data_ptr(), pos.data_ptr(), 10, 4, st)
+        assert rc == 0, q4.last_error(lib)
+        return lg, tok, hist, pos
+
+    def fused(mat, calls=1):
+        tok, hist, pos = state()
+        for _ in range(calls):
+            lg = q4.norm_gemv_argmax_dev(mat, x, d, nw, EPS, tok, pos, hist=hist, s0=10, lib=lib)
+        return lg, tok, hist, pos
+
+    r = int(np.argmax(two_launches(tuple(tensors(w, s.view(np.int16), b.view(np.int16))))[0].cpu().numpy()))
+    cases = [("none", w, s, b, r)]
+    if r > 0:
+        lo = r // 2
+        w2, s2, b2 = w.copy(), s.copy(), b.copy()
+        w2[lo], s2[lo], b2[lo] = w[r], s[r], b[r]
+        cases.append(("tie", w2, s2, b2, lo))
+    a, c = n_out // 3, n_out - 1
+    s3 = s.copy()
+    s3.view(np.uint16)[[a, c]] = 0x7E00                  # fp16 NaN
+    cases.append(("nan", w, s3, b, a))
+    for name, cw, cs, cb, expect in cases:
+        mat = tuple(tensors(cw, cs.view(np.int16), cb.view(np.int16)))
+        ref = two_launches(mat)
+        got = fused(mat)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0].view(torch.int32), ref[0].view(torch.int32)), name
+        assert int(np.argmax(ref[0].cpu().numpy())) == expect, name
+        for g, e in zip(got[1:], ref[1:]):
+            assert torch.equal(g, e), (name, g, e)
+        assert int(got[1].item()) == expect, name
+    tok, hist, pos = fused(mat, calls=3)[1:]
+    torch.cuda.synchronize()
+    assert int(pos.item()) == 14 and hist.cpu().tolist() == [-1, a, a, a]
