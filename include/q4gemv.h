@@ -38,10 +38,13 @@ extern "C" {
  * kernel/q4gemv.c:232-233, bound by hetero/cpu_model.py:41-42 as
  * [c_void_p]*5 + [c_int]*4 -> c_int.  All pointers are host addresses.
  * w/scales/biases are uploaded to HBM on first use and kept resident, keyed
- * by their host addresses and shape and checked against a sampled
- * fingerprint on every call (they must not be modified while registered;
- * q4_release drops them).  nthreads is accepted and ignored.  Returns after
- * out[0..n_out) is written. */
+ * by their host addresses and shape.  Every call checks them against a
+ * fingerprint: 16 sampled words per array by default, so a caller that
+ * edits registered weights in place calls q4_release first; with the
+ * environment variable Q4_RESIDENCY_CHECK=full, a hash of every byte (an
+ * edit anywhere is re-uploaded, as the reference reads host memory on every
+ * call, at the cost of one host read of the weights per call).  nthreads is
+ * accepted and ignored.  Returns after out[0..n_out) is written. */
 int q4_gemv(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
             const float *x, float *out, int n_out, int n_in, int gs, int nthreads);
 

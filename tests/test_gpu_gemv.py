@@ -194,6 +194,22 @@ def test_residency_detects_replaced_weights(lib):
     assert lib.q4_release(w.ctypes.data) >= 1
 
 
+def test_residency_full_check_sees_an_edit_between_samples(lib, monkeypatch):
+    """Q4_RESIDENCY_CHECK=full hashes every byte: one word edited in place,
+    away from the 16 offsets the default fingerprint samples (byte 2708 of
+    32768; samples at multiples of 32767/15), is re-uploaded."""
+    o = oracle.Oracle()
+    w, s, b = synth.qlinear(12, 64, 1024, 64)
+    x = synth.activations(12, 1, 1024)[0]
+    monkeypatch.setenv("Q4_RESIDENCY_CHECK", "full")
+    first = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, 64)
+    assert_bit_exact(first, o.gemv(w, s, b, x, 64), "first")
+    w[5, 37] ^= np.uint32(0x11111111)
+    second = q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, 64)
+    assert_bit_exact(second, o.gemv(w, s, b, x, 64), "after the edit")
+    assert lib.q4_release(w.ctypes.data) >= 1
+
+
 def test_multi_dev_grouped(lib):
     """q4_gemv_multi_dev (q/k/v and gate/up style groups) vs the oracle, bit-exact."""
     import torch
