@@ -267,6 +267,25 @@ def test_matrix_core_tile_variants(lib):
             assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} N={n_out} m={m}")
 
 
+def test_matrix_core_group_count_bounds(lib):
+    """The matrix-core path at one group (K = 64: a window holds a single
+    group, every other group slot past the end) and at 64 and 65 groups
+    (K = 4096, 4160), for 16-row and 32-row tiles, with rows past M zero in
+    the prepared x.  Bit-exact vs the oracle."""
+    import torch
+    o = oracle.Oracle()
+    for k_in, n_out in ((64, 40), (4096, 3584), (4096, 9000), (4160, 200)):
+        w, s, b = synth.qlinear(800 + k_in + n_out, n_out, k_in, 64)
+        x = synth.activations(801, 8, k_in)
+        want = o.gemv_rows(w, s, b, x, 64)
+        tw, ts, tb, tx = (torch.from_numpy(a).cuda() for a in (w, s.view(np.int16), b.view(np.int16), x))
+        for m in (3, 7, 8):
+            print(f"matrix cores, group bounds K={k_in} N={n_out} m={m}", flush=True)
+            got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
+            torch.cuda.synchronize()
+            assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} N={n_out} m={m}")
+
+
 def test_matrix_core_uneven_prep_slices(lib):
     """The matrix-core x prep splits each row's groups over up to 8
     workgroups in slices of ceil(G / slices): K = 6208 (97 groups, slices of
