@@ -64,13 +64,14 @@ def make_weights(torch, gen, n_out, n_in, dev, gs=GS):
 
 
 PMC_SUMMARY = os.path.join("profiles", "gemv_stream_qwen7b_decode_sweep_pmc.md")
+CHAIN_PMC_SUMMARY = os.path.join("profiles", "gemv_chain_qwen7b_decode_sweep_trace_pmc.md")
 
 
-def measured_traffic():
-    """HBM bytes per sweep launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+def measured_traffic(summary=PMC_SUMMARY):
+    """HBM bytes per sweep launch from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
     (counter values scaled by a 256 MiB copy), or None when the summary is absent."""
     try:
-        with open(os.path.join(ROOT, PMC_SUMMARY)) as f:
+        with open(os.path.join(ROOT, summary)) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":", 1)[1])
@@ -769,6 +770,8 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--sweep-only", action="store_true",
                     help="only the grouped decode sweep (for rocprof runs)")
+    ap.add_argument("--chain-only", action="store_true",
+                    help="only the decode sweep as one chained program (for rocprof runs)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the M=512 prefill leg (for counter runs)")
     ap.add_argument("--small-m-only", action="store_true",
@@ -903,16 +906,22 @@ def main():
             wall = time.perf_counter() - t0
         return wall * 1e3 / steps, ev0.elapsed_time(ev1) / steps
 
-    ms_per_step, ev_ms = timed(step_grouped, args.steps, args.warmup)
+    if args.chain_only:
+        args.sweep_only = True
     n_launch = LAYERS * 4 + 1
-    value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
+    grouped_ms, grouped_ev = (float("nan"), float("nan")) if args.chain_only else \
+        timed(step_grouped, args.steps, args.warmup)
     calls_ms = float("nan") if args.sweep_only else timed(step_calls, max(3, args.steps // 2), 1)[0]
 
     # the same sweep as one chained GEMV program (include/q4chain.h): one
     # launch, a grid barrier between phases, each phase's first weights
-    # requested before its barrier
+    # requested before its barrier.  It is the headline unless a barrier
+    # wait timed out (then its outputs are not to be trusted and the grouped
+    # launches give the figure).
     chained = None
-    if not args.sweep_only:
+    chain_ms = chain_ev = float("nan")
+    chain_errors = -1
+    if args.chain_only or not args.sweep_only:
         phases = []
         for q, k, v, o, g, u, d in layers:
             phases += [([q, k, v], xs[3584], [gouts[3584][0], gouts[512][1], gouts[512][2]], False),
@@ -925,12 +934,16 @@ def main():
         def step_chain():
             chain.run(stream=stream)
 
-        chain_ms = timed(step_chain, args.steps, args.warmup)[0]
+        chain_ms, chain_ev = timed(step_chain, args.steps, args.warmup)
         chain_errors = chain.errors()
         chain.close()
         chained = {"ms_per_step": round(chain_ms, 4), "GB_s": round(sweep_bytes / (chain_ms * 1e-3) / 1e9, 1),
-                   "frac_peak": round(sweep_bytes / (chain_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                    "phases": len(phases), "barrier_timeouts": chain_errors}
+    use_chain = chain_errors == 0
+    if not use_chain and args.chain_only:
+        raise SystemExit(f"the chained sweep reported {chain_errors} barrier timeouts")
+    ms_per_step = chain_ms if use_chain else grouped_ms
+    value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
 
     if args.calibrate:
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
@@ -963,7 +976,29 @@ def main():
                            "GB_s": round(gbs, 1), "frac_peak": round(gbs / HBM_PEAK_GBS, 4)}
         del g
 
-    achieved = sweep_bytes / n_launch / (ev_ms * 1e-3 / n_launch) / 1e9
+    grouped_achieved = sweep_bytes / (grouped_ev * 1e-3) / 1e9
+    if use_chain:
+        achieved = sweep_bytes / (chain_ev * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic(CHAIN_PMC_SUMMARY), "traffic_source": CHAIN_PMC_SUMMARY,
+                    "algorithmic_bytes_per_launch": sweep_bytes,
+                    "kernel": "gemv_chain_kernel<false>: the whole sweep as one launch of 113 phases",
+                    "avg_launch_us": round(chain_ev * 1e3, 3)}
+        path = ("one chained GEMV program per step (include/q4chain.h): 113 phases in one persistent "
+                "launch, a grid barrier between phases")
+        launches = 1
+    else:
+        achieved = grouped_achieved
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic(), "traffic_source": PMC_SUMMARY,
+                    "algorithmic_bytes_per_launch": round(sweep_bytes / n_launch),
+                    "kernel": "gemv_stream_kernel<MR=1, RW, PAIR, RING, NORM=false> (x prologue "
+                              "fused), averaged over the launches of the grouped sweep",
+                    "avg_launch_us": round(grouped_ev * 1e3 / n_launch, 3)}
+        path = "grouped launches, the projections that share x (qkv, gate+up) in one launch"
+        launches = n_launch
     result = {
         "metric": "int4 GEMV HBM GB/s (% of MI355X peak) at Qwen2.5-7B shapes; decode tok/s",
         "value": round(value, 1),
@@ -981,19 +1016,21 @@ def main():
         "config": {"workload": "Qwen2.5-7B int4 projection sweep at M=1: 28 layers x "
                                "(q,k,v,o 3584->3584/512/512/3584, gate/up 3584->18944, "
                                "down 18944->3584) + lm_head 3584->152064, gs=64, distinct "
-                               "weights per layer (3.99 GB per step), in decode order with "
-                               "the projections that share x (qkv, gate+up) in one launch",
-                   "global_batch": 1, "launches_per_step": n_launch,
+                               "weights per layer (3.99 GB per step), in decode order",
+                   "path": path,
+                   "global_batch": 1, "launches_per_step": launches,
                    "bytes_per_step": sweep_bytes, "hip_graph": not args.no_graph,
                    "parallelism": "single GPU"},
         "frac_of_peak": round(value / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(), "traffic_source": PMC_SUMMARY,
-                     "algorithmic_bytes_per_launch": round(sweep_bytes / n_launch),
-                     "kernel": "gemv_stream_kernel<MR=1, RW, PAIR, RING, NORM=false> (x prologue "
-                               "fused), averaged over the launches of the grouped sweep",
-                     "avg_launch_us": round(ev_ms * 1e3 / n_launch, 3)},
+        "roofline": roofline,
+        "grouped_launches": None if args.chain_only else {
+            "ms_per_step": round(grouped_ms, 4), "GB_s": round(sweep_bytes / (grouped_ms * 1e-3) / 1e9, 1),
+            "frac_peak": round(sweep_bytes / (grouped_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "launches_per_step": n_launch,
+            "kernel": "gemv_stream_kernel<MR=1, RW, PAIR, RING, NORM=false> (x prologue fused)",
+            "avg_launch_us": round(grouped_ev * 1e3 / n_launch, 3),
+            "achieved_per_launch_GB_s": round(grouped_achieved, 1),
+            "traffic_per_launch": measured_traffic(), "traffic_source": PMC_SUMMARY},
         "per_shape": per_shape,
         "one_call_per_projection": {"ms_per_step": round(calls_ms, 4),
                                     "GB_s": round(sweep_bytes / (calls_ms * 1e-3) / 1e9, 1),
