@@ -501,9 +501,10 @@ int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) 
         while (in.n_out[k] % UB) UB >>= 1;
     const int items = mult * UB * C;
     int ring = 0;
-    if (items % 4 == 0) ring = 4;
+    // two items in flight per wave where they divide the unit: deeper
+    // rings measured slower (more loads queued per CU)
+    if (items % 2 == 0) ring = 2;
     else if (!in.pair && items % 5 == 0) ring = 5;
-    else if (items % 2 == 0) ring = 2;
     else if (!in.pair) ring = 1;
     if (!ring) return fail(Q4_EARG, "no ring size divides %d items", items);
     out.UB = UB;

@@ -558,7 +558,13 @@ int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int 
     const int want = (n_units + nwaves - 1) / nwaves;
     const int cap = num_cus() * per_cu;                 // every workgroup resident at once
     const int grid = want < cap ? want : cap;
-    // ring: a divisor of the unit's items (units change only between rings)
+    // ring: a divisor of the unit's items (units change only between rings),
+    // two items where they divide it.  Deeper rings were slower on every
+    // large shape (same-box, down 18944 -> 3584: 13.5 us at 5 items,
+    // 15.6 us at 10, 12.5 us at 2, 14.7 us at 1; gate+up 17.3 us at 4,
+    // 16.3 us at 2), the more loads a CU has queued the longer each waits.
+    if (items % 2 == 0)
+        return launch_stream_k<MR, RW, PAIR, 2, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
     if (items % 4 == 0)
         return launch_stream_k<MR, RW, PAIR, 4, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
     if constexpr (MR == 1 && !PAIR)
