@@ -983,7 +983,7 @@ def main():
                     "frac": round(achieved / HBM_PEAK_GBS, 4),
                     "traffic": measured_traffic(CHAIN_PMC_SUMMARY), "traffic_source": CHAIN_PMC_SUMMARY,
                     "algorithmic_bytes_per_launch": sweep_bytes,
-                    "kernel": "gemv_chain_kernel<false>: the whole sweep as one launch of 113 phases",
+                    "kernel": "gemv_chain_kernel: the whole sweep as one launch of 113 phases",
                     "avg_launch_us": round(chain_ev * 1e3, 3)}
         path = ("one chained GEMV program per step (include/q4chain.h): 113 phases in one persistent "
                 "launch, a grid barrier between phases")
