@@ -24,9 +24,9 @@
 // Work split.  A workgroup owns a tile of 32 weight rows (16 when 32-row
 // tiles would leave CUs idle; PAIR: 32 gate rows and the same 32 up rows,
 // one A operand for both) and runs S waves over K
-// in windows of 8*S groups, 8 consecutive groups per wave, each wave
-// streaming its groups through a register ring of 8 (the next window's
-// loads are in flight while the window's terms are chained).  Each group's
+// in windows of kMfRing*S groups, kMfRing consecutive groups per wave, each
+// wave streaming its groups through a register ring of kMfRing (the next
+// window's loads are in flight while the window's terms are chained).  Each group's
 // fp32 term goes to an LDS table; after a barrier one lane per (activation
 // row, weight row) adds the window's terms in ascending group order.  The K
 // split keeps enough waves in flight for the 3584-row shapes; the ordered
@@ -37,17 +37,20 @@
 // twice the L2 requests), turned into the B operands of the two groups by
 // v_permlane16_swap and v_permlane32_swap; per group the A operand (the 32
 // lanes of rows 0..15, 32 bytes each) and the xsum of the lane's four
-// activation rows.  Scales and biases come once per window: the
-// lane's row, 8 groups in 16 bytes, scales in k-half 0 and biases in k-half
-// 1, exchanged across the halves (when the group count is a multiple of 8;
-// else one 2-byte load each per group).
+// activation rows.  Scales and biases come once per window: the lane's
+// row, 8 groups in 16 bytes (the window's kMfRing of them used), scales in
+// k-half 0 and biases in k-half 1, exchanged across the halves (when the
+// group count is a multiple of 8; else one 2-byte load each per group).
 #pragma once
 
 #include "q4_common.h"
 
 namespace q4k {
 
-constexpr int kMfRing = 8;          // groups per wave and window (ring: 4 slots of 2 groups)
+// groups per wave and window (ring: 2 slots of 2 groups).  8 groups (4
+// slots) measured slower: q_proj at 8 rows 11.45 against 10.9 us, the MLP
+// block 61.6 against 61.2 us -- fewer loads queued per CU wait less.
+constexpr int kMfRing = 4;
 constexpr int kMfArows = 16;        // A rows stored per (group, k-half): xl 0..7, xh 8..15
 
 // x of up to 8 rows, prepared for the small-M MFMA kernel.  Grid (P, 8):
@@ -206,7 +209,7 @@ __device__ __forceinline__ uint32_t half_of(const uint4& v, int k) {
 
 // out[m][row] for m < M (PAIR: h[m][row] = SiLU(gate) * up), row stride ldo.
 // Grid: one workgroup per tile of TR rows; block: 64 * S threads (S = 4 or
-// 8: the ring takes about 150-200 registers, so at most two waves per SIMD).
+// 8: with the x operand in the ring, two waves per SIMD).
 // SB8: the group count is a multiple of 8 (scales/biases by window).
 // TR: weight rows per tile, 32, or 16 (B columns 16..31 dead) to spread a
 // matrix of few rows over twice the workgroups.
