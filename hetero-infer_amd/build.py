@@ -42,7 +42,7 @@ HIPCC_FLAGS = [
 # (activation rows, gate/up pair, ring size, group size 64 << gsh) of the
 # streaming kernel objects
 STREAM_INSTANCES = [(mr, pair, ring, gsh) for gsh in (0, 1) for mr in (1, 2) for pair in (0, 1)
-                    for ring in (1, 2, 4)] + [(1, 0, 5, 0), (1, 0, 5, 1)]
+                    for ring in (1, 2)] + [(1, 0, 5, 0), (1, 0, 5, 1)]
 
 
 def hipcc() -> str:

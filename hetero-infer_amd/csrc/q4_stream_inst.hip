@@ -1,7 +1,7 @@
 // Instances of the streaming GEMV kernel, one object per (activation rows,
 // gate/up pair, ring size, group size), one-row objects with the norm
 // prologue too: the build compiles this file once per -DQ4_MR=<1|2>
-// -DQ4_PAIR=<0|1> -DQ4_RING=<1|2|4|5> -DQ4_GSH=<0|1> (group size 64 << GSH),
+// -DQ4_PAIR=<0|1> -DQ4_RING=<1|2|5> -DQ4_GSH=<0|1> (group size 64 << GSH),
 // in parallel.
 #include "q4_stream.h"
 
@@ -11,7 +11,7 @@
 
 namespace q4k {
 
-#if Q4_RING == 4
+#if Q4_RING == 2
 #define Q4_STREAM_OCC(RW, NORM) \
     template int stream_blocks_per_cu<Q4_MR, RW, static_cast<bool>(Q4_PAIR), NORM, Q4_GSH>(int, size_t);
 #else

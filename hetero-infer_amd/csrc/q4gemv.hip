@@ -80,7 +80,6 @@ int num_cus() {
                                                                        size_t, int, hipStream_t);
 #define Q4_STREAM_RINGS(MR, RW, PAIR, NORM, GSH)                                                    \
     Q4_STREAM_EXTERN(MR, RW, PAIR, 1, NORM, GSH) Q4_STREAM_EXTERN(MR, RW, PAIR, 2, NORM, GSH)       \
-    Q4_STREAM_EXTERN(MR, RW, PAIR, 4, NORM, GSH)                                                    \
     extern template int stream_blocks_per_cu<MR, RW, PAIR, NORM, GSH>(int, size_t);
 #define Q4_STREAM_GS(GSH)                                                                           \
     Q4_STREAM_RINGS(1, 1, false, false, GSH) Q4_STREAM_RINGS(1, 2, false, false, GSH)              \
@@ -565,8 +564,6 @@ int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int 
     // 16.3 us at 2), the more loads a CU has queued the longer each waits.
     if (items % 2 == 0)
         return launch_stream_k<MR, RW, PAIR, 2, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
-    if (items % 4 == 0)
-        return launch_stream_k<MR, RW, PAIR, 4, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
     if constexpr (MR == 1 && !PAIR)
         if (items % 5 == 0)
             return launch_stream_k<MR, RW, PAIR, 5, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
