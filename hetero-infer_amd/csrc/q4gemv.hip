@@ -1027,7 +1027,7 @@ void* g_scr_ptr[64] = {};
 // last workgroup of each launch sets the counter back to zero), so calls
 // that overlap in time on one GPU race.
 static __device__ __align__(256) float2 greedy_part[kGreedyMaxParts];
-static __device__ __align__(256) unsigned greedy_count[64];
+static __device__ __align__(256) unsigned greedy_count[64];   // one counter ([0]) on a 256-byte line of its own
 std::mutex g_greedy_mu;
 void* g_greedy_part[64] = {};
 void* g_greedy_count[64] = {};
