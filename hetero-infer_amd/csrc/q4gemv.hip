@@ -567,8 +567,6 @@ int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int 
     if constexpr (MR == 1 && !PAIR)
         if (items % 5 == 0)
             return launch_stream_k<MR, RW, PAIR, 5, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
-    if (items % 2 == 0)
-        return launch_stream_k<MR, RW, PAIR, 2, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
     return launch_stream_k<MR, RW, PAIR, 1, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
 }
 
