@@ -41,26 +41,14 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "hetero-infer_amd"))
 
+from hetero import sweep  # noqa: E402
+from hetero.sweep import GS, HEAD_SHAPE, LAYER_SHAPES, LAYERS, gemv_bytes, make_weights  # noqa: E402,F401
+
 HBM_PEAK_GBS = 8000.0
-LAYERS = 28
-GS = 64
-LAYER_SHAPES = [("q_proj", 3584, 3584), ("k_proj", 3584, 512), ("v_proj", 3584, 512),
-                ("o_proj", 3584, 3584), ("gate_proj", 3584, 18944), ("up_proj", 3584, 18944),
-                ("down_proj", 18944, 3584)]
-HEAD_SHAPE = ("lm_head", 3584, 152064)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
-
-
-def make_weights(torch, gen, n_out, n_in, dev, gs=GS):
-    w = torch.randint(-2**31, 2**31, (n_out, n_in // 8), dtype=torch.int64, device=dev,
-                      generator=gen).to(torch.int32)
-    g = n_in // gs
-    s = (torch.randn((n_out, g), device=dev, generator=gen) * 0.02).abs().half()
-    b = (-8.0 * s.float() + torch.randn((n_out, g), device=dev, generator=gen) * 0.002).half()
-    return w, s.view(torch.int16), b.view(torch.int16)
 
 
 PMC_SUMMARY = os.path.join("profiles", "gemv_stream_qwen7b_decode_sweep_pmc.md")
@@ -78,10 +66,6 @@ def measured_traffic(summary=PMC_SUMMARY):
     except OSError:
         pass
     return None
-
-
-def gemv_bytes(m, n_out, n_in, gs=GS):
-    return n_out * n_in // 2 + 4 * n_out * (n_in // gs) + 4 * m * n_in + 4 * m * n_out
 
 
 def graph_us(torch, stream, body, calls, reps=5):
@@ -820,19 +804,14 @@ def main():
         torch.cuda.empty_cache()
         print(json.dumps({"dropin": dropin_bench(cfg, meta, hw, hks, hvs)}), flush=True)
         return
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(1234)
     t_setup = time.perf_counter()
-    layers = [[make_weights(torch, gen, n_out, n_in, dev) for _, n_in, n_out in LAYER_SHAPES]
-              for _ in range(LAYERS)]
+    layers, head, xs = sweep.make_model(torch, dev, seed=1234)
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(torch, lib, layers, dev)}), flush=True)
         return
     if args.small_m_only:
         print(json.dumps({"small_m": small_m_bench(torch, lib, layers, dev)}), flush=True)
         return
-    head = make_weights(torch, gen, HEAD_SHAPE[2], HEAD_SHAPE[1], dev)
-    xs = {k: torch.randn((1, k), device=dev, generator=gen) for k in (3584, 18944)}
     outs = {n: torch.empty((1, n), device=dev) for n in (512, 3584, 18944, 152064)}
     torch.cuda.synchronize()
     log(f"setup {time.perf_counter() - t_setup:.1f}s")
@@ -878,8 +857,7 @@ def main():
             gemv(d)
         gemv(head)
 
-    sweep_bytes = LAYERS * sum(gemv_bytes(1, n_out, n_in) for _, n_in, n_out in LAYER_SHAPES) \
-        + gemv_bytes(1, HEAD_SHAPE[2], HEAD_SHAPE[1])
+    sweep_bytes = sweep.sweep_bytes()
 
     def timed(step, steps, warmup):
         with torch.cuda.stream(stream):
@@ -921,14 +899,11 @@ def main():
     chained = None
     chain_ms = chain_ev = float("nan")
     chain_errors = -1
+    chain_bad = None
     if args.chain_only or not args.sweep_only:
-        phases = []
-        for q, k, v, o, g, u, d in layers:
-            phases += [([q, k, v], xs[3584], [gouts[3584][0], gouts[512][1], gouts[512][2]], False),
-                       ([o], xs[3584], [outs[3584]], False),
-                       ([g, u], xs[3584], [gouts[18944][0], gouts[18944][1]], False),
-                       ([d], xs[18944], [outs[3584]], False)]
-        phases.append(([head], xs[3584], [outs[152064]], False))
+        # every phase its own outputs, so that after the timed replays each
+        # one can be checked against the same phase run as its own launch
+        phases = sweep.phases(layers, head, xs, sweep.distinct_outputs(torch, dev))
         chain = q4.Chain(phases, lib=lib)
 
         def step_chain():
@@ -937,11 +912,22 @@ def main():
         chain_ms, chain_ev = timed(step_chain, args.steps, args.warmup)
         chain_errors = chain.errors()
         chain.close()
+        check = sweep.phases(layers, head, xs, sweep.distinct_outputs(torch, dev))
+        with torch.cuda.stream(stream):
+            sweep.run_launches(check, stream, lib=lib)
+        torch.cuda.synchronize()
+        chain_bad = sweep.mismatches(torch, phases, check)
         chained = {"ms_per_step": round(chain_ms, 4), "GB_s": round(sweep_bytes / (chain_ms * 1e-3) / 1e9, 1),
-                   "phases": len(phases), "barrier_timeouts": chain_errors}
-    use_chain = chain_errors == 0
+                   "phases": len(phases), "barrier_timeouts": chain_errors,
+                   "outputs_vs_launches": {"phases_checked": len(phases),
+                                           "values_checked": int(sum(o.numel() for ph in phases for o in ph[2])),
+                                           "phases_differing": len(chain_bad),
+                                           "first_differences": chain_bad[:5]}}
+        del phases, check
+    use_chain = chain_errors == 0 and chain_bad == []
     if not use_chain and args.chain_only:
-        raise SystemExit(f"the chained sweep reported {chain_errors} barrier timeouts")
+        raise SystemExit(f"the chained sweep reported {chain_errors} barrier timeouts and "
+                         f"{len(chain_bad or [])} phases differing from their own launches")
     ms_per_step = chain_ms if use_chain else grouped_ms
     value = sweep_bytes / (ms_per_step * 1e-3) / 1e9
 

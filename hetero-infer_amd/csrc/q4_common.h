@@ -182,11 +182,14 @@ int gemm_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K, i
 // Stream-K form of the prefill GEMM: P workgroups in nx XCD groups (256 x
 // 256 tiles; P a multiple of nx, and P / nx at least a group's tile count,
 // ceil(tiles / nx)), each matrix's output directly.  part: P x 256 x 256
-// floats of partial sums; flags: 32 P words, zero on entry and on return;
-// errors: a counter of partials that did not arrive in time (their tiles
-// are NaN).
-int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* errors, int M, int K,
+// floats of partial sums; flags: 32 P words; ctl: kSkCtlWords control
+// words (the epoch, the exit counter and, at kSkCtlErrors, a counter of
+// partials that did not arrive in time: their tiles are NaN).  flags and
+// ctl are zero when first used and are left consistent by every launch.
+int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, int M, int K,
                int P, int nx, hipStream_t st);
+constexpr int kSkCtlWordsHost = 96;   // the control words after the flags (q4_gemm.hip: kSkCtlWords)
+constexpr int kSkCtlErrorsHost = 64;  // the error counter among them (kSkCtlErrors)
 
 // Dynamic LDS above 64 KiB needs the kernel's limit raised on each device
 // that runs it.  `done` holds one bit per device already raised (0..63; a

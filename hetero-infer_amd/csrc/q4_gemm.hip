@@ -324,13 +324,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
 // at most two segments, a tile's tail and the next tile's head; the
 // workgroup runs the head first.  A segment that does not reach its tile's
 // end is a partial: it goes to the workgroup's slot in `part` at device
-// scope, then its flag is raised.  The segment that ends a tile (its
-// owner's) adds the partials of the workgroups before it in its group that
-// cover the rest of the tile, nearest first, and stores the tile.  Waits
-// point only to lower-numbered workgroups, which are dispatched first, and
-// a partial is a workgroup's first segment whenever it has two, so an
-// owner, which reaches its tail last, rarely waits.  The owner lowers the
-// flags it consumed: they are zero again for the next launch.
+// scope, then its flag is set to the launch's epoch.  The segment that ends
+// a tile (its owner's) adds the partials of the workgroups before it in its
+// group that cover the rest of the tile, nearest first, and stores the
+// tile.  Waits point only to lower-numbered workgroups, which are
+// dispatched first, and a partial is a workgroup's first segment whenever it
+// has two, so an owner, which reaches its tail last, rarely waits.
+//
+// The epoch makes a flag mean "this launch's partial is in": every
+// workgroup reads it from ctl[0] when it starts, and the last workgroup to
+// leave advances it.  A flag is never lowered, so a partial that arrives
+// after its owner gave up waiting (an error, its tile stored as NaN) holds
+// an old epoch that no later launch waits for.  Stream-ordered launches on
+// one workspace, captured ones included, each see their own epoch.
 //
 // A slot holds 256 x 256 floats as [block b][quad q][thread] of 16 bytes,
 // block b = i TN + j of the accumulators, quad q = v / 4: every store and
@@ -342,6 +348,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
 constexpr int kSkParts = 4;                                        // the owner adds a slot in 4 parts
 constexpr int kSkFlagStride = 32;                                  // flags 128 bytes apart
 constexpr long long kSkSpinTicks = 20000000;                       // 200 ms at 100 MHz
+// The control words after the flags (each on its own 128-byte line): the
+// epoch counter, the exit counter, the error counter.
+constexpr int kSkCtlGen = 0, kSkCtlExited = 32, kSkCtlErrors = 64, kSkCtlWords = 96;
+static_assert(kSkCtlWords == kSkCtlWordsHost && kSkCtlErrors == kSkCtlErrorsHost, "one layout of the control words");
 
 // A workgroup's stream-K group: the tiles [t0, t0 + T / G) of XCD `xcd`
 // (tiles m-block major, split into nx contiguous groups; workgroup i runs
@@ -356,9 +366,9 @@ struct SkGroup {
 // Segment [it, stop) of a stream-K range (stop at most its tile's end).
 template <int BM, int NW>
 __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, const GemmMats& gm, float* part,
-                                              unsigned* flags, unsigned* errors, int M, int K, const SkGroup& gp,
-                                              long it, long stop, const W4Src<BM, NW>& src, int tid, int wave,
-                                              int lane) {
+                                              unsigned* flags, unsigned* errors, unsigned epoch, int M, int K,
+                                              const SkGroup& gp, long it, long stop, const W4Src<BM, NW>& src,
+                                              int tid, int wave, int lane) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
     constexpr int TM = W4Layout<BM, NW>::TM, TN = W4Layout<BM, NW>::TN, NB = TM * TN;
     constexpr int NT = 64 * NW;
@@ -397,7 +407,8 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
         __builtin_amdgcn_s_waitcnt(0x0F70);                    // this thread's stores have landed
         __syncthreads();
         if (tid == 0)
-            __hip_atomic_store(flags + gp.phys(wg) * kSkFlagStride, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(flags + gp.phys(wg) * kSkFlagStride, epoch, __ATOMIC_RELEASE,
+                               __HIP_MEMORY_SCOPE_AGENT);
     } else {
         // the partials of workgroups wg - 1, wg - 2, .. j1, whose ranges
         // end inside this tile
@@ -409,8 +420,7 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
                 if (T * (j + 1) / P == T * j / P) continue;        // an empty range
                 const long long t0 = __builtin_amdgcn_s_memrealtime();
                 while (__hip_atomic_load(flags + gp.phys(j) * kSkFlagStride, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT) ==
-                       0u) {
+                                         __HIP_MEMORY_SCOPE_AGENT) != epoch) {
                     if (__builtin_amdgcn_s_memrealtime() - t0 > kSkSpinTicks) {
                         __hip_atomic_fetch_add(errors, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         missing = 1;
@@ -418,7 +428,6 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
                     }
                     __builtin_amdgcn_s_sleep(2);
                 }
-                __hip_atomic_store(flags + gp.phys(j) * kSkFlagStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         // a tile whose partials did not all arrive is stored as NaN
@@ -469,7 +478,7 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
 template <int BM, int NW>
 __global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __restrict__ xb, GemmMats gm,
                                                              float* __restrict__ part, unsigned* __restrict__ flags,
-                                                             unsigned* __restrict__ errors, int M, int K, int nx) {
+                                                             unsigned* __restrict__ ctl, int M, int K, int nx) {
     static_assert(BM == 256 && NW == 4, "stream-K slots assume 256 x 256 tiles of 4 waves");
     extern __shared__ uint4 w4_lds[];
     char* lds = reinterpret_cast<char*>(w4_lds);
@@ -485,15 +494,35 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __r
     gp.t0 = tiles * gp.xcd / nx;
     gp.T = static_cast<long>(tiles * (gp.xcd + 1) / nx - gp.t0) * G;
     const long begin = gp.T * gp.slot / gp.P, end = gp.T * (gp.slot + 1) / gp.P;
-    if (begin >= end) return;
-    W4Src<BM, NW> src;
-    w4_src<BM, NW>(src, K, wave, lane);
-    const long cut = (begin / G + 1) * G;                         // end of the first tile
-    if (end > cut) {
-        w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, M, K, gp, cut, end, src, tid, wave, lane);
-        w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, M, K, gp, begin, cut, src, tid, wave, lane);
-    } else {
-        w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, M, K, gp, begin, end, src, tid, wave, lane);
+    // this launch's epoch (never 0: the flags start at 0)
+    const unsigned epoch =
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(ctl + kSkCtlGen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) +
+        1u;
+    unsigned* errors = ctl + kSkCtlErrors;
+    if (begin < end) {
+        W4Src<BM, NW> src;
+        w4_src<BM, NW>(src, K, wave, lane);
+        const long cut = (begin / G + 1) * G;                     // end of the first tile
+        if (end > cut) {
+            w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, epoch, M, K, gp, cut, end, src, tid, wave, lane);
+            w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, epoch, M, K, gp, begin, cut, src, tid, wave,
+                                  lane);
+        } else {
+            w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, epoch, M, K, gp, begin, end, src, tid, wave,
+                                  lane);
+        }
+    }
+    // the last workgroup to leave advances the epoch (every workgroup has
+    // read it by then: the release orders that read before the count)
+    if (tid == 0) {
+        const unsigned left =
+            __hip_atomic_fetch_add(ctl + kSkCtlExited, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (left == gridDim.x - 1) {
+            __hip_atomic_store(ctl + kSkCtlExited, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // epoch - 1 is the stored value; skip the one whose epoch would be 0
+            const unsigned next = epoch == 0xFFFFFFFFu ? 0u : epoch;
+            __hip_atomic_store(ctl + kSkCtlGen, next, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -517,14 +546,14 @@ int launch_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K,
 }
 
 template <int BM, int NW>
-int launch_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* errors, int M, int K,
+int launch_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, int M, int K,
                  int P, int nx, hipStream_t st) {
     auto kern = gemm_w4_sk_kernel<BM, NW>;
     const size_t lds = w4_lds_bytes<BM, NW>();
     static_assert(256 * 256 * 4 / kSkParts <= 3 * w4_stage_bytes(BM), "a part of a slot fits the LDS ring");
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
-    hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, gm, part, flags, errors, M, K, nx);
+    hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, gm, part, flags, ctl, M, K, nx);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "prefill gemm (stream-K) launch: %s", hipGetErrorString(e));
     return 0;
@@ -538,9 +567,9 @@ int gemm_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K, i
                      : launch_w4<128, 8>(xb, gm, part, M, K, S, kt_split, ldp, st);
 }
 
-int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* errors, int M, int K,
+int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, int M, int K,
                int P, int nx, hipStream_t st) {
-    return launch_w4_sk<256, 4>(xb, gm, part, flags, errors, M, K, P, nx, st);
+    return launch_w4_sk<256, 4>(xb, gm, part, flags, ctl, M, K, P, nx, st);
 }
 
 }  // namespace q4k

@@ -708,24 +708,22 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
         if (greedy) greedy_tail(g_bv, g_bi, na.greedy, red, reinterpret_cast<int*>(stage), lane, wave, nwaves);
 }
 
-// Workgroups of the kernel resident per CU (the ring-4 instance: the most
-// registers of the rings in use).
-template <int MR, int RW, bool PAIR, bool NORM, int GSH>
-int stream_blocks_per_cu(int nwaves, size_t lds) {
-    int per_cu = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per_cu, gemv_stream_kernel<MR, RW, PAIR, 4, NORM, GSH>, 64 * nwaves, lds);
-    return (e != hipSuccess || per_cu < 1) ? 1 : per_cu;
-}
-
+// Launch the instance: `want` workgroups, capped at what is resident at
+// once for this instance (its own occupancy: rings differ in registers), so
+// that every workgroup runs in the first round.
 template <int MR, int RW, bool PAIR, int RING, bool NORM, int GSH>
 int launch_stream_k(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
-                    size_t lds, int grid, hipStream_t st) {
-    if (na.greedy.part && (MR != 1 || PAIR || grid > kGreedyMaxParts))
-        return fail(Q4_EARG, "greedy token: one matrix, one row and at most %d workgroups", kGreedyMaxParts);
+                    size_t lds, int want, hipStream_t st) {
     auto kern = gemv_stream_kernel<MR, RW, PAIR, RING, NORM, GSH>;
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), kStreamLdsMax, lds_raised)) return rc;
+    int per_cu = 0;
+    const hipError_t oe = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * nwaves, lds);
+    if (oe != hipSuccess || per_cu < 1) per_cu = 1;
+    const int cap = num_cus() * per_cu;
+    const int grid = want < cap ? want : cap;
+    if (na.greedy.part && (MR != 1 || PAIR || grid > kGreedyMaxParts))
+        return fail(Q4_EARG, "greedy token: one matrix, one row and at most %d workgroups", kGreedyMaxParts);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB, na);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "stream gemv launch: %s", hipGetErrorString(e));

@@ -11,16 +11,9 @@
 
 namespace q4k {
 
-#if Q4_RING == 2
-#define Q4_STREAM_OCC(RW, NORM) \
-    template int stream_blocks_per_cu<Q4_MR, RW, static_cast<bool>(Q4_PAIR), NORM, Q4_GSH>(int, size_t);
-#else
-#define Q4_STREAM_OCC(RW, NORM)
-#endif
 #define Q4_STREAM_INST(RW, NORM)                                                                      \
     template int launch_stream_k<Q4_MR, RW, static_cast<bool>(Q4_PAIR), Q4_RING, NORM, Q4_GSH>(      \
-        const MatList&, const float*, const NormArgs&, int, int, int, size_t, int, hipStream_t);     \
-    Q4_STREAM_OCC(RW, NORM)
+        const MatList&, const float*, const NormArgs&, int, int, int, size_t, int, hipStream_t);
 
 Q4_STREAM_INST(1, false)
 #if Q4_MR <= 4

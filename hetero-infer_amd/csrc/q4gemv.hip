@@ -79,8 +79,7 @@ int num_cus() {
                                                                        const NormArgs&, int, int, int, \
                                                                        size_t, int, hipStream_t);
 #define Q4_STREAM_RINGS(MR, RW, PAIR, NORM, GSH)                                                    \
-    Q4_STREAM_EXTERN(MR, RW, PAIR, 1, NORM, GSH) Q4_STREAM_EXTERN(MR, RW, PAIR, 2, NORM, GSH)       \
-    extern template int stream_blocks_per_cu<MR, RW, PAIR, NORM, GSH>(int, size_t);
+    Q4_STREAM_EXTERN(MR, RW, PAIR, 1, NORM, GSH) Q4_STREAM_EXTERN(MR, RW, PAIR, 2, NORM, GSH)
 #define Q4_STREAM_GS(GSH)                                                                           \
     Q4_STREAM_RINGS(1, 1, false, false, GSH) Q4_STREAM_RINGS(1, 2, false, false, GSH)              \
     Q4_STREAM_RINGS(1, 3, false, false, GSH) Q4_STREAM_RINGS(1, 4, false, false, GSH)              \
@@ -312,6 +311,48 @@ __global__ void gemv_generic_kernel(
     out[static_cast<size_t>(m) * n_out + o] = acc;
 }
 
+// The reference's fp32 path for the rows past its last ROWS block
+// (kernel/q4gemv.c:185-200; rows [row0, n_out) of an m-row GEMV): one wave
+// per (row, activation row).  Lane l takes groups l, l + 64, ..; for its
+// group it adds the 64 values of x in ascending order (the xsum of
+// :244-248), chains s = fma(q, x, s) over the group's values in ascending
+// order (:192-195; clang contracts the reference's `s += q * x`), and forms
+// the term fma(scale, s, bias * xsum) (:196-197).  Lane 0 then adds the
+// terms to the row's sum in ascending group order.
+__global__ __launch_bounds__(64) void tail_rows_kernel(
+    const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ bi,
+    const float* __restrict__ x, float* __restrict__ out, int row0, int n_out, int n_in, int gs) {
+    __shared__ float terms[64];
+    const int o = row0 + blockIdx.x, m = blockIdx.y, lane = threadIdx.x;
+    const int G = n_in / gs, wpr = n_in >> 3, wpg = gs >> 3;
+    const float* xr = x + static_cast<size_t>(m) * n_in;
+    const uint32_t* wr = w + static_cast<size_t>(o) * wpr;
+    float acc = 0.0f;
+    for (int g0 = 0; g0 < G; g0 += 64) {
+        const int g = g0 + lane;
+        float term = 0.0f;
+        if (g < G) {
+            float xs = 0.0f, sd = 0.0f;
+            for (int i = 0; i < gs; i++) xs = __fadd_rn(xs, xr[g * gs + i]);
+            for (int k = 0; k < wpg; k++) {
+                const uint32_t d = wr[g * wpg + k];
+                for (int n = 0; n < 8; n++)
+                    sd = __builtin_fmaf(static_cast<float>((d >> (4 * n)) & 0xFu), xr[g * gs + 8 * k + n], sd);
+            }
+            const size_t si = static_cast<size_t>(o) * G + g;
+            term = __builtin_fmaf(h2f(sc[si]), sd, __fmul_rn(h2f(bi[si]), xs));
+        }
+        terms[lane] = term;
+        __syncthreads();
+        if (lane == 0) {
+            const int n = G - g0 < 64 ? G - g0 : 64;
+            for (int i = 0; i < n; i++) acc = __fadd_rn(acc, terms[i]);
+        }
+        __syncthreads();
+    }
+    if (lane == 0) out[static_cast<size_t>(m) * n_out + o] = acc;
+}
+
 // h = SiLU(g) * u elementwise (fallback of the fused gate/up launch).
 __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
                                 float* __restrict__ h, long n) {
@@ -447,7 +488,7 @@ struct Workspace {
     float* tmp = nullptr;                       // up-projection rows of the unfused MLP
     void* xbf = nullptr;                        // prefill: bf16 copy of x
     void* part = nullptr;                       // prefill: split-K / stream-K partial sums
-    unsigned* sk = nullptr;                     // prefill: stream-K flags, then its error counter
+    unsigned* sk = nullptr;                     // prefill: stream-K flags, then its control words
     size_t cap[7] = {0, 0, 0, 0, 0, 0, 0};      // bytes, in the order above
     bool in_graph[7] = {false, false, false, false, false, false, false};
     bool fixed = false;
@@ -488,6 +529,9 @@ int grow(Workspace& ws, T*& p, WsBuf which, size_t bytes, hipStream_t st, const 
     cap = bytes;
     return 0;
 }
+
+// The stream-K control words of the workspace: after one flag line per CU.
+unsigned* sk_ctl(Workspace& ws) { return ws.sk + static_cast<size_t>(num_cus()) * 32; }
 
 int ensure_tmp(Workspace& ws, hipStream_t st, size_t n) {
     return grow(ws, ws.tmp, kWsTmp, n * sizeof(float), st, "MLP");
@@ -553,10 +597,8 @@ hipError_t launch_main(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 template <int MR, int RW, bool PAIR, bool NORM, int GSH>
 int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
                      size_t lds, int n_units, int items, hipStream_t st) {
-    const int per_cu = stream_blocks_per_cu<MR, RW, PAIR, NORM, GSH>(nwaves, lds);
-    const int want = (n_units + nwaves - 1) / nwaves;
-    const int cap = num_cus() * per_cu;                 // every workgroup resident at once
-    const int grid = want < cap ? want : cap;
+    // one unit per wave, capped by the launch at what is resident at once
+    const int grid = (n_units + nwaves - 1) / nwaves;
     // ring: a divisor of the unit's items (units change only between rings),
     // two items where they divide it.  Deeper rings were slower on every
     // large shape (same-box, down 18944 -> 3584: 13.5 us at 5 items,
@@ -783,10 +825,68 @@ int gemv_mfma(const q4k::MfMats& mt, bool pair, const float* x, float* out, int 
     return mfma_main(mt, pair, out, m, n, n_in, st, ws);
 }
 
-// GEMV of m (<= kMaxM) rows already on the device: the matrix cores for
-// kMfMinRows..8 rows, else fused when possible.
+// ROWS of the reference build being replaced (kernel/build.sh:7, -DROWS):
+// HETERO_Q4_ROWS, read on first use, or q4_set_rows.  1..64.
+constexpr int kMaxRowsBlock = 64;
+std::atomic<int> g_rows{0};                    // 0: not read yet
+
+int rows_block(int* out) {
+    int r = g_rows.load(std::memory_order_relaxed);
+    if (r == 0) {
+        const char* e = std::getenv("HETERO_Q4_ROWS");
+        char* end = nullptr;
+        const long v = e && *e ? std::strtol(e, &end, 10) : 1;
+        if (e && *e && (*end != 0 || v < 1 || v > kMaxRowsBlock))
+            return fail(Q4_EARG, "HETERO_Q4_ROWS=%s: expected an integer in [1, %d]", e, kMaxRowsBlock);
+        r = static_cast<int>(v);
+        int expect = 0;
+        g_rows.compare_exchange_strong(expect, r, std::memory_order_relaxed);
+        r = g_rows.load(std::memory_order_relaxed);
+    }
+    *out = r;
+    return 0;
+}
+
+// The last n_out % ROWS rows of an m-row GEMV by the reference's fp32 tail
+// path (kernel/q4gemv.c:185-200, rows past the last ROWS block): after the
+// integer path has written every row, they are computed again and
+// overwritten.  Nothing to do for ROWS = 1 or n_out % ROWS == 0.
+int tail_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x, float* out, int m,
+              int n_out, int n_in, int gs, hipStream_t st) {
+    int R = 1;
+    if (int rc = rows_block(&R)) return rc;
+    const int tail = n_out % R;
+    if (tail == 0 || m == 0 || n_in == 0) return 0;
+    hipLaunchKernelGGL(tail_rows_kernel, dim3(tail, m), dim3(64), 0, st, w, s, b, x, out, n_out - tail, n_out, n_in,
+                       gs);
+    HIP_TRY(hipGetLastError());
+    return 0;
+}
+
+// The tail rows of each matrix of a grouped call (each matrix is a q4_gemv
+// call of its own in the reference).
+int multi_tails(int count, const uint32_t* const* w, const uint16_t* const* scales, const uint16_t* const* biases,
+                float* const* out, const int* n_out, const float* x, int m, int n_in, int gs, hipStream_t st) {
+    for (int k = 0; k < count; k++)
+        if (int rc = tail_rows(w[k], scales[k], biases[k], x, out[k], m, n_out[k], n_in, gs, st)) return rc;
+    return 0;
+}
+
+int gemv_rows_int(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
+                  float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws);
+
+// GEMV of m (<= kMaxM) rows already on the device, as the reference build
+// with ROWS = rows_block() computes it: the integer path, then the tail rows.
 int gemv_rows(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
               float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws) {
+    if (int rc = gemv_rows_int(w, s, b, x, out, m, n_out, n_in, gs, st, ws)) return rc;
+    return tail_rows(w, s, b, x, out, m, n_out, n_in, gs, st);
+}
+
+// The integer path for every row: the matrix cores for kMfMinRows..8 rows,
+// else fused when possible.
+int gemv_rows_int(const uint32_t* w, const uint16_t* s, const uint16_t* b, const float* x,
+                  float* out, int m, int n_out, int n_in, int gs, hipStream_t st, Workspace& ws) {
     if (m >= kMfMinRows) {
         const q4k::MfMats mt{{w, w}, {s, s}, {b, b}};
         const int rc = gemv_mfma(mt, false, x, out, m, n_out, n_in, gs, st, ws);
@@ -1230,6 +1330,14 @@ int q4_release_all(void) {
 
 const char* q4_last_error(void) { return g_err; }
 
+int q4_set_rows(int rows) {
+    if (rows < 1 || rows > kMaxRowsBlock) return fail(Q4_EARG, "rows=%d: expected [1, %d]", rows, kMaxRowsBlock);
+    int prev = 1;
+    if (rows_block(&prev)) prev = 1;                 // an unreadable HETERO_Q4_ROWS is replaced
+    g_rows.store(rows, std::memory_order_relaxed);
+    return prev;
+}
+
 int q4_gemv_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const float* x,
                 float* out, int m, int n_out, int n_in, int gs, void* stream) {
     int rc = check_gemv_shape(n_out, n_in, gs);
@@ -1306,7 +1414,7 @@ int q4_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const
         if (ml.row_begin[count] == 0) return 0;
         rc = try_fused_m(ml, x, m, n_in, gs, st);
         if (rc < 0) return rc;
-        if (rc == 1) return 0;
+        if (rc == 1) return multi_tails(count, w, scales, biases, out, n_out, x, m, n_in, gs, st);
     }
     // 3..8 rows on the matrix cores: x prepared once for every matrix
     bool all_mf = m <= kMaxM, any = false;
@@ -1328,7 +1436,7 @@ int q4_gemv_multi_dev(int count, const uint32_t* const* w, const uint16_t* const
             const q4k::MfMats mt{{w[k], w[k]}, {scales[k], scales[k]}, {biases[k], biases[k]}};
             if ((rc = mfma_main(mt, false, out[k], m, n_out[k], n_in, st, *ws)) < 0) return rc;
         }
-        return 0;
+        return multi_tails(count, w, scales, biases, out, n_out, x, m, n_in, gs, st);
     }
     for (int k = 0; k < count; k++)
         if ((rc = q4_gemv_dev(w[k], scales[k], biases[k], x, out[k], m, n_out[k], n_in, gs, stream)))
@@ -1571,13 +1679,15 @@ int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
     const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * ncols;
     if ((rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
     if (plan.sk_p > 0) {
-        const size_t flag_words = static_cast<size_t>(num_cus()) * 32 + 32;
+        // the flags of up to one workgroup per CU (sk_ok: P <= CUs), then the control words
+        const size_t flag_words = static_cast<size_t>(num_cus()) * 32 + kSkCtlWordsHost;
         if ((rc = grow(*ws, ws->part, kWsPart, static_cast<size_t>(plan.sk_p) * 256 * 256 * 4, st, "prefill")))
             return rc;
         const size_t cap_before = ws->cap[kWsSk];
         if ((rc = grow(*ws, ws->sk, kWsSk, flag_words * 4, st, "prefill"))) return rc;
         if (ws->cap[kWsSk] != cap_before) {
-            // flags start at zero once; every launch leaves them at zero
+            // flags and control words start at zero once; every launch
+            // leaves them consistent (the epoch scheme of q4_gemm.hip)
             const long n = static_cast<long>(ws->cap[kWsSk] / 4);
             hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st,
                                reinterpret_cast<float*>(ws->sk), n);
@@ -1592,8 +1702,7 @@ int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
     HIP_TRY(hipGetLastError());
     const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
     if (plan.sk_p > 0) {
-        const size_t words = ws->cap[kWsSk] / 4;
-        return gemm_w4_sk(xb, gm, static_cast<float*>(ws->part), ws->sk, ws->sk + words - 1, m, n_in, plan.sk_p,
+        return gemm_w4_sk(xb, gm, static_cast<float*>(ws->part), ws->sk, sk_ctl(*ws), m, n_in, plan.sk_p,
                           plan.sk_nx, st);
     }
     const int S = plan.S, kt_split = (n_in / 64 + S - 1) / S;
@@ -1634,6 +1743,29 @@ int q4_dequant_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_
     if (reinterpret_cast<uintptr_t>(out) & 15) return fail(Q4_EARG, "out must be 16-byte aligned");
     return dequant_launch<true>(w, scales, biases, out, row0, row1 - row0, n_in, gs,
                                 static_cast<hipStream_t>(stream));
+}
+
+int q4_prefill_errors(void* stream) {
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    unsigned* ctl = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mu);
+        int dev;
+        if (int rc = current_device(&dev)) return rc;
+        auto d = g_dev.find(dev);
+        if (d == g_dev.end()) return 0;
+        auto w = d->second.ws.find(st);
+        if (w == d->second.ws.end() || !w->second.sk) return 0;
+        ctl = sk_ctl(w->second);
+    }
+    HIP_TRY(hipStreamSynchronize(st));
+    unsigned n = 0;
+    HIP_TRY(hipMemcpy(&n, ctl + kSkCtlErrorsHost, sizeof(n), hipMemcpyDeviceToHost));
+    if (n) {
+        const unsigned zero = 0;
+        HIP_TRY(hipMemcpy(ctl + kSkCtlErrorsHost, &zero, sizeof(zero), hipMemcpyHostToDevice));
+    }
+    return static_cast<int>(n);
 }
 
 }  // extern "C"

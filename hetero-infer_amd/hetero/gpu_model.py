@@ -189,7 +189,8 @@ class GpuStage:
 
     def capture(self):
         """Run one step eagerly (sizes every workspace), restore the state and
-        capture the step as a HIP graph."""
+        capture the step as a HIP graph.  The decode state (token, position,
+        caches, steps taken) is what it was before the call."""
         torch = self.torch
         tok0, pos0 = self.tok.clone(), self.pos.clone()
         caches = [(L["k_cache"].clone(), L["v_cache"].clone()) for L in self.layers]
@@ -206,7 +207,6 @@ class GpuStage:
         with torch.cuda.graph(self.graph, stream=self.stream):
             self._step()
         torch.cuda.synchronize()
-        self.steps_done = 0
 
     def set_token(self, tok: int):
         self.tok.fill_(int(tok))

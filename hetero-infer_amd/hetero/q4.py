@@ -21,7 +21,9 @@ LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
 
 EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
            "q4_last_error", "q4_gemv_dev", "q4_gemv_noalloc_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
-           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_gemm_bf16_multi_dev", "q4_dequant_dev", "q4_dequant_bf16_dev",
+           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_gemm_bf16_multi_dev", "q4_set_rows", "q4_prefill_errors",
+           "q4_dequant_dev",
+           "q4_dequant_bf16_dev",
            # decode-step kernels (include/q4decode.h)
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
            "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev",
@@ -65,6 +67,10 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_gemm_bf16_dev.restype = _I
         lib.q4_gemm_bf16_multi_dev.argtypes = [_I] + [_VP] * 6 + [_I] * 3 + [_VP]
         lib.q4_gemm_bf16_multi_dev.restype = _I
+        lib.q4_set_rows.argtypes = [_I]
+        lib.q4_set_rows.restype = _I
+        lib.q4_prefill_errors.argtypes = [_VP]
+        lib.q4_prefill_errors.restype = _I
         lib.q4_dequant_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
         lib.q4_dequant_dev.restype = _I
         lib.q4_dequant_bf16_dev.argtypes = [_VP] * 4 + [_I] * 4 + [_VP]
@@ -322,6 +328,26 @@ def gemm_bf16_multi_dev(mats, x, outs=None, stream=None, lib=None):
                                     _ptr(x2), m, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gemm_bf16_multi_dev")
     return outs
+
+
+def set_rows(rows: int, lib=None) -> int:
+    """The reference build's ROWS whose fp32 tail rows the plain GEMV entry
+    points reproduce (kernel/q4gemv.c:185-200); returns the previous value."""
+    lib = lib or load()
+    prev = lib.q4_set_rows(int(rows))
+    if prev < 0:
+        check(lib, prev, "q4_set_rows")
+    return prev
+
+
+def prefill_errors(stream=None, lib=None) -> int:
+    """Stream-K partial sums on `stream` that missed their bounded wait since
+    the last call (0 in a correct run); synchronises the stream."""
+    lib = lib or load()
+    rc = lib.q4_prefill_errors(_stream(stream))
+    if rc < 0:
+        check(lib, rc, "q4_prefill_errors")
+    return rc
 
 
 def dequant_dev(w, scales, biases, row0=0, row1=None, out=None, bf16=False, stream=None, lib=None):

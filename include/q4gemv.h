@@ -17,7 +17,13 @@
  * (x quantised to int16 once per call, exact integer dot per group, groups
  * accumulated in ascending order as acc + fma(scale, xscale*dot, bias*xsum)),
  * i.e. the reference built with ROWS=1 -- and with any ROWS when
- * n_out % ROWS == 0.
+ * n_out % ROWS == 0.  To replace a build tuned to another ROWS (its
+ * kernel/tuning.json "rows"), set HETERO_Q4_ROWS=<rows> (read on first use)
+ * or call q4_set_rows: the last n_out % ROWS rows of each matrix then take
+ * the reference's fp32 tail path (kernel/q4gemv.c:185-200), in q4_gemv,
+ * q4_gemv_batched, q4_gemv_dev, q4_gemv_noalloc_dev and q4_gemv_multi_dev.
+ * The fused and chained entry points (gate/up SiLU, MLP, norm prologue,
+ * chained programs) always compute every row by the integer path.
  */
 #ifndef HETERO_AMD_Q4GEMV_H
 #define HETERO_AMD_Q4GEMV_H
@@ -163,6 +169,21 @@ int q4_gemm_bf16_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *
 int q4_gemm_bf16_multi_dev(int count, const uint32_t *const *w, const uint16_t *const *scales,
                            const uint16_t *const *biases, float *const *out, const int *n_out,
                            const float *x, int m, int n_in, int gs, void *stream);
+
+/* Set the reference ROWS whose tail rows the plain GEMV entry points
+ * reproduce (1..64; 1 = every row by the integer path).  Returns the
+ * previous setting, or Q4_EARG.  No counterpart in the reference's ABI: the
+ * reference fixes ROWS when it is built (kernel/build.sh:7, -DROWS) and its
+ * autotuner picks it (kernel/autotune.py:52-63).  Affects later calls only;
+ * not to be changed while calls run on other threads. */
+int q4_set_rows(int rows);
+
+/* Synchronise `stream` and return how many stream-K partial sums of the
+ * prefill calls on it did not arrive within their bounded wait since the
+ * last call (0 in a correct run; each such tile was stored as NaN), then
+ * clear the count.  No counterpart in the reference: its prefill is one
+ * BLAS call (hetero/cpu_model.py:135), which cannot time out. */
+int q4_prefill_errors(void *stream);
 
 /* Device q4_dequant: rows [row0,row1) to fp32 [row1-row0][n_in]. */
 int q4_dequant_dev(const uint32_t *w, const uint16_t *scales, const uint16_t *biases,

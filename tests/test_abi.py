@@ -77,6 +77,29 @@ def test_shape_errors_before_any_device_call(lib):
     assert lib.q4_dequant_dev(*d, 0, 2, 256, 12, None) == -1
 
 
+def test_set_rows_rejects_and_restores(lib):
+    """ROWS outside [1, 64] is refused (no device call) and leaves the
+    setting alone; a valid one returns the previous setting."""
+    prev = q4.set_rows(1, lib)
+    for bad in (0, -1, 65):
+        assert lib.q4_set_rows(bad) == q4.Q4_EARG
+    assert q4.set_rows(4, lib) == 1
+    assert q4.set_rows(prev, lib) == 4
+
+
+def test_rows_env_is_read_on_first_use(tmp_path):
+    """HETERO_Q4_ROWS sets the ROWS of the reference build being replaced;
+    a value outside [1, 64] is reported by the first call that needs it."""
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, {pkg!r}); from hetero import q4; lib = q4.load(); "
+            "print(lib.q4_set_rows(1))").format(pkg=os.path.join(ROOT, "hetero-infer_amd"))
+    for env, want in (("8", "8"), ("1", "1"), ("0", "1"), ("x", "1")):
+        out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                             env=dict(os.environ, HETERO_Q4_ROWS=env), check=True).stdout.strip()
+        assert out == want, (env, out)
+
+
 def test_argument_errors(lib):
     assert lib.q4_gemv(None, None, None, None, None, 4, 256, 64, 1) == q4.Q4_EARG
     assert "null" in q4.last_error(lib)

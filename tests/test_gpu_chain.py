@@ -83,10 +83,12 @@ def test_dependent_qwen_layers_bit_exact():
     (832, (300, 40), False),            # 13 groups, partial chunk, two matrices
     (3584, (96, 64, 8, 40), False),     # four matrices of uneven rows: ring 2
     (6144, (200,), False),              # three chunks: ring 1
-    (18944, (3584,), False),            # ten chunks: ring 5
+    (18944, (3584,), False),            # ten chunks: ring 2
+    (9216, (1000,), False),             # five chunks: ring 5
     (24576, (64,), False),              # the longest row: twelve chunks
+    (3584, (152064,), False),           # lm_head: eight rows per unit, ring 2
     (2048, (1000, 1000), True),         # gate/up, one chunk: ring 2
-    (3584, (18944, 18944), True),       # gate/up, Qwen shape: ring 4
+    (3584, (18944, 18944), True),       # gate/up, Qwen shape: two rows per unit, ring 2
     (320, (48, 48), True),              # gate/up, five groups
 ])
 def test_phase_shapes_vs_separate_launches(n_in, counts, pair):
@@ -156,3 +158,55 @@ def test_graph_replays_and_barrier_reset():
     assert all(np.array_equal(bits(b), w) for b, w in zip(bufs, want))
     assert ch.errors() == 0
     ch.close()
+
+
+def test_headline_sweep_at_full_size():
+    """The benchmark's headline program at the size it is timed: the 113
+    phases of the Qwen2.5-7B sweep (28 layers of distinct weights generated
+    on the GPU, q/k/v, o, gate+up and down each, plus lm_head's 152,064
+    rows at eight rows per unit) in one chained launch, twice.  Every
+    phase's outputs are bit-identical to the same phase run as its own
+    launch; layers 0 and 27 and lm_head are bit-exact against the oracle."""
+    import torch
+    from hetero import sweep
+    dev = torch.device("cuda:0")
+    layers, head, xs = sweep.make_model(torch, dev, seed=1234)
+    phases = sweep.phases(layers, head, xs, sweep.distinct_outputs(torch, dev))
+    assert len(phases) == 113
+    ch = q4.Chain(phases)
+    ch.run()
+    torch.cuda.synchronize()
+    assert ch.errors() == 0
+    first = [[t.clone() for t in ph[2]] for ph in phases]
+    for ph in phases:
+        for t in ph[2]:
+            t.fill_(float("nan"))
+    ch.run()
+    torch.cuda.synchronize()
+    assert ch.errors() == 0
+    ch.close()
+    for p, ph in enumerate(phases):
+        for k, t in enumerate(ph[2]):
+            assert torch.equal(t.view(torch.int32), first[p][k].view(torch.int32)), f"run 2, phase {p} matrix {k}"
+    check = sweep.phases(layers, head, xs, sweep.distinct_outputs(torch, dev))
+    sweep.run_launches(check, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert sweep.mismatches(torch, phases, check) == []
+    o = oracle.Oracle()
+    xh = {n: t.cpu().numpy()[0] for n, t in xs.items()}
+
+    def host(wsb):
+        w, sc, b = (t.cpu().numpy() for t in wsb)
+        return w.view(np.uint32), sc.view(np.float16), b.view(np.float16)
+
+    for l in (0, 27):
+        for j, idx in enumerate(sweep.LAYER_PHASES):
+            ph = phases[4 * l + j]
+            for k, i in enumerate(idx):
+                _, n_in, n_out = sweep.LAYER_SHAPES[i]
+                print(f"layer {l} {sweep.LAYER_SHAPES[i][0]}", flush=True)
+                want = o.gemv(*host(layers[l][i]), xh[n_in], 64)
+                assert np.array_equal(bits(ph[2][k])[0], want.view(np.uint32)), f"layer {l} projection {i}"
+    print("lm_head", flush=True)
+    want = o.gemv(*host(head), xh[3584], 64)
+    assert np.array_equal(bits(phases[-1][2][0])[0], want.view(np.uint32))

@@ -74,6 +74,44 @@ def test_small_golden_dev_abi(lib, manifest, small):
         assert_bit_exact(out.cpu().numpy()[0], small[f"{name}.out_rows1"], name)
 
 
+@pytest.mark.parametrize("rows", [2, 4, 8])
+def test_rows_tail_golden(lib, manifest, small, rows):
+    """With the reference build's ROWS set (q4_set_rows), the last
+    n_out % ROWS rows take its fp32 tail path (kernel/q4gemv.c:185-200):
+    bit-exact against the reference compiled with that ROWS, through the
+    host ABI, the device ABI at 1 and 3 rows of x (streaming and
+    matrix-core paths) and grouped calls of two matrices."""
+    import torch
+    o = oracle.Oracle()
+    prev = q4.set_rows(rows, lib)
+    try:
+        for name in gemv_cases(manifest):
+            p = manifest["cases"][name]["params"]
+            w, s, b, x = (small[f"{name}.{k}"] for k in ("w", "scales", "biases", "x"))
+            gs = p["gs"]
+            print(f"case {name} {p} rows {rows}", flush=True)
+            want = small[f"{name}.out_rows{rows}"]
+            assert_bit_exact(q4.gemv_host(lib, w, s.view(np.uint16), b.view(np.uint16), x, gs), want,
+                             f"{name} host")
+            x3 = np.stack([x, synth.activations(130 + rows, 1, x.size)[0], -x])
+            want3 = np.stack([o.gemv(w, s, b, xr, gs, rows_block=rows) for xr in x3])
+            assert_bit_exact(want3[0], want, f"{name} oracle")
+            tw, ts, tb = (torch.from_numpy(np.ascontiguousarray(a)).cuda()
+                          for a in (w, s.view(np.int16), b.view(np.int16)))
+            tx3 = torch.from_numpy(x3).cuda()
+            for m in (1, 3):
+                got = q4.gemv_dev(tw, ts, tb, tx3[:m])
+                got2 = q4.gemv_multi_dev([(tw, ts, tb), (tw, ts, tb)], tx3[:m])
+                torch.cuda.synchronize()
+                assert_bit_exact(got.cpu().numpy(), want3[:m], f"{name} dev m={m}")
+                for k, g in enumerate(got2):
+                    assert_bit_exact(g.cpu().numpy(), want3[:m], f"{name} multi m={m} matrix {k}")
+            lib.q4_release(w.ctypes.data)
+    finally:
+        q4.set_rows(prev, lib)
+    assert q4.set_rows(1, lib) == 1
+
+
 def test_return_codes(lib, manifest):
     """Invalid shapes give the reference's return codes."""
     rcs = manifest["return_codes"]
@@ -245,6 +283,28 @@ def test_dev_all_m_and_paths(lib):
             got = q4.gemv_dev(tw, ts, tb, tx[:m].contiguous())
             torch.cuda.synchronize()
             assert_bit_exact(got.cpu().numpy(), want[:m], f"K={k_in} m={m}")
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+def test_one_row_five_item_ring(lib, gs):
+    """One row at n_in = 9216 (five chunks of 256 words, one row per unit:
+    the streaming kernel's five-item ring) and at 8200 (a partial fifth
+    chunk), bit-exact vs the oracle, through q4_gemv_dev and a grouped call."""
+    import torch
+    o = oracle.Oracle()
+    for n_in, n_out in ((9216, 1000), (9216, 37), (8192 + gs, 300)):
+        print(f"n_in {n_in} n_out {n_out} gs {gs}", flush=True)
+        w, s, b = synth.qlinear(140 + n_in + gs + n_out, n_out, n_in, gs)
+        x = synth.activations(141 + n_in, 1, n_in)
+        want = o.gemv(w, s, b, x[0], gs)
+        tw, ts, tb, tx = (torch.from_numpy(np.ascontiguousarray(a)).cuda()
+                          for a in (w, s.view(np.int16), b.view(np.int16), x))
+        got = q4.gemv_dev(tw, ts, tb, tx)
+        got2 = q4.gemv_multi_dev([(tw, ts, tb), (tw, ts, tb)], tx)
+        torch.cuda.synchronize()
+        assert_bit_exact(got.cpu().numpy()[0], want, f"dev n_in={n_in}")
+        for g in got2:
+            assert_bit_exact(g.cpu().numpy()[0], want, f"multi n_in={n_in}")
 
 
 def test_matrix_core_tile_variants(lib):

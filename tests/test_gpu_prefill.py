@@ -116,12 +116,15 @@ def test_gemm_bf16_stream_k(monkeypatch, m, n_out, n_in, ps):
         assert np.isfinite(got).all(), "a tile's partials did not arrive"
         assert oracle.normwise_rel(got, exact) < EXACT_OPERAND_TOL
         assert torch.equal(a, b2), "stream-K sums in a fixed order: runs agree bit for bit"
+        assert q4.prefill_errors() == 0, "a partial missed its wait"
     _plan(monkeypatch, None)
 
 
 def test_gemm_bf16_stream_k_graph_replays(monkeypatch):
-    """Owners lower the flags they consume, so a captured stream-K launch
-    replays correctly: every replay equals the eager result bit for bit."""
+    """Each launch waits for flags carrying its own epoch, which the launch
+    before it advanced, so a captured stream-K launch replays correctly:
+    every replay equals the eager result bit for bit, and no partial ever
+    misses its wait."""
     import torch
     m, n_out, n_in = 512, 3584, 3584
     (tw, ts, tb, tx), exact = _operands(760, m, n_out, n_in)
@@ -143,6 +146,7 @@ def test_gemm_bf16_stream_k_graph_replays(monkeypatch):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {r}"
         q4.gemm_bf16_dev(tw, ts, tb, tx)                # eager work between replays
+    assert q4.prefill_errors(stream=s) == 0 and q4.prefill_errors() == 0
     assert oracle.normwise_rel(eager.cpu().numpy(), exact) < EXACT_OPERAND_TOL
     _plan(monkeypatch, None)
 
