@@ -736,6 +736,41 @@ def cpu_decode_baseline(cfg, meta, hw, hks, hvs, rows, threads, steps=4):
             "sample": f"oracle/decode.py on kernel/q4gemv.c ROWS={rows}, {threads} threads, {steps} timed steps"}
 
 
+def chain_stamp_table(torch, chain, n_phases, dev, stream, reps=3):
+    """Per-phase event times of the chained sweep (q4_chain_stamps, 100 MHz
+    clock), per phase kind: medians over workgroups and layers, in
+    microseconds, of each step of a phase -- the wait at the grid barrier
+    before it, x loaded and staged, the int16 planes, wave 0's items, every
+    wave's items and stores -- and the latency from the last workgroup's
+    arrival to the first one's release."""
+    import numpy as np
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    buf = torch.zeros((n_phases + 1) * cus * 8, dtype=torch.int64, device=dev)
+    chain.stamps(buf)
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            chain.run(stream=stream)
+    torch.cuda.synchronize()
+    chain.stamps(None)
+    t = buf.cpu().numpy().reshape(n_phases + 1, cus, 8).astype(np.float64) / 100.0   # us
+    kinds = ["qkv", "o", "gate_up", "down"]
+    rows = {}
+    for p in range(1, n_phases):
+        kind = "lm_head" if p == n_phases - 1 else kinds[p % 4]
+        arrived, released, staged, planes, wave0 = (t[p, :, i] for i in range(1, 6))
+        nxt = t[p + 1, :, 1]
+        r = rows.setdefault(kind, {k: [] for k in ("barrier_wait", "release_after_last_arrival", "x_staged",
+                                                   "planes", "items_wave0", "items_and_stores", "phase")})
+        r["barrier_wait"].append(np.median(released - arrived))
+        r["release_after_last_arrival"].append(released.min() - arrived.max())
+        r["x_staged"].append(np.median(staged - released))
+        r["planes"].append(np.median(planes - staged))
+        r["items_wave0"].append(np.median(wave0 - planes))
+        r["items_and_stores"].append(np.median(nxt - planes))
+        r["phase"].append(np.median(nxt - arrived))
+    return {k: {kk: round(float(np.median(vv)), 3) for kk, vv in v.items() if vv} for k, v in rows.items()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -756,6 +791,8 @@ def main():
                     help="only the grouped decode sweep (for rocprof runs)")
     ap.add_argument("--chain-only", action="store_true",
                     help="only the decode sweep as one chained program (for rocprof runs)")
+    ap.add_argument("--chain-stamps", action="store_true",
+                    help="with --chain-only: also the per-phase event times of the chained sweep")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the M=512 prefill leg (for counter runs)")
     ap.add_argument("--small-m-only", action="store_true",
@@ -911,6 +948,7 @@ def main():
 
         chain_ms, chain_ev = timed(step_chain, args.steps, args.warmup)
         chain_errors = chain.errors()
+        stamp_table = chain_stamp_table(torch, chain, len(phases), dev, stream) if args.chain_stamps else None
         chain.close()
         check = sweep.phases(layers, head, xs, sweep.distinct_outputs(torch, dev))
         with torch.cuda.stream(stream):
@@ -923,6 +961,8 @@ def main():
                                            "values_checked": int(sum(o.numel() for ph in phases for o in ph[2])),
                                            "phases_differing": len(chain_bad),
                                            "first_differences": chain_bad[:5]}}
+        if stamp_table is not None:
+            chained["phase_events_us"] = stamp_table
         del phases, check
     use_chain = chain_errors == 0 and chain_bad == []
     if not use_chain and args.chain_only:

@@ -43,6 +43,14 @@ constexpr int kChainMaxIn = kChainRounds * kChainWaves * 64 * 8;
 constexpr size_t kChainLdsFloor = 81 * 1024;  // > half the CU's LDS: one workgroup per CU
 constexpr int kStoreDevice = 16;              // cache policy sc1: device-scope coherent
 constexpr long long kChainSpinTicks = 2000000;  // 20 ms of the 100 MHz clock per barrier wait
+// Event times a plan can record (q4_chain_stamps), per phase and workgroup,
+// kChainStamps words each: 1 the workgroup done with the phase before (its
+// waves' stores complete) and arriving at the barrier, 2 the barrier
+// released, 3 x staged in LDS, 4 the int16 planes ready, 5 wave 0 done with
+// its items.  Kept in LDS during the phase (words 2..5) and written out by
+// thread 0 at the next arrival.
+constexpr int kChainStamps = 8;
+constexpr int kChainLdsHead = 80;             // the failure flag, then 8 event words
 
 struct ChainPhase {
     MatList ml;
@@ -114,10 +122,27 @@ __device__ __forceinline__ void wait_own_stores() {
     __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
+// Event e of the current phase, in LDS (thread 0).
+__device__ __forceinline__ void chain_event(unsigned long long* stamps, unsigned long long* st, int e) {
+    if (stamps && threadIdx.x == 0) st[e] = __builtin_amdgcn_s_memrealtime();
+}
+
+// The phase's events out of LDS, and event 1 (the arrival) of phase p + 1.
+__device__ __forceinline__ void chain_flush_events(unsigned long long* stamps, const unsigned long long* st, int p) {
+    if (stamps && threadIdx.x == 0) {
+        unsigned long long* row = stamps + (static_cast<size_t>(p) * gridDim.x + blockIdx.x) * kChainStamps;
+        for (int e = 2; e <= 5; e++) row[e] = st[e];
+        stamps[(static_cast<size_t>(p + 1) * gridDim.x + blockIdx.x) * kChainStamps + 1] =
+            __builtin_amdgcn_s_memrealtime();
+    }
+}
+
 // Workgroup b's arrival at barrier k (after phase k-1): every wave has waited
 // for its stores; one atomic per workgroup, no return value needed.
-__device__ __forceinline__ void chain_arrive(ChainSync* s) {
+__device__ __forceinline__ void chain_arrive(ChainSync* s, unsigned long long* stamps, const unsigned long long* st,
+                                             int p) {
     lds_barrier();
+    chain_flush_events(stamps, st, p);
     if (threadIdx.x == 0)
         __hip_atomic_fetch_add(&s->group[blockIdx.x / kChainGroup][0], 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -162,7 +187,8 @@ __device__ __forceinline__ void chain_wait(ChainSync* s, unsigned k, int* failed
 // arrival at the next barrier.
 template <int RING, bool PAIR>
 __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
-                                            int* failed, uint4* lds4, bool arrive_after) {
+                                            int* failed, uint4* lds4, bool arrive_after,
+                                            unsigned long long* stamps, unsigned long long* st) {
     constexpr int lpg = 2;                                        // lanes per group in an item
     constexpr int WPG = 8;                                        // packed words per group
     const float* __restrict__ x = ph->x;
@@ -204,6 +230,7 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     // ---- 2. every workgroup is done with the phases before (x may be one
     //         of their outputs)
     if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
+    chain_event(stamps, st, 2);
 
     // ---- 3. x: device-scope loads, thread t owns words t, t + nt, t + 2nt
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(n_in) * 4u);
@@ -237,6 +264,7 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
         amax = wave_max(amax);
         if (lane == 0) red[wave] = amax;
         __syncthreads();
+        chain_event(stamps, st, 3);
         // one lane per group adds its 64 values in ascending order
         for (int g = tid; g < G; g += nt)
             xsum_lds[g] = chain_add<32>(chain_add<32>(0.0f, xstage + g * SS), xstage + g * SS + 32);
@@ -276,6 +304,7 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
         }
     }
     __syncthreads();
+    chain_event(stamps, st, 4);
 
     // ---- 4. the item stream (as gemv_stream_kernel)
     constexpr int GPC = kChunkWords / WPG;                        // groups per chunk
@@ -399,18 +428,26 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
         finish(cu_unit);
     }
 
+    chain_event(stamps, st, 5);
+
     // ---- 5. this wave's stores are done; the workgroup arrives at the next
     //         barrier (the LDS of this phase is free once every wave is past it)
     wait_own_stores();
-    if (arrive_after) chain_arrive(sync);
-    else lds_barrier();
+    if (arrive_after) {
+        chain_arrive(sync, stamps, st, p);
+    } else {
+        lds_barrier();
+        chain_flush_events(stamps, st, p);
+    }
 }
 
 __global__ __launch_bounds__(64 * kChainWaves) void gemv_chain_kernel(const ChainPhase* __restrict__ phases,
-                                                                      int n_phases, ChainSync* __restrict__ sync) {
+                                                                      int n_phases, ChainSync* __restrict__ sync,
+                                                                      unsigned long long* __restrict__ stamps) {
     extern __shared__ uint4 lds_all[];
     int* failed = reinterpret_cast<int*>(lds_all);               // read and written by thread 0 only
-    uint4* lds4 = lds_all + 1;
+    unsigned long long* st = reinterpret_cast<unsigned long long*>(lds_all + 1);   // this phase's events
+    uint4* lds4 = lds_all + kChainLdsHead / 16;
     if (threadIdx.x == 0) *failed = 0;
     CPhase* table = (CPhase*)phases;
     for (int p = 0; p < n_phases; p++) {
@@ -418,16 +455,16 @@ __global__ __launch_bounds__(64 * kChainWaves) void gemv_chain_kernel(const Chai
         const int pair = ph->pair, ring = ph->ring;               // uniform
         const bool arrive = p + 1 < n_phases;
         if (pair) {
-            if (ring == 4) chain_phase<4, true>(ph, p, sync, failed, lds4, arrive);
-            else chain_phase<2, true>(ph, p, sync, failed, lds4, arrive);
+            if (ring == 4) chain_phase<4, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            else chain_phase<2, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 1) {
-            chain_phase<1, false>(ph, p, sync, failed, lds4, arrive);
+            chain_phase<1, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 2) {
-            chain_phase<2, false>(ph, p, sync, failed, lds4, arrive);
+            chain_phase<2, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 4) {
-            chain_phase<4, false>(ph, p, sync, failed, lds4, arrive);
+            chain_phase<4, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else {
-            chain_phase<5, false>(ph, p, sync, failed, lds4, arrive);
+            chain_phase<5, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         }
     }
     // every workgroup is past its last barrier wait once it gets here; the
@@ -451,6 +488,7 @@ struct q4_chain_plan {
     int n_phases = 0;
     int grid = 0;
     size_t lds = 0;
+    unsigned long long* stamps = nullptr;
     ChainPhase* d_phases = nullptr;
     ChainSync* d_sync = nullptr;
 };
@@ -509,7 +547,7 @@ int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) 
     if (!ring) return fail(Q4_EARG, "no ring size divides %d items", items);
     out.UB = UB;
     out.ring = ring;
-    const size_t need = 16 + stream_lds_bytes(1, C, G, kChainWaves, mult * UB, kChainRounds, 0);
+    const size_t need = kChainLdsHead + stream_lds_bytes(1, C, G, kChainWaves, mult * UB, kChainRounds, 0);
     if (need > lds) lds = need;
     return 0;
 }
@@ -578,9 +616,17 @@ int q4_chain_run(q4_chain_plan* plan, void* stream) {
     hipGetDevice(&dev);
     if (dev != plan->device) return fail(Q4_EARG, "plan made on device %d, current device %d", plan->device, dev);
     hipLaunchKernelGGL(gemv_chain_kernel, dim3(plan->grid), dim3(64 * kChainWaves), plan->lds,
-                       static_cast<hipStream_t>(stream), plan->d_phases, plan->n_phases, plan->d_sync);
+                       static_cast<hipStream_t>(stream), plan->d_phases, plan->n_phases, plan->d_sync, plan->stamps);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "chain launch: %s", hipGetErrorString(e));
+    return 0;
+}
+
+int q4_chain_stamps(q4_chain_plan* plan, unsigned long long* stamps, long words) {
+    if (!plan) return fail(Q4_EARG, "null plan");
+    const long need = static_cast<long>(plan->n_phases + 1) * plan->grid * kChainStamps;
+    if (stamps && words < need) return fail(Q4_EARG, "stamps: %ld words, the plan records %ld", words, need);
+    plan->stamps = stamps;
     return 0;
 }
 

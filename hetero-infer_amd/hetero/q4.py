@@ -31,7 +31,7 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            # activation wire codec (include/q4wire.h)
            "q4_wire_payload_bytes", "q4_wire_encode_dev", "q4_wire_decode_dev",
            # chained GEMV programs (include/q4chain.h)
-           "q4_chain_create", "q4_chain_run", "q4_chain_errors", "q4_chain_destroy")
+           "q4_chain_create", "q4_chain_run", "q4_chain_stamps", "q4_chain_errors", "q4_chain_destroy")
 
 Q4_EHIP, Q4_ENOMEM, Q4_EARG = -2, -3, -4
 
@@ -109,6 +109,8 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_chain_create.restype = _I
         lib.q4_chain_run.argtypes = [_VP, _VP]
         lib.q4_chain_run.restype = _I
+        lib.q4_chain_stamps.argtypes = [_VP, _VP, _L]
+        lib.q4_chain_stamps.restype = _I
         lib.q4_chain_errors.argtypes = [_VP]
         lib.q4_chain_errors.restype = _I
         lib.q4_chain_destroy.argtypes = [_VP]
@@ -393,6 +395,12 @@ class Chain:
 
     def run(self, stream=None):
         check(self.lib, self.lib.q4_chain_run(self._plan, _stream(stream)), "q4_chain_run")
+
+    def stamps(self, buf):
+        """Record per-phase event times (include/q4chain.h: q4_chain_stamps)
+        into the int64 device tensor `buf` on later runs; None stops."""
+        check(self.lib, self.lib.q4_chain_stamps(self._plan, None if buf is None else _ptr(buf),
+                                                 0 if buf is None else buf.numel()), "q4_chain_stamps")
 
     def errors(self) -> int:
         """Barrier waits that ran out of time since the last call (synchronises)."""

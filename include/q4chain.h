@@ -56,6 +56,17 @@ int q4_chain_create(const q4_chain_phase *phases, int n_phases, q4_chain_plan **
 /* Run every phase, in order, in one launch on `stream`. */
 int q4_chain_run(q4_chain_plan *plan, void *stream);
 
+/* Measurement: with `stamps` a device buffer of at least
+ * (n_phases + 1) * workgroups * 8 words (workgroups = the device's CU count),
+ * later runs record, for each phase p and workgroup b, the 100 MHz clock
+ * (s_memrealtime) at stamps[(p * workgroups + b) * 8 + e] for the events
+ * e = 1: the workgroup done with phase p - 1 (every wave's stores complete),
+ * arriving at the grid barrier; 2: the barrier released; 3: p's x staged in
+ * LDS; 4: p's int16 planes ready; 5: wave 0 done with its items of p (row
+ * n_phases holds event 1 only: the end).  NULL stops recording.  Returns
+ * Q4_EARG when `words` is too small. */
+int q4_chain_stamps(q4_chain_plan *plan, unsigned long long *stamps, long words);
+
 /* Synchronise the device and return how many barrier waits ran out of time
  * since the last call (0 in a correct run; then clears the count and the
  * barrier state).  A run with a nonzero count produced invalid outputs. */
