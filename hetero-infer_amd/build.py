@@ -5,7 +5,8 @@ kernel (hetero/cpu_model.py:35-37: <package parent>/kernel/libq4gemv.so), so
 hetero/cpu_model.py here loads it the same way.
 
 csrc/q4gemv.hip (host code, C-ABI and the other kernels), csrc/q4_decode.hip
-(the decode-step kernels of include/q4decode.h), csrc/q4_chain.hip (the
+(the decode-step kernels of include/q4decode.h), csrc/q4_prompt.hip (the
+prompt forward's causal attention, also include/q4decode.h), csrc/q4_chain.hip (the
 chained GEMV programs of include/q4chain.h), csrc/q4_gemm.hip (the prefill
 GEMM) and the instances of the
 streaming GEMV kernel (csrc/q4_stream_inst.hip, once per activation rows x
@@ -26,6 +27,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 SRC = os.path.join(CSRC, "q4gemv.hip")
 DECODE = os.path.join(CSRC, "q4_decode.hip")
+PROMPT = os.path.join(CSRC, "q4_prompt.hip")
 WIRE = os.path.join(CSRC, "q4_wire.hip")
 CHAIN = os.path.join(CSRC, "q4_chain.hip")
 GEMM = os.path.join(CSRC, "q4_gemm.hip")
@@ -70,6 +72,7 @@ def build(verbose: bool = False, jobs: int | None = None, out: str = OUT, define
     jobs = jobs or min(16, os.cpu_count() or 4)
     with tempfile.TemporaryDirectory(prefix="q4build") as tmpd:
         units = [(SRC, os.path.join(tmpd, "q4gemv.o"), []), (DECODE, os.path.join(tmpd, "q4_decode.o"), []),
+                 (PROMPT, os.path.join(tmpd, "q4_prompt.o"), []),
                  (WIRE, os.path.join(tmpd, "q4_wire.o"), []), (CHAIN, os.path.join(tmpd, "q4_chain.o"), []),
                  (GEMM, os.path.join(tmpd, "q4_gemm.o"), [])]
         for mr, pair, ring, gsh in STREAM_INSTANCES:

@@ -77,6 +77,14 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __fadd_rn(__fadd_rn(__fadd_rn(r0, r1), r2), r3);
 }
 
+// SiLU(g) * u as hetero/cpu_model.py:169-170 and :291-292 compute it in
+// fp32: g / (1 + exp(-g)) * u (expf here; NumPy's float32 exp may differ in
+// the last place).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = expf(-g);
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+}
+
 // 1 / sqrt(mean + eps) of RMSNorm from the sum of squares of n values
 // (hetero/cpu_model.py:164-166).
 __device__ __forceinline__ float rms_factor(float sum_sq, int n, float eps) {

@@ -26,11 +26,13 @@ __device__ __forceinline__ float h2f_bits(uint16_t h) {
 // ------------------------------------------------------------ embedding ---
 // hetero/cpu_model.py:334-338 (Stage.embed) / :67-81 (dequantize):
 // value 8j+n of the row = q * scale + bias with q * scale exact, so one fma.
+// Token blockIdx.y of tok[] into row blockIdx.y of out.
 __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ sc,
                                                     const uint16_t* __restrict__ bi, const int64_t* __restrict__ tok,
                                                     float* __restrict__ out, int n_rows, int n_in, int gs) {
     const int wpr = n_in >> 3, G = n_in / gs;
-    const int64_t t = *tok;
+    const int64_t t = tok[blockIdx.y];
+    out += static_cast<size_t>(blockIdx.y) * n_in;
     const int row = (t >= 0 && t < n_rows) ? static_cast<int>(t) : (t < 0 ? 0 : n_rows - 1);
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= wpr) return;
@@ -47,7 +49,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 
 // ------------------------------------------------ residual add + RMSNorm ---
 // hetero/cpu_model.py:164-166: x * (1 / sqrt(mean(x * x) + eps)) * w, after
-// the residual add of :304-306.  One workgroup; n <= 8 * 1024.  Thread t
+// the residual add of :304-306.  One workgroup per row (blockIdx.x of
+// [rows][n]); n <= 8 * 1024.  Thread t
 // owns the 8 consecutive values of word t and adds their squares in order;
 // the wave sums (wave_sum) are added in wave order.  The streaming GEMV's
 // norm prologue sums in exactly this order, so its input is y bit for bit.
@@ -58,6 +61,10 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x
     __shared__ float red[16];
     const int tid = threadIdx.x, nt = blockDim.x;
     const int i0 = tid * kNormPer;
+    const size_t row = static_cast<size_t>(blockIdx.x) * n;
+    x += row;
+    y += row;
+    if (delta) delta += row;
     float v[kNormPer];
     float ss = 0.0f;
 #pragma unroll
@@ -91,13 +98,19 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x
 // hetero/cpu_model.py:156-157 (bias), :195-204 (RoPE: x1*cos - x2*sin,
 // x1*sin + x2*cos on the two halves), :207-230 (cache at the position).
 // Items: [0, nh*half) query pairs, then nkv*half key pairs, then nkv*d values.
+// Row blockIdx.y of q/k/v/q_out ([rows][nh*d], [rows][nkv*d]) at position
+// (*pos_p, or pos0 when pos_p is null) + blockIdx.y.
 __global__ __launch_bounds__(256) void rope_kv_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                       const float* __restrict__ v, const float* __restrict__ bias,
                                                       const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                                                      const int64_t* __restrict__ pos_p, uint16_t* __restrict__ kc,
-                                                      uint16_t* __restrict__ vc, float* __restrict__ q_out, int nh,
-                                                      int nkv, int d, int cap) {
-    const int64_t pos = *pos_p;
+                                                      const int64_t* __restrict__ pos_p, int64_t pos0,
+                                                      uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                      float* __restrict__ q_out, int nh, int nkv, int d, int cap) {
+    const int64_t pos = (pos_p ? *pos_p : pos0) + blockIdx.y;
+    q += static_cast<size_t>(blockIdx.y) * nh * d;
+    q_out += static_cast<size_t>(blockIdx.y) * nh * d;
+    k += static_cast<size_t>(blockIdx.y) * nkv * d;
+    v += static_cast<size_t>(blockIdx.y) * nkv * d;
     const int half = d >> 1;
     const int it = blockIdx.x * blockDim.x + threadIdx.x;
     const int nq = nh * half, nk = nkv * half, nv = nkv * d;
@@ -131,6 +144,16 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const float* __restrict__ 
         const float val = __fadd_rn(v[e], bias[(nh + nkv) * d + e]);
         vc[(static_cast<size_t>(head) * cap + prow) * d + i] = f2h_rne(val);
     }
+}
+
+// ------------------------------------------------------------ SiLU * up ---
+// h = SiLU(g) * u elementwise (hetero/cpu_model.py:169-170, :291-292), the
+// expression the fused gate/up GEMV applies to its two sums.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                       float* __restrict__ h, long n) {
+    const long stride = static_cast<long>(gridDim.x) * blockDim.x;
+    for (long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        h[i] = silu_mul(g[i], u[i]);
 }
 
 // ---------------------------------------------------------- attention ---
@@ -289,6 +312,20 @@ int q4_embed_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* bias
     return check_launch("q4_embed_dev");
 }
 
+int q4_embed_rows_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const int64_t* ids,
+                      int n_ids, float* out, int n_rows, int n_in, int gs, void* stream) {
+    if (n_ids < 0 || n_ids > 65535) return fail(Q4_EARG, "q4_embed_rows_dev: n_ids = %d outside [0, 65535]", n_ids);
+    if (!w || !scales || !biases || !ids || !out) return fail(Q4_EARG, "q4_embed_rows_dev: null pointer");
+    if (n_rows <= 0 || n_in <= 0 || gs <= 0 || n_in % gs || gs % 8 || (reinterpret_cast<uintptr_t>(out) & 15))
+        return fail(Q4_EARG, "q4_embed_rows_dev: bad sizes (n_rows %d, n_in %d, gs %d) or out not 16-byte aligned",
+                    n_rows, n_in, gs);
+    if (n_ids == 0) return 0;
+    const int wpr = n_in / 8;
+    hipLaunchKernelGGL(embed_kernel, dim3((wpr + 255) / 256, n_ids), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       w, scales, biases, ids, out, n_rows, n_in, gs);
+    return check_launch("q4_embed_rows_dev");
+}
+
 int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, float* y, int n, void* stream) {
     if (!x || !w || !y) return fail(Q4_EARG, "q4_add_rmsnorm_dev: null pointer");
     if (n <= 0 || n > kNormPer * 1024) return fail(Q4_EARG, "q4_add_rmsnorm_dev: n = %d outside [1, %d]", n,
@@ -296,6 +333,17 @@ int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, 
     hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), x, delta, w,
                        eps, y, n);
     return check_launch("q4_add_rmsnorm_dev");
+}
+
+int q4_add_rmsnorm_rows_dev(float* x, const float* delta, const float* w, float eps, float* y, int rows, int n,
+                            void* stream) {
+    if (!x || !w || !y) return fail(Q4_EARG, "q4_add_rmsnorm_rows_dev: null pointer");
+    if (rows < 0 || n <= 0 || n > kNormPer * 1024)
+        return fail(Q4_EARG, "q4_add_rmsnorm_rows_dev: rows = %d, n = %d (n in [1, %d])", rows, n, kNormPer * 1024);
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(1024), 0, static_cast<hipStream_t>(stream), x, delta, w,
+                       eps, y, n);
+    return check_launch("q4_add_rmsnorm_rows_dev");
 }
 
 int q4_rope_kv_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
@@ -308,8 +356,38 @@ int q4_rope_kv_dev(const float* q, const float* k, const float* v, const float* 
                     n_kv, head_dim, cap);
     const int items = n_heads * (head_dim / 2) + n_kv * (head_dim / 2) + n_kv * head_dim;
     hipLaunchKernelGGL(rope_kv_kernel, dim3((items + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
-                       q, k, v, bias, cos_t, sin_t, pos, k_cache, v_cache, q_out, n_heads, n_kv, head_dim, cap);
+                       q, k, v, bias, cos_t, sin_t, pos, int64_t{0}, k_cache, v_cache, q_out, n_heads, n_kv, head_dim,
+                       cap);
     return check_launch("q4_rope_kv_dev");
+}
+
+int q4_rope_kv_rows_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
+                        const float* sin_t, int64_t pos0, int rows, uint16_t* k_cache, uint16_t* v_cache,
+                        float* q_out, int n_heads, int n_kv, int head_dim, int cap, void* stream) {
+    if (!q || !k || !v || !bias || !cos_t || !sin_t || !k_cache || !v_cache || !q_out)
+        return fail(Q4_EARG, "q4_rope_kv_rows_dev: null pointer");
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || head_dim <= 0 || head_dim % 2 || cap <= 0)
+        return fail(Q4_EARG, "q4_rope_kv_rows_dev: bad sizes (heads %d, kv heads %d, head_dim %d, cap %d)", n_heads,
+                    n_kv, head_dim, cap);
+    if (rows < 0 || rows > 65535 || pos0 < 0 || pos0 + rows > cap)
+        return fail(Q4_EARG, "q4_rope_kv_rows_dev: positions [%lld, %lld) outside the cache [0, %d) or rows > 65535",
+                    static_cast<long long>(pos0), static_cast<long long>(pos0 + rows), cap);
+    if (rows == 0) return 0;
+    const int items = n_heads * (head_dim / 2) + n_kv * (head_dim / 2) + n_kv * head_dim;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((items + 255) / 256, rows), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), q, k, v, bias, cos_t, sin_t, nullptr, pos0, k_cache, v_cache,
+                       q_out, n_heads, n_kv, head_dim, cap);
+    return check_launch("q4_rope_kv_rows_dev");
+}
+
+int q4_silu_mul_dev(const float* g, const float* u, float* h, long n, void* stream) {
+    if (!g || !u || !h) return fail(Q4_EARG, "q4_silu_mul_dev: null pointer");
+    if (n < 0) return fail(Q4_EARG, "q4_silu_mul_dev: n = %ld", n);
+    if (n == 0) return 0;
+    const long blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(blocks < 4096 ? blocks : 4096)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), g, u, h, n);
+    return check_launch("q4_silu_mul_dev");
 }
 
 long q4_attention_scratch_floats(int n_heads, int head_dim, int cap) {

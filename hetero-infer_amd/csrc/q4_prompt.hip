@@ -1,0 +1,228 @@
+// Causal grouped-query attention of a prompt chunk over the fp16 KV cache
+// (gfx950), the attention of the device-resident prompt forward.  Declared
+// in q4decode.h (q4_prompt_attention_dev).
+//
+// hetero/cpu_model.py:233-252 (sdpa with causal=True, L > 1): query row r
+// of a chunk that starts at position pos0 sits at position pos0 + r and
+// sees the positions [0, pos0 + r] -- the reference's mask
+// `arange(S) <= arange(L) + (S - L)` with S = pos0 + L; query head h reads
+// kv head h / (nh / nkv); s = (q . k) * scale, softmax over the visible
+// positions, o = sum p v.
+//
+// A workgroup takes one kv head and four consecutive query rows (one per
+// wave) for all G query heads that share the kv head, and walks the cache
+// in tiles of 64 positions up to the last position its rows see: the tile's
+// K and V rows are staged in LDS once for the 4 x G queries.  Per tile a
+// wave computes the scores of its row with lane = position (the K row from
+// LDS, the query broadcast from LDS), updates a running softmax (running
+// maximum m, sum l, and the output rescaled by e^(m_old - m_new)), and adds
+// p v with lane = pair of output dimensions.  The softmax is therefore
+// evaluated online, tile by tile, not as the reference's one max and one
+// sum over the whole row: the results agree to fp32 rounding, not bit for
+// bit.  Workgroups of the last rows, which see the most positions, are
+// launched first.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "q4_common.h"
+#include "q4decode.h"
+
+namespace q4k {
+namespace {
+
+constexpr int kPTile = 64;                  // positions per tile
+constexpr int kPRows = 4;                   // query rows per workgroup: one per wave
+constexpr int kPMaxG = 8;                   // query heads per kv head
+constexpr int kPMaxD = 128;
+constexpr int kPRowU4 = kPMaxD / 8 + 1;     // LDS row of K / V: 16 uint4 of fp16 + 1 pad (reads spread over the banks)
+
+struct PromptAttnArgs {
+    const float* q;          // [rows][nh * d], rotated queries
+    const uint16_t* kc;      // [nkv][cap][d] fp16
+    const uint16_t* vc;
+    float* out;              // [rows][nh * d]
+    int rows;
+    int64_t pos0;
+    int nh, nkv, d, cap;
+    float scale;
+};
+
+__device__ __forceinline__ float p_h2f(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// LDS stores by some lanes of a wave are visible to the other lanes' later
+// loads (the wave's LDS operations complete in order).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <int G>
+__global__ __launch_bounds__(64 * kPRows) void prompt_attn_kernel(PromptAttnArgs a) {
+    __shared__ uint4 k_s[kPTile][kPRowU4];
+    __shared__ uint4 v_s[kPTile][kPRowU4];
+    __shared__ float4 q_s[kPRows][G][kPMaxD / 4];
+    __shared__ float4 p_s[kPRows][G][kPTile / 4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kvh = blockIdx.y;
+    const int r0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * kPRows;
+    const int r = r0 + wave;                                   // this wave's query row
+    const bool row_ok = r < a.rows;                            // wave-uniform
+    const int d = a.d, du4 = d >> 3, dp = d >> 1, dq = d >> 2;
+    const int hd = a.nh * d;
+    const int last_row = (r0 + kPRows < a.rows ? r0 + kPRows : a.rows) - 1;
+    const int64_t wg_last = a.pos0 + last_row;                 // the last position a row of the workgroup sees
+    const int64_t my_last = a.pos0 + r;                        // the last position this row sees
+    const int n_tiles = static_cast<int>(wg_last / kPTile) + 1;
+    if (row_ok) {
+        const float4* src = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(r) * hd +
+                                                            static_cast<size_t>(kvh) * G * d);
+        for (int e = lane; e < G * dq; e += 64) q_s[wave][e / dq][e % dq] = src[e];
+    }
+    float m[G], l[G], o0[G], o1[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        m[g] = -__builtin_inff();
+        l[g] = o0[g] = o1[g] = 0.0f;
+    }
+    const size_t head_row0 = static_cast<size_t>(kvh) * a.cap;
+    for (int t = 0; t < n_tiles; t++) {
+        const int64_t c0 = static_cast<int64_t>(t) * kPTile;
+        const int valid = static_cast<int>(wg_last + 1 - c0 < kPTile ? wg_last + 1 - c0 : kPTile);
+        __syncthreads();                                       // the last tile's K, V and p are read
+        // K and V rows [c0, c0 + valid); the rows past them read 0 (past the
+        // end of the buffer resource), so p = 0 never meets a stale value
+        const uint32_t bytes = static_cast<uint32_t>(valid) * static_cast<uint32_t>(d) * 2u;
+        const __amdgpu_buffer_rsrc_t kr = buf_rsrc(a.kc + (head_row0 + c0) * d, bytes);
+        const __amdgpu_buffer_rsrc_t vr = buf_rsrc(a.vc + (head_row0 + c0) * d, bytes);
+        for (int e = tid; e < kPTile * du4; e += 64 * kPRows) {
+            const int row = e / du4, c = e - row * du4;
+            const uint32_t off = static_cast<uint32_t>(e) * 16u;
+            k_s[row][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+            v_s[row][c] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
+        }
+        __syncthreads();
+        if (!row_ok || c0 > my_last) continue;                 // wave-uniform: nothing this row sees
+        // scores: lane j = position c0 + j; dims in ascending order
+        const int j = lane;
+        float acc[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) acc[g] = 0.0f;
+        for (int c = 0; c < du4; c++) {
+            const uint4 kk = k_s[j][c];
+            const float kf[8] = {p_h2f(kk.x), p_h2f(kk.x >> 16), p_h2f(kk.y), p_h2f(kk.y >> 16),
+                                 p_h2f(kk.z), p_h2f(kk.z >> 16), p_h2f(kk.w), p_h2f(kk.w >> 16)};
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float4 qa = q_s[wave][g][2 * c], qb = q_s[wave][g][2 * c + 1];
+                acc[g] = __builtin_fmaf(qa.x, kf[0], acc[g]);
+                acc[g] = __builtin_fmaf(qa.y, kf[1], acc[g]);
+                acc[g] = __builtin_fmaf(qa.z, kf[2], acc[g]);
+                acc[g] = __builtin_fmaf(qa.w, kf[3], acc[g]);
+                acc[g] = __builtin_fmaf(qb.x, kf[4], acc[g]);
+                acc[g] = __builtin_fmaf(qb.y, kf[5], acc[g]);
+                acc[g] = __builtin_fmaf(qb.z, kf[6], acc[g]);
+                acc[g] = __builtin_fmaf(qb.w, kf[7], acc[g]);
+            }
+        }
+        // the running softmax (every tile a row reaches holds position c0 <=
+        // my_last, so the tile's maximum is finite)
+        const bool vis = c0 + j <= my_last;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float s = vis ? __fmul_rn(acc[g], a.scale) : -__builtin_inff();
+            const float mn = fmaxf(m[g], wave_max(s));
+            const float corr = expf(__fsub_rn(m[g], mn));       // 0 on the row's first tile
+            const float p = vis ? expf(__fsub_rn(s, mn)) : 0.0f;
+            l[g] = __fadd_rn(__fmul_rn(l[g], corr), wave_sum(p));
+            o0[g] = __fmul_rn(o0[g], corr);
+            o1[g] = __fmul_rn(o1[g], corr);
+            m[g] = mn;
+            reinterpret_cast<float*>(&p_s[wave][g][0])[j] = p;
+        }
+        wave_lds_sync();
+        // o += p v: lane = pair of dimensions; positions in ascending order
+        if (lane < dp) {
+            const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v_s[0][0]);
+            constexpr int kRowW = kPRowU4 * 4;
+            const int span = my_last - c0 + 1 < kPTile ? static_cast<int>(my_last - c0 + 1) : kPTile;
+            for (int j0 = 0; j0 < span; j0 += 4) {
+                uint32_t w2[4];
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) w2[jj] = vw[(j0 + jj) * kRowW + lane];
+                float4 pg[G];
+#pragma unroll
+                for (int g = 0; g < G; g++) pg[g] = p_s[wave][g][j0 >> 2];
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const float v0 = p_h2f(w2[jj]), v1 = p_h2f(w2[jj] >> 16);
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const float p = jj == 0 ? pg[g].x : jj == 1 ? pg[g].y : jj == 2 ? pg[g].z : pg[g].w;
+                        o0[g] = __builtin_fmaf(p, v0, o0[g]);
+                        o1[g] = __builtin_fmaf(p, v1, o1[g]);
+                    }
+                }
+            }
+        }
+        wave_lds_sync();
+    }
+    if (row_ok && lane < dp) {
+        float* dst = a.out + static_cast<size_t>(r) * hd + static_cast<size_t>(kvh) * G * d + 2 * lane;
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            dst[g * d] = __fdiv_rn(o0[g], l[g]);
+            dst[g * d + 1] = __fdiv_rn(o1[g], l[g]);
+        }
+    }
+}
+
+int launch_failed(const char* what) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q4_EHIP, "%s launch: %s", what, hipGetErrorString(e));
+    return 0;
+}
+
+}  // namespace
+}  // namespace q4k
+
+using namespace q4k;
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int rows,
+                            int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream) {
+    if (!q || !k_cache || !v_cache || !out) return fail(Q4_EARG, "q4_prompt_attention_dev: null pointer");
+    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kPMaxG ||
+        (head_dim != 32 && head_dim != 64 && head_dim != 128) || cap <= 0)
+        return fail(Q4_EARG, "q4_prompt_attention_dev: unsupported sizes (heads %d, kv heads %d, head_dim %d, cap %d)",
+                    n_heads, n_kv, head_dim, cap);
+    if (rows < 0 || pos0 < 0 || pos0 + rows > cap)
+        return fail(Q4_EARG, "q4_prompt_attention_dev: rows at positions [%lld, %lld) outside the cache [0, %d)",
+                    static_cast<long long>(pos0), static_cast<long long>(pos0 + rows), cap);
+    if ((reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(out) & 15) ||
+        (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15))
+        return fail(Q4_EARG, "q4_prompt_attention_dev: q, out and the caches must be 16-byte aligned");
+    if (rows == 0) return 0;
+    const PromptAttnArgs a{q, k_cache, v_cache, out, rows, pos0, n_heads, n_kv, head_dim, cap, scale};
+    const dim3 grid((rows + kPRows - 1) / kPRows, n_kv);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    switch (n_heads / n_kv) {
+#define Q4_PROMPT_CASE(g)                                                                       \
+    case g:                                                                                     \
+        hipLaunchKernelGGL(prompt_attn_kernel<g>, grid, dim3(64 * kPRows), 0, st, a);           \
+        break;
+        Q4_PROMPT_CASE(1) Q4_PROMPT_CASE(2) Q4_PROMPT_CASE(3) Q4_PROMPT_CASE(4)
+        Q4_PROMPT_CASE(5) Q4_PROMPT_CASE(6) Q4_PROMPT_CASE(7) Q4_PROMPT_CASE(8)
+#undef Q4_PROMPT_CASE
+        default: break;
+    }
+    return launch_failed("q4_prompt_attention_dev");
+}
+
+}  // extern "C"
+#pragma GCC visibility pop

@@ -246,14 +246,6 @@ __device__ __forceinline__ float chain_add(float acc, const float* tp) {
     return acc;
 }
 
-// SiLU(g) * u as hetero/cpu_model.py:169-170 and :291-292 compute it in
-// fp32: g / (1 + exp(-g)) * u (expf here; NumPy's float32 exp may differ in
-// the last place).
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    const float e = expf(-g);
-    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
-}
-
 // Words of x per thread and activation row that the word pass keeps in
 // registers (RW rounds of blockDim.x words); the host picks the instance.
 template <int MR>

@@ -28,6 +28,9 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            "q4_embed_dev", "q4_add_rmsnorm_dev", "q4_rope_kv_dev", "q4_attention_scratch_floats",
            "q4_attention_dev", "q4_attention_rope_dev", "q4_argmax_dev",
            "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev", "q4_norm_gemv_argmax_dev",
+           # the prompt forward (include/q4decode.h)
+           "q4_embed_rows_dev", "q4_add_rmsnorm_rows_dev", "q4_rope_kv_rows_dev", "q4_silu_mul_dev",
+           "q4_prompt_attention_dev",
            # activation wire codec (include/q4wire.h)
            "q4_wire_payload_bytes", "q4_wire_encode_dev", "q4_wire_decode_dev",
            # chained GEMV programs (include/q4chain.h)
@@ -97,6 +100,16 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_norm_gemv_argmax_dev.argtypes = ([_VP] * 4 + [_I] + [_VP] * 3 + [_F, _VP, _I, _I] + [_VP] * 3
                                                 + [ctypes.c_int64, _I, _VP])
         lib.q4_norm_gemv_argmax_dev.restype = _I
+        lib.q4_embed_rows_dev.argtypes = [_VP] * 4 + [_I, _VP] + [_I] * 3 + [_VP]
+        lib.q4_embed_rows_dev.restype = _I
+        lib.q4_add_rmsnorm_rows_dev.argtypes = [_VP] * 3 + [_F, _VP, _I, _I, _VP]
+        lib.q4_add_rmsnorm_rows_dev.restype = _I
+        lib.q4_rope_kv_rows_dev.argtypes = [_VP] * 6 + [ctypes.c_int64, _I] + [_VP] * 3 + [_I] * 4 + [_VP]
+        lib.q4_rope_kv_rows_dev.restype = _I
+        lib.q4_silu_mul_dev.argtypes = [_VP] * 3 + [_L, _VP]
+        lib.q4_silu_mul_dev.restype = _I
+        lib.q4_prompt_attention_dev.argtypes = [_VP] * 4 + [_I, ctypes.c_int64] + [_I] * 4 + [_F, _VP]
+        lib.q4_prompt_attention_dev.restype = _I
     if hasattr(lib, "q4_wire_encode_dev"):
         lib.q4_wire_payload_bytes.argtypes = [_I] * 3
         lib.q4_wire_payload_bytes.restype = ctypes.c_longlong

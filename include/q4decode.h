@@ -31,11 +31,23 @@ extern "C" {
 int q4_embed_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const int64_t* tok,
                  float* out, int n_rows, int n_in, int gs, void* stream);
 
+/* q4_embed_dev for n_ids tokens: row i of out [n_ids][n_in] is the
+ * embedding of ids[i] (hetero/cpu_model.py:334-338 over a prompt's token
+ * ids).  n_ids <= 65535. */
+int q4_embed_rows_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, const int64_t* ids,
+                      int n_ids, float* out, int n_rows, int n_in, int gs, void* stream);
+
 /* Residual add and RMSNorm (hetero/cpu_model.py:164-166 rms_norm, :304-306
  * the residual adds of DecoderLayer): if delta is not NULL, x += delta
  * (in place); then y = x * (1 / sqrt(mean(x*x) + eps)) * w.  n <= 8192. */
 int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, float* y, int n,
                        void* stream);
+
+/* q4_add_rmsnorm_dev on each row of x, delta, y [rows][n] (the prompt's
+ * rows, hetero/cpu_model.py:304-306 with L > 1); row i gives the bits
+ * q4_add_rmsnorm_dev gives for that row alone. */
+int q4_add_rmsnorm_rows_dev(float* x, const float* delta, const float* w, float eps, float* y, int rows, int n,
+                            void* stream);
 
 /* The GEMVs that follow a residual add + RMSNorm, with the norm folded into
  * their prologue (every workgroup normalises the input itself, so the
@@ -73,6 +85,32 @@ int q4_norm_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, con
 int q4_rope_kv_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
                    const float* sin_t, const int64_t* pos, uint16_t* k_cache, uint16_t* v_cache,
                    float* q_out, int n_heads, int n_kv, int head_dim, int cap, void* stream);
+
+/* q4_rope_kv_dev for the rows of a prompt chunk: row i of q [rows][nh*d],
+ * k, v [rows][nkv*d] at position pos0 + i (hetero/cpu_model.py:195-204 with
+ * offset = pos0, :216-230 storing L rows), written to q_out [rows][nh*d]
+ * and the cache rows pos0 .. pos0 + rows - 1, which must lie in [0, cap).
+ * Row i gives the bits q4_rope_kv_dev gives at that position.
+ * rows <= 65535. */
+int q4_rope_kv_rows_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
+                        const float* sin_t, int64_t pos0, int rows, uint16_t* k_cache, uint16_t* v_cache,
+                        float* q_out, int n_heads, int n_kv, int head_dim, int cap, void* stream);
+
+/* h[i] = SiLU(g[i]) * u[i] for i < n (hetero/cpu_model.py:169-170, :291-292),
+ * the expression q4_gate_up_silu_dev applies to its two sums. */
+int q4_silu_mul_dev(const float* g, const float* u, float* h, long n, void* stream);
+
+/* Causal grouped-query attention of a prompt chunk (hetero/cpu_model.py:
+ * 233-252 with causal=True and L > 1): query row i of q [rows][nh*d]
+ * (rotated, q4_rope_kv_rows_dev) sits at position pos0 + i and attends to
+ * the cache positions [0, pos0 + i], which the caller has written (the
+ * chunk's own keys and values by q4_rope_kv_rows_dev first); out
+ * [rows][nh*d].  The softmax is evaluated online over 64-position tiles, so
+ * results agree with the reference's single max-and-sum to fp32 rounding.
+ * head_dim 32, 64 or 128; at most 8 query heads per kv head;
+ * pos0 + rows <= cap; q, out and the caches 16-byte aligned. */
+int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int rows,
+                            int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream);
 
 /* Floats of scratch memory q4_attention_dev needs for these sizes. */
 long q4_attention_scratch_floats(int n_heads, int head_dim, int cap);

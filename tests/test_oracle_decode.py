@@ -8,6 +8,12 @@ the product (hetero/numpy_stage.py), on the CPU.
   int16 quantisation of x in every GEMV leaves (1e-3, max |diff| / max |ref|).
   Planted mistakes in the oracle (KV head mapping, rotation sign, a dropped
   residual) must fail the same comparison.
+* The oracle's prompt path (L > 1 rows, causal attention, the q4_dequant +
+  BLAS contraction above 16 rows) against the same float64 decode: in
+  exact arithmetic a causal prompt's last row has the logits of decoding
+  its tokens one by one.  Planted mistakes (a causal mask shifted by one
+  position, RoPE at offset 0 instead of the cache position, the chunk's
+  keys written one position late) must fail it.
 * The product's NumPy stage on the reference kernel compiled from source
   against the oracle on the same kernel: logits bit-identical step for step.
 * The generators the fixtures and the GPU tests share: NumPy and torch
@@ -127,12 +133,12 @@ def _planted(monkeypatch, which):
         orig = odec._rope
         monkeypatch.setattr(odec, "_rope", lambda x, c, s: orig(x, c, -s))
     elif which == "dropped mlp residual":
-        orig = odec.DecodeOracle.gemv
+        orig = odec.DecodeOracle.project
 
-        def gemv(self, name, x):
+        def project(self, name, x):
             y = orig(self, name, x)
             return np.zeros_like(y) if name.endswith("down_proj") else y
-        monkeypatch.setattr(odec.DecodeOracle, "gemv", gemv)
+        monkeypatch.setattr(odec.DecodeOracle, "project", project)
 
 
 @needs_ref
@@ -143,6 +149,101 @@ def test_textbook_comparison_catches_planted_mistakes(tiny, monkeypatch, which):
     _planted(monkeypatch, which)
     got = run_oracle(cfg, w, ks, vs, TOKENS, oracle.load_ref(1))
     assert max(oracle.normwise_rel(a, b) for a, b in zip(got, want)) > 10 * TOL, which
+
+
+PROMPT = [7, 3, 250, 41, 0, 299, 12, 12, 5, 88, 140, 2, 61, 33, 9, 170, 203, 4, 77, 150]   # 20 tokens
+
+
+@needs_ref
+@pytest.mark.parametrize("chunks", [(5,), (20,), (12, 8), (17, 3)], ids=lambda c: "+".join(map(str, c)))
+def test_oracle_prompt_matches_textbook(tiny, chunks):
+    """Prompt chunks of <= 16 rows take the per-row GEMV, longer ones the
+    q4_dequant + BLAS contraction; either way the last row's logits are the
+    textbook decode's of the same tokens."""
+    cfg, w, ks, vs = tiny
+    n = sum(chunks)
+    want = textbook_decode(cfg, w, ks, vs, PROMPT[:n])[-1]
+    orc = odec.DecodeOracle(cfg, w, ks, vs, oracle.load_ref(1), extra=n)
+    lo = 0
+    for c in chunks:
+        got = orc.prompt(PROMPT[lo:lo + c])
+        lo += c
+    assert orc.pos == ks[0].shape[1] + n
+    assert oracle.normwise_rel(got, want) < TOL
+
+
+def _planted_prompt(monkeypatch, which):
+    if which == "causal mask shifted":
+        orig = odec._sdpa
+
+        def sdpa(q, k, v, scale, causal=False):
+            if not causal:
+                return orig(q, k, v, scale)
+            # every row also sees the next position
+            B, H, L, D = q.shape
+            KH, S = k.shape[1], k.shape[2]
+            s = np.einsum("bkgld,bksd->bkgls", q.reshape(B, KH, H // KH, L, D), k) * scale
+            s = np.where(np.arange(S)[None, :] <= np.arange(L)[:, None] + (S - L) + 1, s, -np.inf)
+            e = np.exp(s - s.max(-1, keepdims=True))
+            e /= e.sum(-1, keepdims=True)
+            return np.einsum("bkgls,bksd->bkgld", e, v).reshape(B, H, L, D)
+        monkeypatch.setattr(odec, "_sdpa", sdpa)
+    elif which == "rope at offset 0":
+        orig = odec.DecodeOracle.prompt
+
+        def prompt(self, ids):
+            c, s_ = self.cos, self.sin
+            self.cos, self.sin = np.roll(c, self.pos, axis=0), np.roll(s_, self.pos, axis=0)
+            try:
+                return orig(self, ids)
+            finally:
+                self.cos, self.sin = c, s_
+        monkeypatch.setattr(odec.DecodeOracle, "prompt", prompt)
+    elif which == "keys one position late":
+        orig = odec._rope
+        state = {"n": 0}
+
+        def rope(x, cos, sin):
+            y = orig(x, cos, sin)
+            state["n"] += 1
+            if state["n"] % 2 == 0 and x.shape[2] > 1:             # the keys: shift by one position
+                y = np.concatenate([np.zeros_like(y[:, :, :1]), y[:, :, :-1]], axis=2)
+            return y
+        monkeypatch.setattr(odec, "_rope", rope)
+
+
+@needs_ref
+@pytest.mark.parametrize("which", ["causal mask shifted", "rope at offset 0", "keys one position late"])
+def test_prompt_comparison_catches_planted_mistakes(tiny, monkeypatch, which):
+    cfg, w, ks, vs = tiny
+    want = textbook_decode(cfg, w, ks, vs, PROMPT)[-1]
+    _planted_prompt(monkeypatch, which)
+    orc = odec.DecodeOracle(cfg, w, ks, vs, oracle.load_ref(1), extra=len(PROMPT))
+    got = orc.prompt(PROMPT)
+    assert oracle.normwise_rel(got, want) > 10 * TOL, which
+
+
+@needs_ref
+def test_oracle_bf16_contraction_moves_logits_slightly(tiny):
+    """gemm_bf16 changes only the contraction's operands: a prompt of <= 16
+    rows is unchanged bit for bit, a longer one moves by bf16 rounding."""
+    cfg, w, ks, vs = tiny
+    lib = oracle.load_ref(1)
+    a = odec.DecodeOracle(cfg, w, ks, vs, lib, extra=20).prompt(PROMPT[:12])
+    b = odec.DecodeOracle(cfg, w, ks, vs, lib, extra=20, gemm_bf16=True).prompt(PROMPT[:12])
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    a = odec.DecodeOracle(cfg, w, ks, vs, lib, extra=20).prompt(PROMPT)
+    b = odec.DecodeOracle(cfg, w, ks, vs, lib, extra=20, gemm_bf16=True).prompt(PROMPT)
+    assert 1e-5 < oracle.normwise_rel(b, a) < 5e-2
+
+
+def test_bf16_round_is_nearest_even():
+    import torch
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0 ** rng.integers(-20, 20, 100000),
+                        np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -1.0 - 2 ** -8, 0.0, -0.0], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    assert np.array_equal(odec.bf16_round(x).view(np.uint32), want.view(np.uint32))
 
 
 @needs_ref
