@@ -449,6 +449,7 @@ def load_bench(torch, dev, layers=4, reps=2):
 
 
 DECODE_FIXTURE = os.path.join(ROOT, "tests", "golden", "decode_qwen7b.json")
+PROMPT_FIXTURE = os.path.join(ROOT, "tests", "golden", "prompt_qwen7b.json")
 
 
 def decode_model(torch, dev):
@@ -508,6 +509,52 @@ def decode_bench(torch, dev, cfg, meta, w, ks, vs, steps=128):
     del g
     torch.cuda.empty_cache()
     return res
+
+
+def prompt_bench(torch, dev, cfg, w, reps=3):
+    """The 512-token prompt forward through the 28 layers on the device
+    (GpuStage.prefill in one chunk: embedding rows, norms, the grouped bf16
+    GEMMs, RoPE and the cache write, causal attention, the MLP, the final
+    norm, lm_head and the greedy token of the last row), from an empty
+    cache: time per prompt, prompt tokens/s, the TFLOP/s of its
+    projections, and its last-position logits against the reference path's
+    (tests/golden/prompt_qwen7b.npz, oracle/decode.py on kernel/q4gemv.c)."""
+    import numpy as np
+    import oracle
+    from hetero.gpu_model import GpuStage
+    with open(PROMPT_FIXTURE) as f:
+        meta = json.load(f)
+    fx = np.load(PROMPT_FIXTURE.replace(".json", ".npz"))
+    ids = fx["ids"].tolist()
+    n = len(ids)
+    g = GpuStage(cfg, w, None, None, max_new=8)
+    g.prefill(ids, chunk=n)                       # sizes the GEMM workspaces
+    times = []
+    for _ in range(reps):
+        g.truncate(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        tok = g.prefill(ids, chunk=n)             # ends with the token on the host: synchronised
+        times.append(time.perf_counter() - t0)
+    lg = g.logits.cpu().numpy().reshape(-1)
+    ms = 1e3 * float(np.median(times))
+    h, inter, nl = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_hidden_layers"]
+    kvd = cfg["num_key_value_heads"] * (h // cfg["num_attention_heads"])
+    proj = nl * 2 * n * h * (h + 2 * kvd + h + 3 * inter) + 2 * h * cfg["vocab_size"]
+    attn = nl * 2 * 2 * h * (n * (n + 1) // 2)    # q.k and p.v over the causal triangle, all heads
+    ref = fx["ref_logits"]
+    del g
+    torch.cuda.empty_cache()
+    return {"workload": f"{n}-token prompt (uniform random ids) through the 28-layer 4-bit Qwen2 stage in one chunk, "
+                        "empty cache, last-position logits and greedy token",
+            "ms": round(ms, 2), "prompt_tok_s": round(n / (ms * 1e-3), 1),
+            "tflops_projections": round(proj / (ms * 1e-3) / 1e12, 1),
+            "tflops_with_attention": round((proj + attn) / (ms * 1e-3) / 1e12, 1),
+            "flops_projections": proj, "flops_attention": attn,
+            "logits_err_vs_reference_path": round(oracle.normwise_rel(lg, ref), 6),
+            "bf16_operand_drift_of_reference_path": round(meta["bf16_drift"]["logits"], 6),
+            "greedy_token": tok, "reference_greedy_token": int(np.argmax(ref)),
+            "reference": "tests/golden/prompt_qwen7b.npz (oracle/decode.py on kernel/q4gemv.c, fp32 BLAS)"}
 
 
 def host_arrays(torch, w, ks, vs):
@@ -795,6 +842,8 @@ def main():
                     help="with --chain-only: also the per-phase event times of the chained sweep")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the M=512 prefill leg (for counter runs)")
+    ap.add_argument("--prompt-only", action="store_true",
+                    help="only the 512-token prompt forward through the 28 layers (for rocprof runs)")
     ap.add_argument("--small-m-only", action="store_true",
                     help="only the small-M section (for rocprof runs)")
     ap.add_argument("--decode-only", action="store_true",
@@ -830,6 +879,11 @@ def main():
         cfg, meta, w, ks, vs = decode_model(torch, dev)
         res = decode_bench(torch, dev, cfg, meta, w, ks, vs, steps=args.decode_steps)
         print(json.dumps({"decode": res}), flush=True)
+        return
+    if args.prompt_only:
+        cfg, meta, w, ks, vs = decode_model(torch, dev)
+        del ks, vs
+        print(json.dumps({"prompt_forward": prompt_bench(torch, dev, cfg, w)}), flush=True)
         return
     if args.gs128_only:
         print(json.dumps({"group128": group128_bench(torch, lib, dev)}), flush=True)
@@ -1088,10 +1142,13 @@ def main():
         threads = result["cpu_baseline"].get("cores", 16) or 16
     else:
         result["cpu_baseline"] = None
-    if not (args.no_decode and args.no_dropin):
+    if not (args.no_decode and args.no_dropin and args.no_prefill):
         del layers, head
         torch.cuda.empty_cache()
         cfg, meta, w, ks, vs = decode_model(torch, dev)
+        if not args.no_prefill:
+            log("prompt forward ...")
+            result["prompt_forward"] = prompt_bench(torch, dev, cfg, w)
         if not args.no_decode:
             log("decode ...")
             result["decode"] = decode_bench(torch, dev, cfg, meta, w, ks, vs, steps=args.decode_steps)

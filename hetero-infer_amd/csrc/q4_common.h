@@ -86,10 +86,15 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 }
 
 // 1 / sqrt(mean + eps) of RMSNorm from the sum of squares of n values
-// (hetero/cpu_model.py:164-166).
+// (hetero/cpu_model.py:164-166).  NumPy's mean divides the float32 sum by
+// the element count, an integer scalar, in float64 and stores the quotient
+// as float32 (true_divide with casting='unsafe'); eps then adds in float32.
+// The square root is the correctly rounded one (__builtin_sqrtf expands to
+// v_sqrt_f32 plus a one-ulp correction; __fsqrt_rn is v_sqrt_f32 alone,
+// which is off by an ulp now and then), as np.sqrt's.
 __device__ __forceinline__ float rms_factor(float sum_sq, int n, float eps) {
-    const float ms = __fdiv_rn(sum_sq, static_cast<float>(n));
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(ms, eps)));
+    const float ms = static_cast<float>(static_cast<double>(sum_sq) / static_cast<double>(n));
+    return __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(ms, eps)));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -102,6 +107,68 @@ __device__ __forceinline__ float wave_max(float v) {
     const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
     const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// The sum of a row of n values, thread t holding the 8 values of word t
+// (values 8t .. 8t+7; threads past the row hold zeros), added in the order
+// of NumPy's float32 reductions (np.add.reduce, which x.mean() and x.sum()
+// use): pairwise summation -- a row of more than 128 values is split at
+// n2 = n/2 rounded down to a multiple of 8 and the two halves' sums are
+// added; a block of 8 < n <= 128 values is added by 8 accumulators, r[j]
+// taking values j, j + 8, j + 16, ... in order, combined as
+// ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)) (plus a sequential rest
+// when n % 8 != 0).  When every split is exact (n = L m, L a power of two,
+// m <= 128, m % 8 == 0 and each halving an exact half) the tree is perfect:
+// lane (block b, accumulator j) adds block b's column j, and lane-xor sums
+// combine the accumulators and then the blocks, which is that order since
+// IEEE addition is commutative.  Other n fall back to the wave_sum tree.
+// Every thread of the workgroup calls it (blockDim.x a multiple of 64 and
+// at least n / 8); scratch: n floats of LDS, red: 16 floats of LDS.  The
+// sum is returned in every thread.
+__device__ __forceinline__ float row_sum_numpy(const float v[8], int n, float* scratch, float* red) {
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
+    int m = n, L = 1;
+    bool perfect = n >= 8 && n % 8 == 0;
+    while (perfect && m > 128) {
+        if (m % 16) perfect = false;
+        else { m >>= 1; L <<= 1; }
+    }
+    if (!perfect || 8 * L > nt) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss = __fadd_rn(ss, v[i]);
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int i = 0; i < (nt >> 6); i++) tot = __fadd_rn(tot, red[i]);
+        __syncthreads();                                           // red is free again
+        return tot;
+    }
+    if (tid < (n >> 3)) {
+        float4* d = reinterpret_cast<float4*>(scratch + 8 * tid);
+        d[0] = make_float4(v[0], v[1], v[2], v[3]);
+        d[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __syncthreads();
+    float r = 0.0f;
+    if (tid < 8 * L) {                                             // block b, accumulator j
+        const float* p = scratch + (tid >> 3) * m + (tid & 7);
+        r = p[0];
+        for (int i = 8; i < m; i += 8) r = __fadd_rn(r, p[i]);
+    }
+    r = __fadd_rn(r, __shfl_xor(r, 1));
+    r = __fadd_rn(r, __shfl_xor(r, 2));
+    r = __fadd_rn(r, __shfl_xor(r, 4));
+    for (int s = 8; s < 64 && s < 8 * L; s <<= 1) r = __fadd_rn(r, __shfl_xor(r, s));
+    const int W = (8 * L + 63) >> 6;                               // waves holding blocks (a power of two)
+    if (lane == 0 && wave < W) red[wave] = r;
+    __syncthreads();
+    float t = lane < W ? red[lane] : 0.0f;
+    for (int s = 1; s < W; s <<= 1) t = __fadd_rn(t, __shfl_xor(t, s));
+    t = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(t)));     // lane 0: the whole tree
+    __syncthreads();                                               // red and scratch are free again
+    return t;
 }
 
 // One packed word of x (8 values, MLX order) -> {xl even, xl odd, xh even,

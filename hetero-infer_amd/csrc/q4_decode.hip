@@ -50,27 +50,27 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 // ------------------------------------------------ residual add + RMSNorm ---
 // hetero/cpu_model.py:164-166: x * (1 / sqrt(mean(x * x) + eps)) * w, after
 // the residual add of :304-306.  One workgroup per row (blockIdx.x of
-// [rows][n]); n <= 8 * 1024.  Thread t
-// owns the 8 consecutive values of word t and adds their squares in order;
-// the wave sums (wave_sum) are added in wave order.  The streaming GEMV's
-// norm prologue sums in exactly this order, so its input is y bit for bit.
+// [rows][n]); n <= 8 * 1024.  Thread t owns the 8 consecutive values of
+// word t; the squares are summed in NumPy's order (row_sum_numpy), and the
+// streaming GEMV's norm prologue sums them the same way, so its input is y
+// bit for bit.
 constexpr int kNormPer = 8;
 __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ delta,
                                                           const float* __restrict__ w, float eps,
                                                           float* __restrict__ y, int n) {
     __shared__ float red[16];
+    __shared__ __attribute__((aligned(16))) float sq_s[kNormPer * 1024];
     const int tid = threadIdx.x, nt = blockDim.x;
     const int i0 = tid * kNormPer;
     const size_t row = static_cast<size_t>(blockIdx.x) * n;
     x += row;
     y += row;
     if (delta) delta += row;
-    float v[kNormPer];
-    float ss = 0.0f;
+    float v[kNormPer], sq[kNormPer];
 #pragma unroll
     for (int k = 0; k < kNormPer; k++) {
         const int i = i0 + k;
-        v[k] = 0.0f;
+        v[k] = sq[k] = 0.0f;
         if (i < n) {
             float a = x[i];
             if (delta) {
@@ -78,15 +78,11 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x
                 x[i] = a;
             }
             v[k] = a;
-            ss = __fadd_rn(ss, __fmul_rn(a, a));
+            sq[k] = __fmul_rn(a, a);
         }
     }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < (nt >> 6); i++) tot = __fadd_rn(tot, red[i]);
-    const float r = rms_factor(tot, n, eps);
+    (void)nt;
+    const float r = rms_factor(row_sum_numpy(sq, n, sq_s, red), n, eps);
 #pragma unroll
     for (int k = 0; k < kNormPer; k++) {
         const int i = i0 + k;

@@ -426,9 +426,11 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     //      order: a sequential sum with no cross-lane chain.
     if constexpr (NORM) {
         // hetero/cpu_model.py:304-306 (x + delta) and :164-166 (RMSNorm); the
-        // wave sums of squares go through the term tables' space (free until
-        // the main loop), the amax slots stay untouched
-        float ss = 0.0f;
+        // squares are summed in NumPy's order (row_sum_numpy, as
+        // add_rmsnorm_kernel does) through the x staging space and the
+        // 16-float slot after red (both free until the x staging below); the
+        // amax slots stay untouched
+        float sq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         float v[8] = {wv[0][0][0].x, wv[0][0][0].y, wv[0][0][0].z, wv[0][0][0].w,
                       wv[0][0][1].x, wv[0][0][1].y, wv[0][0][1].z, wv[0][0][1].w};
         if (wave * 64 < wpr) {                                    // uniform
@@ -446,15 +448,12 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
                         __builtin_bit_cast(u32x4, make_float4(v[4], v[5], v[6], v[7])), xo, off + 16, 0, 0);
                 }
             }
+            if (tid < wpr) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
+                for (int i = 0; i < 8; i++) sq[i] = __fmul_rn(v[i], v[i]);
+            }
         }
-        ss = wave_sum(ss);
-        if (lane == 0) stage[wave] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int i = 0; i < nwaves; i++) tot = __fadd_rn(tot, stage[i]);
-        const float r = rms_factor(tot, n_in, na.eps);
+        const float r = rms_factor(row_sum_numpy(sq, n_in, xstage, stage), n_in, na.eps);
         const float w8[8] = {nw[0].x, nw[0].y, nw[0].z, nw[0].w, nw[1].x, nw[1].y, nw[1].z, nw[1].w};
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = __fmul_rn(__fmul_rn(v[i], r), w8[i]);

@@ -291,6 +291,17 @@ class GpuStage:
         self.tok.fill_(int(tok))
         self.steps_done = 0
 
+    def truncate(self, n: int = 0):
+        """Keep the first n cache positions and drop the rest (they are
+        masked and rewritten by what comes next): the context becomes those
+        n positions, decoding and prompts continue from position n."""
+        if not 0 <= n <= self.position:
+            raise ValueError(f"truncate({n}) with {self.position} positions held")
+        self.s0 = n
+        self.steps_done = 0
+        self.pos.fill_(n)
+        self.graph = None                          # s0 is an argument of the captured step
+
     def _take(self, n: int):
         """Claim n steps: the cache and the token history grow first when
         they lack room (the kernels would otherwise clamp the position and

@@ -5,8 +5,11 @@
 * RoPE + bias + KV-cache write: bit-exact with the reference's fp32
   expressions (hetero/cpu_model.py:195-204) evaluated by NumPy, the cache as
   NumPy's float16 rounding of the same values;
-* residual add + RMSNorm: the add bit-exact, y within 1e-6 (norm-wise) of an
-  fp64 evaluation (the mean is a tree sum, not NumPy's pairwise order);
+* residual add + RMSNorm: the add bit-exact; y bit-exact with the
+  reference's NumPy expression (hetero/cpu_model.py:164-166) for the row
+  lengths NumPy's pairwise sum halves exactly (the Qwen2 hidden sizes
+  among them), one row and several; other lengths within 1e-6 (norm-wise)
+  of an fp64 evaluation (a tree sum there);
 * attention: within 1e-5 (norm-wise) of an fp64 masked GQA softmax over the
   fp16 cache (hetero/cpu_model.py:233-252), at positions on both sides of
   the 64-position chunk boundaries;
@@ -63,10 +66,14 @@ def test_embed_row_bit_exact(torch, lib):
         assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32)), t
 
 
+PAIRWISE_EXACT = (3584, 896, 1536, 2048, 5120, 8192, 64, 120)
+
+
 def test_add_rmsnorm(torch, lib):
+    from hetero.numpy_stage import rms_norm
     rng = np.random.default_rng(4)
     dev = torch.device("cuda")
-    for n in (3584, 1000, 8192):
+    for n in PAIRWISE_EXACT + (1000, 4104):
         x = rng.normal(0, 1, n).astype(np.float32)
         d = rng.normal(0, 1, n).astype(np.float32)
         w = rng.normal(1, 0.1, n).astype(np.float32)
@@ -79,10 +86,33 @@ def test_add_rmsnorm(torch, lib):
         x64 = xs.astype(np.float64)
         ref = x64 / np.sqrt((x64 * x64).mean() + 1e-6) * w
         assert oracle.normwise_rel(y.cpu().numpy(), ref) < RMS_TOL, n
+        if n in PAIRWISE_EXACT:
+            want = rms_norm(xs, w, 1e-6)
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32)), n
         # no residual: x untouched
         rc = lib.q4_add_rmsnorm_dev(tx.data_ptr(), None, tw.data_ptr(), 1e-6, y.data_ptr(), n, sp(torch))
         assert rc == 0 and np.array_equal(tx.cpu().numpy(), xs)
     assert lib.q4_add_rmsnorm_dev(tx.data_ptr(), None, tw.data_ptr(), 1e-6, y.data_ptr(), 8193, None) == q4.Q4_EARG
+
+
+def test_add_rmsnorm_rows_bit_exact_with_numpy(torch, lib):
+    """A prompt's rows: each as the one-row kernel, all equal to NumPy's
+    rms_norm over the [rows, n] block (the reduction runs per row)."""
+    from hetero.numpy_stage import rms_norm
+    rng = np.random.default_rng(5)
+    dev = torch.device("cuda")
+    rows, n = 5, 3584
+    x = rng.normal(0, 3, (rows, n)).astype(np.float32)
+    d = rng.normal(0, 1, (rows, n)).astype(np.float32)
+    w = rng.normal(1, 0.1, n).astype(np.float32)
+    tx, td, tw = (torch.from_numpy(a).to(dev) for a in (x, d, w))
+    y = torch.empty((rows, n), device=dev)
+    rc = lib.q4_add_rmsnorm_rows_dev(tx.data_ptr(), td.data_ptr(), tw.data_ptr(), 1e-6, y.data_ptr(), rows, n,
+                                     sp(torch))
+    assert rc == 0, q4.last_error(lib)
+    xs = x + d
+    assert np.array_equal(tx.cpu().numpy(), xs)
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), rms_norm(xs[None], w, 1e-6)[0].view(np.uint32))
 
 
 def rope_np(x, cos, sin):

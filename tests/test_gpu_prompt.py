@@ -28,7 +28,21 @@ by `drift` (max |diff| / max |ref|).  The bars, per case:
     position and the token carry over.
 With no chunk above 16 rows there is no GEMM, drift is 0 and every bar is
 LOGIT_TOL.
+
+At full size -- the 28-layer Qwen2.5-7B-architecture model of the decode
+fixture, an empty cache and a 512-token prompt in one chunk -- the device
+runs against the committed fixture tests/golden/prompt_qwen7b.npz (written
+by tests/golden/make_prompt_golden.py: the oracle on the reference kernel,
+and the same with bf16 contraction operands, whose drift the fixture
+records): last-position logits within max(2 drift, LOGIT_TOL) of the
+reference path's and nearer the bf16 run's than that run is to the
+reference, the greedy token equal unless the reference's top two are
+within the error, and the keys and values of layers 0 and 27 within twice
+their recorded drift.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -40,7 +54,8 @@ pytestmark = pytest.mark.gpu
 
 LOGIT_TOL = 1e-3
 CONTEXT = 64
-needs_ref = pytest.mark.skipif(not __import__("os").path.exists(oracle.ref_path(1)), reason="oracle/_ref not built")
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+needs_ref = pytest.mark.skipif(not os.path.exists(oracle.ref_path(1)), reason="oracle/_ref not built")
 
 
 def small_cfg():
@@ -160,3 +175,51 @@ def test_cache_growth_and_capture_after_eager_steps(model):
     torch.cuda.synchronize()
     assert small.cap > cap0 + KV_STEP and small.position == CONTEXT + steps
     assert int(small.pos.item()) == CONTEXT + steps
+
+
+def test_qwen7b_prompt_full_size_vs_reference_fixture():
+    """The 512-token prompt forward of the 28-layer model against the
+    reference path's fixture."""
+    import torch
+    from hetero.gpu_model import GpuStage
+    from test_gpu_decode import _checksum_torch
+    with open(os.path.join(GOLDEN, "prompt_qwen7b.json")) as f:
+        meta = json.load(f)
+    fx = np.load(os.path.join(GOLDEN, "prompt_qwen7b.npz"))
+    with open(os.path.join(GOLDEN, "decode_qwen7b.json")) as f:
+        sums = json.load(f)
+    assert sums["seed"] == meta["seed"] and sums["config"] == meta["config"]
+    cfg, dev = meta["config"], torch.device("cuda")
+    print("generating the 28-layer model on the GPU", flush=True)
+    w = qwen2.synthetic_weights_torch(cfg, meta["seed"], dev)
+    bad = [k for k, v in sums["input_checksums"].items() if k in w and int(v) != _checksum_torch(w[k])]
+    assert not bad, f"generated weights differ from the fixture's: {bad[:5]}"
+    g = GpuStage(cfg, w, None, None, max_new=4)
+    del w
+    ids = fx["ids"].tolist()
+    print(f"prefill of {len(ids)} tokens", flush=True)
+    tok = g.prefill(ids, chunk=len(ids))
+    lg = g.logits.cpu().numpy().reshape(-1)
+    ref, bfl = fx["ref_logits"], fx["bf16_logits"]
+    drift = meta["bf16_drift"]["logits"]
+    e_ref, e_bf = oracle.normwise_rel(lg, ref), oracle.normwise_rel(lg, bfl)
+    print(f"bf16 drift {drift:.2e}; device vs reference path {e_ref:.2e}, vs bf16 run {e_bf:.2e}", flush=True)
+    failures = []
+    if not e_ref < max(2 * drift, LOGIT_TOL):
+        failures.append(f"logits {e_ref:.2e} from the reference path")
+    if not e_bf < max(drift, LOGIT_TOL):
+        failures.append(f"logits {e_bf:.2e} from the bf16 run")
+    want = int(np.argmax(ref))
+    if tok != want:
+        gap = float(ref[want]) - float(ref[tok])
+        if gap > 2 * e_ref * float(np.abs(ref).max()):
+            failures.append(f"token {tok} != {want} (gap {gap:.3e})")
+    for l in meta["kv_layers"]:
+        for kv in "kv":
+            mine = g.layers[l][f"{kv}_cache"][:, :len(ids)].cpu().numpy().astype(np.float32)
+            e = oracle.normwise_rel(mine, fx[f"kv_{l}_{kv}"].astype(np.float32))
+            d = meta["bf16_drift"][f"kv_{l}_{kv}"]
+            print(f"layer {l} {kv}: {e:.2e} from the reference path (bf16 drift {d:.2e})", flush=True)
+            if not e < max(2 * d, LOGIT_TOL):
+                failures.append(f"layer {l} {kv}: {e:.2e}")
+    assert not failures, failures
