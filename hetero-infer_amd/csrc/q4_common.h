@@ -109,22 +109,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
-// The sum of a row of n values, thread t holding the 8 values of word t
-// (values 8t .. 8t+7; threads past the row hold zeros), added in the order
-// of NumPy's float32 reductions (np.add.reduce, which x.mean() and x.sum()
-// use): pairwise summation -- a row of more than 128 values is split at
-// n2 = n/2 rounded down to a multiple of 8 and the two halves' sums are
-// added; a block of 8 < n <= 128 values is added by 8 accumulators, r[j]
-// taking values j, j + 8, j + 16, ... in order, combined as
-// ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)) (plus a sequential rest
-// when n % 8 != 0).  When every split is exact (n = L m, L a power of two,
-// m <= 128, m % 8 == 0 and each halving an exact half) the tree is perfect:
-// lane (block b, accumulator j) adds block b's column j, and lane-xor sums
-// combine the accumulators and then the blocks, which is that order since
-// IEEE addition is commutative.  Other n fall back to the wave_sum tree.
-// Every thread of the workgroup calls it (blockDim.x a multiple of 64 and
-// at least n / 8); scratch: n floats of LDS, red: 16 floats of LDS.  The
-// sum is returned in every thread.
+// The sum of a row of n non-negative values (sums of squares), thread t
+// holding the 8 values of word t (values 8t .. 8t+7; threads past the row
+// hold zeros), added in the order of NumPy's float32 reductions
+// (np.add.reduce, which x.mean() and x.sum() use): pairwise summation -- a
+// row of more than 128 values is split at n2 = n/2 rounded down to a
+// multiple of 8 and the two halves' sums are added; a block of
+// 8 <= n <= 128 values is added by 8 accumulators, r[j] taking values j,
+// j + 8, j + 16, ... in order, combined as ((r0 + r1) + (r2 + r3)) +
+// ((r4 + r5) + (r6 + r7)).  When every split is exact (n = L m with L a
+// power of two, m <= 128, m % 8 == 0, each halving an exact half) the tree
+// is perfect: lane 8b + j adds block b's column j, and pairs of lanes, then
+// of lane groups, are added -- that order, IEEE addition being commutative
+// -- by DPP within rows of 16 lanes, the 4 rows of a wave by readlane, and
+// the waves' sums through LDS; groups past the L blocks hold zeros, which
+// add exactly.  Other n fall back to a tree order (wave_sum).  Every
+// thread of the workgroup calls it (blockDim.x a multiple of 64 and at
+// least n / 8); scratch: n floats of LDS, red: 16 floats of LDS.  Returns
+// the sum in every thread, after two workgroup barriers; scratch is free
+// for other use on return, red keeps the waves' sums.
 __device__ __forceinline__ float row_sum_numpy(const float v[8], int n, float* scratch, float* red) {
     const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
     int m = n, L = 1;
@@ -142,7 +145,7 @@ __device__ __forceinline__ float row_sum_numpy(const float v[8], int n, float* s
         __syncthreads();
         float tot = 0.0f;
         for (int i = 0; i < (nt >> 6); i++) tot = __fadd_rn(tot, red[i]);
-        __syncthreads();                                           // red is free again
+        __syncthreads();
         return tot;
     }
     if (tid < (n >> 3)) {
@@ -152,23 +155,30 @@ __device__ __forceinline__ float row_sum_numpy(const float v[8], int n, float* s
     }
     __syncthreads();
     float r = 0.0f;
-    if (tid < 8 * L) {                                             // block b, accumulator j
+    if (tid < 8 * L) {                                             // block b = tid / 8, accumulator j = tid % 8
         const float* p = scratch + (tid >> 3) * m + (tid & 7);
         r = p[0];
         for (int i = 8; i < m; i += 8) r = __fadd_rn(r, p[i]);
     }
-    r = __fadd_rn(r, __shfl_xor(r, 1));
-    r = __fadd_rn(r, __shfl_xor(r, 2));
-    r = __fadd_rn(r, __shfl_xor(r, 4));
-    for (int s = 8; s < 64 && s < 8 * L; s <<= 1) r = __fadd_rn(r, __shfl_xor(r, s));
-    const int W = (8 * L + 63) >> 6;                               // waves holding blocks (a power of two)
-    if (lane == 0 && wave < W) red[wave] = r;
+    r = dpp_add<0xB1>(r);                                          // + lane ^ 1: r0 + r1, ...
+    r = dpp_add<0x4E>(r);                                          // + lane ^ 2: (r0 + r1) + (r2 + r3)
+    r = dpp_add<0x141>(r);                                         // + the half-row's other quad: the block
+    r = dpp_add<0x140>(r);                                         // + the row's other half: blocks in pairs
+    const float q0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
+    const float q1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 16));
+    const float q2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 32));
+    const float q3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 48));
+    const int W = (8 * L + 63) >> 6;                               // waves holding blocks: 1, 2, 4, ..., 16
+    if (lane == 0 && wave < W) red[wave] = __fadd_rn(__fadd_rn(q0, q1), __fadd_rn(q2, q3));
     __syncthreads();
-    float t = lane < W ? red[lane] : 0.0f;
-    for (int s = 1; s < W; s <<= 1) t = __fadd_rn(t, __shfl_xor(t, s));
-    t = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(t)));     // lane 0: the whole tree
-    __syncthreads();                                               // red and scratch are free again
-    return t;
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) t[i] = i < W ? red[i] : 0.0f;
+#pragma unroll
+    for (int s = 1; s < 16; s <<= 1)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2 * s) t[i] = __fadd_rn(t[i], t[i + s]);
+    return t[0];
 }
 
 // One packed word of x (8 values, MLX order) -> {xl even, xl odd, xh even,
