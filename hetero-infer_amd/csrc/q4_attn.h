@@ -1,23 +1,18 @@
-// Grouped-query attention of one query token over an fp16 KV cache, as
-// device functions: the partial over one (64-position chunk, kv head) job
-// and the combine of one query head's chunks.  The decode-step kernels
-// (q4_decode.hip) run them as launches of their own; the chained programs
-// (q4_chain.hip) run them as phases of one persistent launch.
+// Grouped-query attention of one query token over an fp16 KV cache, as one
+// launch (the decode-step kernels of q4_decode.hip).
 //
 // hetero/cpu_model.py:233-252 for one query token: per query head,
 // s = (q . k_t) * scale over the positions t <= pos, p = exp(s - max s),
-// o = (sum p_t v_t) / (sum p_t).  Job (chunk, kv head) takes 64 positions
-// and the G = nh / nkv query heads that share the kv head, and writes its
-// partial (max, sum, unnormalised o); the combine merges the chunks
-// (o = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c).
-//
-// The functions are called by every thread of a workgroup of at least the
-// threads they use (64 NW for the partial, 256 for the combine): the others
-// pass the same barriers and do no work.  DEV: the values another
-// workgroup of the same launch produced or consumes -- the raw q/k/v, the
-// partials, the output -- are loaded and stored at device scope (cache
-// policy sc1); with separate launches plain accesses suffice.  The
-// arithmetic does not depend on DEV.
+// o = (sum p_t v_t) / (sum p_t).  Workgroup (chunk, kv head) takes 64
+// positions and the G = nh / nkv query heads that share the kv head:
+// wave g is query head g -- for the scores and the softmax lane j takes
+// position j of the chunk (all in registers), for the weighted sum of v
+// lane i the dimensions 2i, 2i + 1.  Each wave writes its head's partial
+// result (max m, sum l, unnormalised o) and arrives at the head's counter;
+// the wave of the last chunk to arrive merges the head's parts
+// (o = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, the o sum in chunk
+// order, the l sum a fixed lane tree), so there is no second launch.  The
+// result does not depend on which chunk arrives last.
 #pragma once
 
 #include "q4_common.h"
@@ -29,6 +24,11 @@ constexpr int kMaxG = 8;          // query heads per kv head
 constexpr int kMaxD = 128;
 constexpr int kRowU4 = kMaxD / 8 + 1;   // LDS row of a chunk: 16 uint4 of fp16 + 1 pad (16-byte reads spread over the banks)
 constexpr int kMaxChunks = 1024;        // cap <= 65536
+constexpr int kAttnThreads = 64 * kMaxG;   // a wave per query head
+constexpr int kAttnCounters = 512;      // arrival counters after the partials (one per query head)
+constexpr int kCounterStride = 32;      // words between counters: each on its own 128-byte line
+constexpr int kMergeBatch = 36;         // chunks merged per round of loads (2304 positions in one round)
+constexpr int kAttnCoherent = 16;       // cache policy sc1: device-scope stores and loads of the parts
 
 __device__ __forceinline__ uint16_t attn_f2h(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
@@ -38,35 +38,18 @@ __device__ __forceinline__ float attn_h2f(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
 
-template <bool DEV>
-__device__ __forceinline__ float attn_ld(const float* p) {
-    if constexpr (DEV) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else return *p;
-}
-
-template <bool DEV>
-__device__ __forceinline__ void attn_st(float* p, float v) {
-    if constexpr (DEV) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
-}
-
-// LDS of the partial of NW waves: q [kMaxG][kMaxD], the chunk's K and V rows
-// [kChunk][kRowU4] uint4 each, p [kMaxG][kChunk], the waves' partial scores
-// [NW][kMaxG][kChunk] and outputs [NW][kMaxG][kMaxD].
-template <int NW>
-__host__ __device__ constexpr size_t attn_partial_lds_bytes() {
-    return static_cast<size_t>(kMaxG) * kMaxD * 4 + 2 * static_cast<size_t>(kChunk) * kRowU4 * 16 +
-           static_cast<size_t>(kMaxG) * kChunk * 4 + static_cast<size_t>(NW) * kMaxG * kChunk * 4 +
-           static_cast<size_t>(NW) * kMaxG * kMaxD * 4;
-}
-constexpr size_t kAttnCombineLdsBytes = (kMaxChunks + 8) * 4;
+// LDS of the kernel: q [kMaxG][kMaxD], the chunk's K and V rows
+// [kChunk][kRowU4] uint4 each, p [kMaxG][kChunk].
+constexpr size_t kAttnLdsBytes = static_cast<size_t>(kMaxG) * kMaxD * 4 +
+                                 2 * static_cast<size_t>(kChunk) * kRowU4 * 16 +
+                                 static_cast<size_t>(kMaxG) * kChunk * 4;
 
 struct AttnArgs {
     const float* q;          // raw projection outputs (ROPE) or rotated queries
     uint16_t* kc;
     uint16_t* vc;
     const int64_t* pos;
-    float* part;             // [nh][n_chunks][d + 2]
+    float* part;             // [nh][n_chunks][d + 2], then kAttnCounters arrival counters
     float* out;              // [nh][d]
     int nh, nkv, d, cap, n_chunks;
     float scale;
@@ -77,57 +60,44 @@ struct AttnArgs {
     const float* sin_t;
 };
 
-// ROPE: q, k and v are the raw projection outputs; the job applies the
-// biases and the rotary embedding to its G query heads (as rope_kv_kernel
-// does), and the job whose chunk holds the position also rotates the new
-// key, writes the new key and value rows to the cache and takes them from
-// registers instead of the cache.
-// G: query heads per kv head, a template parameter so that the per-head
-// loops unroll and their LDS reads are issued together.  NW: waves (4, or 8
-// for head_dim >= 64), which split the head dimension of the scores and the
-// positions of the outputs between them.
-template <bool ROPE, int G, int NW, bool DEV>
-__device__ __forceinline__ void attn_partial(const AttnArgs& a, int chunk, int kvh, char* lds) {
-    constexpr int NT = 64 * NW;                              // threads that work
+// ROPE: q, k and v are the raw projection outputs; the workgroup applies
+// the biases and the rotary embedding to its G query heads (as
+// rope_kv_kernel does), and the one whose chunk holds the position also
+// rotates the new key, writes the new key and value rows to the cache and
+// takes them from registers instead of the cache.  G: query heads per kv
+// head, D: head_dim (32, 64 or 128; a.d), template parameters so that the
+// loops over them unroll and their LDS reads are issued together.  Called
+// by the kAttnThreads threads of the workgroup.
+template <bool ROPE, int G, int D>
+__device__ __forceinline__ void attn_decode(const AttnArgs& a, int chunk, int kvh, char* lds) {
+    static_assert(D == 32 || D == 64 || D == 128, "head_dim 32, 64 or 128");
+    constexpr int NT = kAttnThreads;
     constexpr int KV = kChunk * (kMaxD / 8) / NT;            // uint4 of K (and of V) per thread at d = 128
-    constexpr int QR = kMaxG * (kMaxD / 2) / NT;             // rounds of the RoPE'd query pairs
-    constexpr int PW = kChunk / NW;                          // positions per wave in the output pass
+    constexpr int QR = (G * (kMaxD / 2) + NT - 1) / NT;      // rounds of the RoPE'd query pairs
     typedef float4 QRow[kMaxD / 4];
     typedef uint4 KRow[kRowU4];
-    typedef float SRow[kMaxG][kChunk];
-    typedef float ORow[kMaxG][kMaxD];
     QRow* q_s = reinterpret_cast<QRow*>(lds);                                          // [kMaxG]
     KRow* k_s = reinterpret_cast<KRow*>(lds + kMaxG * kMaxD * 4);                      // [kChunk]
     KRow* v_s = k_s + kChunk;                                                          // [kChunk]
     float(*p_s)[kChunk] = reinterpret_cast<float(*)[kChunk]>(v_s + kChunk);             // [kMaxG]
-    SRow* sc_part = reinterpret_cast<SRow*>(p_s + kMaxG);                              // [NW]
-    ORow* out_part = reinterpret_cast<ORow*>(sc_part + NW);                            // [NW]
-    const int n_chunks = a.n_chunks, d = a.d, cap = a.cap, nh = a.nh, nkv = a.nkv;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const bool act = tid < NT;                               // wave-uniform
+    const int n_chunks = a.n_chunks, cap = a.cap, nh = a.nh, nkv = a.nkv;
+    constexpr int d = D;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: the wave's resources stay scalar
     const int64_t pos = *a.pos;
     const int c0 = chunk * kChunk;
     const int64_t lim = pos + 1 < cap ? pos + 1 : cap;      // positions [0, lim)
-    const int valid = lim - c0 >= kChunk ? kChunk : static_cast<int>(lim - c0 > 0 ? lim - c0 : 0);
-    const int du4 = d >> 3;                                  // uint4 (8 fp16) per row
-    float* my = a.part;                                      // [nh][n_chunks][d + 2]
-    if (valid == 0) {                                        // chunk past the position (uniform)
-        if (act)
-            for (int e = tid; e < G * (d + 2); e += NT) {
-                const int g = e / (d + 2), i = e - g * (d + 2);
-                float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2);
-                attn_st<DEV>(dst + i, i == 0 ? -__builtin_inff() : 0.0f);
-            }
-        return;
-    }
+    if (lim <= c0) return;                                   // past the position: no part, no arrival
+    const int valid = lim - c0 >= kChunk ? kChunk : static_cast<int>(lim - c0);
+    const int n_act = static_cast<int>((lim + kChunk - 1) / kChunk);   // chunks that arrive
+    constexpr int du4 = d >> 3;                              // uint4 (8 fp16) per row
     // the chunk's new row (the position) comes from registers, not the cache
     const bool fresh = ROPE && pos >= c0 && pos < c0 + kChunk && pos < cap;
     const int frow = fresh ? static_cast<int>(pos - c0) : -1;
-    if (act) {
-        // every load up front: q, the chunk's K and V rows (4 uint4 each per
-        // thread at d = 128), unconditional, through resources that end with
-        // the rows to read: rows past `valid` (and a fresh row) read 0
-        // without an access, and the staging registers stay registers
+    // every load up front: q, the chunk's K and V rows, unconditional,
+    // through resources that end with the rows to read: rows past `valid`
+    // (and a fresh row) read 0 without an access
+    {
         const int nkv4 = (fresh ? valid - 1 : valid) * du4;
         const __amdgpu_buffer_rsrc_t kr =
             buf_rsrc(a.kc + (static_cast<size_t>(kvh) * cap + c0) * d, static_cast<uint32_t>(nkv4) * 16u);
@@ -155,7 +125,7 @@ __device__ __forceinline__ void attn_partial(const AttnArgs& a, int chunk, int k
                 if (e < G * half) {
                     const int g = e / half, i = e - g * half;
                     const int e1 = (kvh * G + g) * d + i;
-                    qa[r][0] = attn_ld<DEV>(a.q + e1); qa[r][1] = attn_ld<DEV>(a.q + e1 + half);
+                    qa[r][0] = a.q[e1]; qa[r][1] = a.q[e1 + half];
                     qb[r][0] = a.bias[e1]; qb[r][1] = a.bias[e1 + half];
                     cs[r][0] = a.cos_t[prow * half + i]; cs[r][1] = a.sin_t[prow * half + i];
                 }
@@ -164,12 +134,12 @@ __device__ __forceinline__ void attn_partial(const AttnArgs& a, int chunk, int k
             if (fresh) {
                 if (tid < half) {
                     const int e1 = kvh * d + tid;
-                    nk[0] = attn_ld<DEV>(a.kraw + e1); nk[1] = attn_ld<DEV>(a.kraw + e1 + half);
+                    nk[0] = a.kraw[e1]; nk[1] = a.kraw[e1 + half];
                     nkb[0] = a.bias[nh * d + e1]; nkb[1] = a.bias[nh * d + e1 + half];
                     nkc[0] = a.cos_t[prow * half + tid]; nkc[1] = a.sin_t[prow * half + tid];
                 } else if (tid < half + d) {
                     const int e = kvh * d + (tid - half);
-                    nv = attn_ld<DEV>(a.vraw + e);
+                    nv = a.vraw[e];
                     nvb = a.bias[(nh + nkv) * d + e];
                 }
             }
@@ -203,10 +173,7 @@ __device__ __forceinline__ void attn_partial(const AttnArgs& a, int chunk, int k
         } else {
             const int nq4 = G * d / 4;
             float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (tid < nq4) {
-                const float* qp = a.q + static_cast<size_t>(kvh * G) * d + 4 * tid;
-                qv = make_float4(attn_ld<DEV>(qp), attn_ld<DEV>(qp + 1), attn_ld<DEV>(qp + 2), attn_ld<DEV>(qp + 3));
-            }
+            if (tid < nq4) qv = reinterpret_cast<const float4*>(a.q + static_cast<size_t>(kvh * G) * d)[tid];
             load_kv();
             if (tid < nq4) q_s[tid / (d / 4)][tid % (d / 4)] = qv;
         }
@@ -221,9 +188,9 @@ __device__ __forceinline__ void attn_partial(const AttnArgs& a, int chunk, int k
             }
         }
         if (fresh) {
-            const int row = frow, half = d >> 1;
-            uint16_t* kl = reinterpret_cast<uint16_t*>(&k_s[row][0]);
-            uint16_t* vl = reinterpret_cast<uint16_t*>(&v_s[row][0]);
+            const int half = d >> 1;
+            uint16_t* kl = reinterpret_cast<uint16_t*>(&k_s[frow][0]);
+            uint16_t* vl = reinterpret_cast<uint16_t*>(&v_s[frow][0]);
             if (tid < half) {
                 kl[tid] = fh1;
                 kl[tid + half] = fh2;
@@ -233,194 +200,144 @@ __device__ __forceinline__ void attn_partial(const AttnArgs& a, int chunk, int k
         }
     }
     __syncthreads();
-    // scores: wave w takes dims [w*d/NW, (w+1)*d/NW) of every position of
-    // the chunk (lane = position) for all G heads, so each K element is
-    // converted once; the NW partial dots are added in wave order below
-    if (act) {
-        const int s = lane;
-        const int c_begin = wave * (du4 / NW), c_end = c_begin + du4 / NW;
-        float acc[kMaxG];
+    const int g = wave;                                      // this wave's query head (uniform)
+    const int h = kvh * G + g;
+    const int stride = d + 2;
+    const int i = lane;
+    constexpr int dp = d >> 1;
+    if (g >= G) return;
+    {
+        // scores: lane j = position c0 + j, the dimensions in four
+        // interleaved partial sums
+        const int j = lane;
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int g = 0; g < kMaxG; g++) acc[g] = 0.0f;
-        for (int c = c_begin; c < c_end; c++) {
-            const uint4 kk = k_s[s][c];
-            const float kf[8] = {attn_h2f(static_cast<uint16_t>(kk.x)), attn_h2f(static_cast<uint16_t>(kk.x >> 16)),
-                                 attn_h2f(static_cast<uint16_t>(kk.y)), attn_h2f(static_cast<uint16_t>(kk.y >> 16)),
-                                 attn_h2f(static_cast<uint16_t>(kk.z)), attn_h2f(static_cast<uint16_t>(kk.z >> 16)),
-                                 attn_h2f(static_cast<uint16_t>(kk.w)), attn_h2f(static_cast<uint16_t>(kk.w >> 16))};
-#pragma unroll
-            for (int g = 0; g < kMaxG; g++) {
-                if (g < G) {                                         // uniform
-                    const float4 qa = q_s[g][2 * c], qb = q_s[g][2 * c + 1];
-                    acc[g] = __builtin_fmaf(qa.x, kf[0], acc[g]);
-                    acc[g] = __builtin_fmaf(qa.y, kf[1], acc[g]);
-                    acc[g] = __builtin_fmaf(qa.z, kf[2], acc[g]);
-                    acc[g] = __builtin_fmaf(qa.w, kf[3], acc[g]);
-                    acc[g] = __builtin_fmaf(qb.x, kf[4], acc[g]);
-                    acc[g] = __builtin_fmaf(qb.y, kf[5], acc[g]);
-                    acc[g] = __builtin_fmaf(qb.z, kf[6], acc[g]);
-                    acc[g] = __builtin_fmaf(qb.w, kf[7], acc[g]);
-                }
-            }
+        for (int c = 0; c < du4; c++) {
+            const uint4 kk = k_s[j][c];
+            const float4 qa = q_s[g][2 * c], qb = q_s[g][2 * c + 1];
+            acc[0] = __builtin_fmaf(qa.x, attn_h2f(static_cast<uint16_t>(kk.x)), acc[0]);
+            acc[1] = __builtin_fmaf(qa.y, attn_h2f(static_cast<uint16_t>(kk.x >> 16)), acc[1]);
+            acc[2] = __builtin_fmaf(qa.z, attn_h2f(static_cast<uint16_t>(kk.y)), acc[2]);
+            acc[3] = __builtin_fmaf(qa.w, attn_h2f(static_cast<uint16_t>(kk.y >> 16)), acc[3]);
+            acc[0] = __builtin_fmaf(qb.x, attn_h2f(static_cast<uint16_t>(kk.z)), acc[0]);
+            acc[1] = __builtin_fmaf(qb.y, attn_h2f(static_cast<uint16_t>(kk.z >> 16)), acc[1]);
+            acc[2] = __builtin_fmaf(qb.z, attn_h2f(static_cast<uint16_t>(kk.w)), acc[2]);
+            acc[3] = __builtin_fmaf(qb.w, attn_h2f(static_cast<uint16_t>(kk.w >> 16)), acc[3]);
         }
-#pragma unroll
-        for (int g = 0; g < kMaxG; g++)
-            if (g < G) sc_part[wave][g][s] = acc[g];
-    }
-    __syncthreads();
-    // softmax over the chunk, heads wave, wave + NW, ... (lane = position)
-    if (act) {
-        for (int g = wave; g < G; g += NW) {
-            const int s = lane;
-            float dot = sc_part[0][g][s];
-#pragma unroll
-            for (int w = 1; w < NW; w++) dot = __fadd_rn(dot, sc_part[w][g][s]);
-            const float sc = s < valid ? __fmul_rn(dot, a.scale) : -__builtin_inff();
-            const float m = wave_max(sc);
-            const float p = s < valid ? expf(__fsub_rn(sc, m)) : 0.0f;
-            const float l = wave_sum(p);
-            p_s[g][s] = p;
-            if (lane == 0) {
-                float* dst = my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2);
-                attn_st<DEV>(dst, m);
-                attn_st<DEV>(dst + 1, l);
-            }
-        }
-    }
-    __syncthreads();
-    // unnormalised outputs: wave w takes positions [PW*w, PW*w + PW), lane
-    // = fp16 pair of the row, all G heads; the NW partial outputs are
-    // added in wave order
-    if (act) {
-        const int i = lane, dp = d >> 1;
-        float a0[kMaxG], a1[kMaxG];
-#pragma unroll
-        for (int g = 0; g < kMaxG; g++) a0[g] = a1[g] = 0.0f;
+        const float dot = __fadd_rn(__fadd_rn(acc[0], acc[1]), __fadd_rn(acc[2], acc[3]));
+        // softmax over the chunk (lane = position; position c0 is visible, so
+        // m is finite)
+        const float sc = j < valid ? __fmul_rn(dot, a.scale) : -__builtin_inff();
+        const float m = wave_max(sc);
+        const float p = j < valid ? expf(__fsub_rn(sc, m)) : 0.0f;
+        const float l = wave_sum(p);
+        p_s[g][j] = p;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // unnormalised output: lane i = dimensions 2i, 2i + 1; positions in
+        // order (p is 0 and the V row is 0 past the valid positions); stored
+        // at device scope
+        float* my = a.part + (static_cast<size_t>(h) * n_chunks + chunk) * stride;
+        const __amdgpu_buffer_rsrc_t pr = buf_rsrc(my, static_cast<uint32_t>(stride) * 4u);
+        using u32x2 = unsigned int __attribute__((ext_vector_type(2)));
         if (i < dp) {
             const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v_s[0][0]);
             constexpr int kRowW = kRowU4 * 4;
-            // p is 0 and the V row is 0 past the valid positions
-            for (int s0 = PW * wave; s0 < PW * wave + PW; s0 += 4) {
-                uint32_t w2[4];
+            float a0 = 0.0f, a1 = 0.0f;
+            // 16 positions' V words and p values per round, loaded together
 #pragma unroll
-                for (int j = 0; j < 4; j++) w2[j] = vw[(s0 + j) * kRowW + i];
-                float4 pg[kMaxG];
+            for (int s0 = 0; s0 < kChunk; s0 += 16) {
+                uint32_t w2[16];
+                float4 p4[4];
 #pragma unroll
-                for (int g = 0; g < kMaxG; g++)
-                    if (g < G) pg[g] = *reinterpret_cast<const float4*>(&p_s[g][s0]);
+                for (int t = 0; t < 16; t++) w2[t] = vw[(s0 + t) * kRowW + i];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float v0 = attn_h2f(static_cast<uint16_t>(w2[j]));
-                    const float v1 = attn_h2f(static_cast<uint16_t>(w2[j] >> 16));
+                for (int k = 0; k < 4; k++) p4[k] = *reinterpret_cast<const float4*>(&p_s[g][s0 + 4 * k]);
 #pragma unroll
-                    for (int g = 0; g < kMaxG; g++) {
-                        if (g < G) {
-                            const float p = j == 0 ? pg[g].x : j == 1 ? pg[g].y : j == 2 ? pg[g].z : pg[g].w;
-                            a0[g] = __builtin_fmaf(p, v0, a0[g]);
-                            a1[g] = __builtin_fmaf(p, v1, a1[g]);
-                        }
-                    }
+                for (int t = 0; t < 16; t++) {
+                    const float4 q4 = p4[t >> 2];
+                    const float pv = (t & 3) == 0 ? q4.x : (t & 3) == 1 ? q4.y : (t & 3) == 2 ? q4.z : q4.w;
+                    a0 = __builtin_fmaf(pv, attn_h2f(static_cast<uint16_t>(w2[t])), a0);
+                    a1 = __builtin_fmaf(pv, attn_h2f(static_cast<uint16_t>(w2[t] >> 16)), a1);
                 }
             }
-#pragma unroll
-            for (int g = 0; g < kMaxG; g++)
-                if (g < G) {
-                    out_part[wave][g][2 * i] = a0[g];
-                    out_part[wave][g][2 * i + 1] = a1[g];
-                }
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(a0), __float_as_uint(a1)}, pr,
+                                                  (2 + 2 * i) * 4u, 0, kAttnCoherent);
         }
+        if (lane == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m), __float_as_uint(l)}, pr, 0u, 0,
+                                                  kAttnCoherent);
+        __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0): this wave's part is stored
     }
-    __syncthreads();
-    if (act)
-        for (int e = tid; e < G * d; e += NT) {
-            const int g = e / d, j = e - g * d;
-            float o = out_part[0][g][j];
-#pragma unroll
-            for (int w = 1; w < NW; w++) o = __fadd_rn(o, out_part[w][g][j]);
-            attn_st<DEV>(my + (static_cast<size_t>(kvh * G + g) * n_chunks + chunk) * (d + 2) + 2 + j, o);
-        }
-}
-
-// The combine of query head h: M = max_c m_c, w_c = e^(m_c - M),
-// o = sum_c w_c o_c / sum_c w_c l_c, on 256 threads.  Every load is issued
-// before the first reduction: m and l of chunk c by thread c (c + 256, ...),
-// and thread (part k, dim i) prefetches o[i] of its chunks k, k + nparts, ...
-// (nparts = 256 / d) -- one round of memory latency instead of three.
-// lds: kAttnCombineLdsBytes.
-template <bool DEV>
-__device__ __forceinline__ void attn_combine(const AttnArgs& a, int h, char* lds) {
-    constexpr int NT = 256;
-    float* w_s = reinterpret_cast<float*>(lds);                       // [kMaxChunks]
-    float* red = w_s + kMaxChunks;                                    // [8]
-    const int tid = threadIdx.x;
-    const bool act = tid < NT;                                        // wave-uniform
-    const int n_chunks = a.n_chunks, d = a.d;
-    const int stride = d + 2;
-    const int i = tid % d, part_k = tid / d;
-    const int nparts = NT / d;
-    constexpr int kAux = DEV ? 16 : 0;                                // sc1 when DEV
-    const __amdgpu_buffer_rsrc_t pr = buf_rsrc(a.part + static_cast<size_t>(h) * n_chunks * stride,
-                                               static_cast<uint32_t>(n_chunks * stride) * 4u);
-    auto ld = [&](int c, int k) {                 // element k of chunk c (0 past the last chunk)
-        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             pr, static_cast<uint32_t>(c * stride + k) * 4u, 0, kAux));
+    // the query head's arrival: one per chunk, the last merges (each wave
+    // on its own: no workgroup barrier after the staging)
+    unsigned* count = reinterpret_cast<unsigned*>(a.part + static_cast<size_t>(nh) * n_chunks * stride) +
+                      h * kCounterStride;
+    int last = 0;
+    if (lane == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        last = __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               static_cast<unsigned>(n_act - 1);
+        if (last) __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    {
+    // the merge of query head h: lane c takes the (m, l) of chunks c,
+    // c + 64, ...: the maximum M over all chunks, the weights e^(m_c - M)
+    // and the lane tree of the w_c l_c; lane i then adds w_c o_c for its
+    // dimensions 2i, 2i + 1 in chunk order, w_c read from lane c.  The first
+    // kMergeBatch chunks' o and the first 64 chunks' (m, l) are loaded in
+    // one round; loads past the arrived chunks read 0 and their weights are
+    // 0, so they add exactly nothing.
+    const float* ph = a.part + static_cast<size_t>(h) * n_chunks * stride;
+    const __amdgpu_buffer_rsrc_t hr = buf_rsrc(ph, static_cast<uint32_t>(n_act * stride) * 4u);
+    auto ld_ml = [&](int c) {                    // (m, l) of chunk c; (0, 0) past the arrived chunks
+        return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                              hr, static_cast<uint32_t>(c * stride) * 4u, 0, kAttnCoherent));
     };
-    constexpr int kPre = 32;                      // o values prefetched per thread
-    constexpr int kMl = kMaxChunks / NT;          // chunks per thread for m and l
-    float ob[kPre], mv[kMl], lv[kMl];
-    if (act) {
+    auto ld_o = [&](int c) {                     // o[2i], o[2i + 1] of chunk c
+        return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                              hr, static_cast<uint32_t>(c * stride + 2 + 2 * i) * 4u, 0,
+                                              kAttnCoherent));
+    };
+    float2 ob[kMergeBatch];
 #pragma unroll
-        for (int j = 0; j < kPre; j++) ob[j] = ld(part_k + j * nparts, 2 + i);
+    for (int c = 0; c < kMergeBatch; c++) ob[c] = ld_o(c);
+    const float2 ml0 = ld_ml(lane);
+    float mloc = lane < n_act ? ml0.x : -__builtin_inff();
+    for (int c = lane + 64; c < n_act; c += 64) mloc = fmaxf(mloc, ld_ml(c).x);
+    const float M = wave_max(mloc);
+    auto weight = [&](float2 ml, int c) {
+        return c < n_act && ml.x != -__builtin_inff() ? expf(__fsub_rn(ml.x, M)) : 0.0f;
+    };
+    float w = weight(ml0, lane);                 // lane c: the weight of chunk c (of this round of 64)
+    float lloc = __fmul_rn(ml0.y, w);
+    float o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kMl; r++) {
-            mv[r] = ld(tid + NT * r, 0);
-            lv[r] = ld(tid + NT * r, 1);
-        }
-        float mloc = -__builtin_inff();
-#pragma unroll
-        for (int r = 0; r < kMl; r++)
-            if (tid + NT * r < n_chunks) mloc = fmaxf(mloc, mv[r]);
-        mloc = wave_max(mloc);
-        if ((tid & 63) == 0) red[tid >> 6] = mloc;
+    for (int c = 0; c < kMergeBatch; c++) {
+        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c));
+        o0 = __builtin_fmaf(ob[c].x, wc, o0);
+        o1 = __builtin_fmaf(ob[c].y, wc, o1);
     }
-    __syncthreads();
-    float M = -__builtin_inff();
-    for (int k = 0; k < (NT >> 6); k++) M = fmaxf(M, red[k]);
-    __syncthreads();
-    if (act) {
-        float lloc = 0.0f;
-#pragma unroll
-        for (int r = 0; r < kMl; r++) {
-            const int c = tid + NT * r;
-            if (c < n_chunks) {
-                const float wgt = mv[r] == -__builtin_inff() ? 0.0f : expf(__fsub_rn(mv[r], M));
-                w_s[c] = wgt;
-                lloc = __builtin_fmaf(lv[r], wgt, lloc);
-            }
+    for (int c = kMergeBatch; c < n_act; c++) {
+        if (c % 64 == 0) {                       // the next round of 64 chunks' weights
+            const float2 ml = ld_ml(c + lane);
+            w = weight(ml, c + lane);
+            lloc = __builtin_fmaf(ml.y, w, lloc);
         }
-        lloc = wave_sum(lloc);
-        if ((tid & 63) == 0) red[tid >> 6] = lloc;
+        const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), c % 64));
+        const float2 o = ld_o(c);
+        o0 = __builtin_fmaf(o.x, wc, o0);
+        o1 = __builtin_fmaf(o.y, wc, o1);
     }
-    __syncthreads();
-    float L = 0.0f;
-    for (int k = 0; k < (NT >> 6); k++) L = __fadd_rn(L, red[k]);
-    // the part's chunks in order: the prefetched ones, then any past them
-    float O = 0.0f;
-    if (act) {
-#pragma unroll
-        for (int j = 0; j < kPre; j++) {
-            const int c = part_k + j * nparts;
-            if (c < n_chunks) O = __builtin_fmaf(ob[j], w_s[c], O);
-        }
-        for (int c = part_k + kPre * nparts; c < n_chunks; c += nparts) O = __builtin_fmaf(ld(c, 2 + i), w_s[c], O);
+    const float L = wave_sum(lloc);
+    if (i < dp) {
+        float* dst = a.out + static_cast<size_t>(h) * d + 2 * i;
+        dst[0] = __fdiv_rn(o0, L);
+        dst[1] = __fdiv_rn(o1, L);
     }
-    __syncthreads();
-    float* o_s = w_s;                                        // the weights are no longer read
-    if (act) o_s[part_k * d + i] = O;
-    __syncthreads();
-    if (act && part_k == 0) {
-        for (int k = 1; k < nparts; k++) O = __fadd_rn(O, o_s[k * d + i]);
-        attn_st<DEV>(a.out + static_cast<size_t>(h) * d + i, __fdiv_rn(O, L));
     }
 }
 

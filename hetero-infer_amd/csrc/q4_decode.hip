@@ -153,20 +153,19 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
 }
 
 // ---------------------------------------------------------- attention ---
-// The partial and combine of q4_attn.h, each as a launch of its own: the
-// partial over grid (chunk, kv head), the combine over grid (query head).
-template <bool ROPE, int G, int NW>
-__global__ __launch_bounds__(64 * NW) void attn_partial_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) char lds[attn_partial_lds_bytes<NW>()];
-    attn_partial<ROPE, G, NW, false>(a, blockIdx.x, blockIdx.y, lds);
+// attn_decode of q4_attn.h as one launch over grid (chunk, kv head).
+template <bool ROPE, int G, int D>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) char lds[kAttnLdsBytes];
+    attn_decode<ROPE, G, D>(a, blockIdx.x, blockIdx.y, lds);
 }
 
-template <bool ROPE, int NW>
-void launch_partial_nw(int G, dim3 grid, hipStream_t st, const AttnArgs& a) {
+template <bool ROPE, int D>
+void launch_attention_d(int G, dim3 grid, hipStream_t st, const AttnArgs& a) {
     switch (G) {
 #define Q4_ATTN_CASE(g)                                                                                      \
     case g:                                                                                                  \
-        hipLaunchKernelGGL((attn_partial_kernel<ROPE, g, NW>), grid, dim3(64 * NW), 0, st, a);              \
+        hipLaunchKernelGGL((attn_decode_kernel<ROPE, g, D>), grid, dim3(kAttnThreads), 0, st, a);          \
         break;
         Q4_ATTN_CASE(1) Q4_ATTN_CASE(2) Q4_ATTN_CASE(3) Q4_ATTN_CASE(4)
         Q4_ATTN_CASE(5) Q4_ATTN_CASE(6) Q4_ATTN_CASE(7) Q4_ATTN_CASE(8)
@@ -175,18 +174,12 @@ void launch_partial_nw(int G, dim3 grid, hipStream_t st, const AttnArgs& a) {
     }
 }
 
-// 8 waves when every wave gets a whole uint4 of the head dimension (d >= 64)
+// head_dim 32, 64 or 128 (the callers check)
 template <bool ROPE>
-void launch_partial(int G, dim3 grid, hipStream_t st, const AttnArgs& a) {
-    if (a.d >= 64)
-        launch_partial_nw<ROPE, 8>(G, grid, st, a);
-    else
-        launch_partial_nw<ROPE, 4>(G, grid, st, a);
-}
-
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) char lds[kAttnCombineLdsBytes];
-    attn_combine<false>(a, blockIdx.x, lds);
+void launch_attention(int G, dim3 grid, hipStream_t st, const AttnArgs& a) {
+    if (a.d == 128) launch_attention_d<ROPE, 128>(G, grid, st, a);
+    else if (a.d == 64) launch_attention_d<ROPE, 64>(G, grid, st, a);
+    else launch_attention_d<ROPE, 32>(G, grid, st, a);
 }
 
 // ---------------------------------------------------------------- argmax ---
@@ -389,14 +382,15 @@ int q4_silu_mul_dev(const float* g, const float* u, float* h, long n, void* stre
 long q4_attention_scratch_floats(int n_heads, int head_dim, int cap) {
     if (n_heads <= 0 || head_dim <= 0 || cap <= 0) return 0;
     const long n_chunks = (cap + kChunk - 1) / kChunk;
-    return static_cast<long>(n_heads) * n_chunks * (head_dim + 2);
+    return static_cast<long>(n_heads) * n_chunks * (head_dim + 2) + kAttnCounters * kCounterStride;
 }
 
 int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int64_t* pos,
                      float* out, float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale,
                      void* stream) {
     if (!q || !k_cache || !v_cache || !pos || !out || !scratch) return fail(Q4_EARG, "q4_attention_dev: null pointer");
-    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kMaxG || head_dim <= 0 || head_dim % 2 ||
+    if (n_heads <= 0 || n_kv <= 0 || n_heads > kAttnCounters || n_heads % n_kv || n_heads / n_kv > kMaxG ||
+        head_dim <= 0 || head_dim % 2 ||
         head_dim > kMaxD || cap <= 0)
         return fail(Q4_EARG, "q4_attention_dev: unsupported sizes (heads %d, kv heads %d, head_dim %d, cap %d)",
                     n_heads, n_kv, head_dim, cap);
@@ -409,10 +403,8 @@ int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_
     hipStream_t st = static_cast<hipStream_t>(stream);
     const AttnArgs a{q, const_cast<uint16_t*>(k_cache), const_cast<uint16_t*>(v_cache), pos, scratch, out, n_heads,
                      n_kv, head_dim, cap, n_chunks, scale, nullptr, nullptr, nullptr, nullptr, nullptr};
-    launch_partial<false>(n_heads / n_kv, dim3(n_chunks, n_kv), st, a);
-    if (int rc = check_launch("q4_attention_dev (partial)")) return rc;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(256), 0, st, a);
-    return check_launch("q4_attention_dev (combine)");
+    launch_attention<false>(n_heads / n_kv, dim3(n_chunks, n_kv), st, a);
+    return check_launch("q4_attention_dev");
 }
 
 int q4_attention_rope_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,
@@ -420,7 +412,8 @@ int q4_attention_rope_dev(const float* q, const float* k, const float* v, const 
                           float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream) {
     if (!q || !k || !v || !bias || !cos_t || !sin_t || !pos || !k_cache || !v_cache || !out || !scratch)
         return fail(Q4_EARG, "q4_attention_rope_dev: null pointer");
-    if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kMaxG || head_dim <= 0 || head_dim % 32 ||
+    if (n_heads <= 0 || n_kv <= 0 || n_heads > kAttnCounters || n_heads % n_kv || n_heads / n_kv > kMaxG ||
+        head_dim <= 0 || head_dim % 32 ||
         256 % head_dim || head_dim > kMaxD || cap <= 0 || (cap + kChunk - 1) / kChunk > kMaxChunks ||
         (reinterpret_cast<uintptr_t>(k_cache) & 15) || (reinterpret_cast<uintptr_t>(v_cache) & 15) ||
         (reinterpret_cast<uintptr_t>(scratch) & 7))
@@ -430,10 +423,8 @@ int q4_attention_rope_dev(const float* q, const float* k, const float* v, const 
     hipStream_t st = static_cast<hipStream_t>(stream);
     const AttnArgs a{q, k_cache, v_cache, pos, scratch, out, n_heads, n_kv, head_dim, cap, n_chunks, scale,
                      k, v, bias, cos_t, sin_t};
-    launch_partial<true>(n_heads / n_kv, dim3(n_chunks, n_kv), st, a);
-    if (int rc = check_launch("q4_attention_rope_dev (partial)")) return rc;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(n_heads), dim3(256), 0, st, a);
-    return check_launch("q4_attention_rope_dev (combine)");
+    launch_attention<true>(n_heads / n_kv, dim3(n_chunks, n_kv), st, a);
+    return check_launch("q4_attention_rope_dev");
 }
 
 int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0, int hist_len,

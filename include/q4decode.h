@@ -112,23 +112,28 @@ int q4_silu_mul_dev(const float* g, const float* u, float* h, long n, void* stre
 int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int rows,
                             int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream);
 
-/* Floats of scratch memory q4_attention_dev needs for these sizes. */
+/* Floats of scratch memory q4_attention_dev needs for these sizes: the
+ * chunks' partial results and, at the end, 512 arrival counters (one per
+ * 128-byte line: 16384 floats), which must
+ * be zero before the first call (allocate the scratch zeroed); every call
+ * leaves them zero.  Calls that overlap in time on one scratch race. */
 long q4_attention_scratch_floats(int n_heads, int head_dim, int cap);
 
 /* Grouped-query attention of one query token over cache positions
  * [0, *pos] (hetero/cpu_model.py:233-252 sdpa: scores q.k * scale, softmax
  * with the maximum subtracted, weighted sum of v; query head h uses kv head
  * h / (n_heads / n_kv)).  q [n_heads][d] fp32, caches fp16 [nkv][cap][d],
- * out [n_heads][d] fp32.  The context is split in chunks of 64 positions
- * (one workgroup per kv head and chunk), whose partial softmax results are
- * combined by a second launch; scratch holds them
- * (q4_attention_scratch_floats).  head_dim 32, 64 or 128; at most 8 query
- * heads per kv head; cap <= 65536. */
+ * out [n_heads][d] fp32.  One launch: the context is split in chunks of 64
+ * positions (one workgroup per kv head and chunk) whose partial softmax
+ * results go to scratch (q4_attention_scratch_floats); for each query
+ * head, the last chunk to finish merges the head's parts.  head_dim 32, 64
+ * or 128; at most 8 query heads per kv head, at most 512 query heads;
+ * cap <= 65536. */
 int q4_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, const int64_t* pos,
                      float* out, float* scratch, int n_heads, int n_kv, int head_dim, int cap, float scale,
                      void* stream);
 
-/* q4_rope_kv_dev followed by q4_attention_dev, in the same two launches as
+/* q4_rope_kv_dev followed by q4_attention_dev, in the one launch of
  * q4_attention_dev: q, k, v are the raw projection outputs (fp32 [n_heads*d],
  * [n_kv*d], [n_kv*d]) and bias/cos_t/sin_t are as for q4_rope_kv_dev; the
  * workgroups apply bias and RoPE to the query heads they need, and the one

@@ -145,8 +145,10 @@ def test_decode_kernel_argument_errors(lib):
     assert lib.q4_norm_gate_up_silu_dev(*([p] * 6), p, None, p, 1e-6, None, p, 64, 8256, 64, None) == q4.Q4_EARG
     assert lib.q4_norm_gate_up_silu_dev(*([p] * 6), p, p, p, 1e-6, p, p, 64, 256, 64, None) == q4.Q4_EARG
     assert lib.q4_norm_gate_up_silu_dev(*([p] * 6), p, None, p, 1e-6, None, p, 64, 256, 128, None) == q4.Q4_EARG
-    assert lib.q4_attention_scratch_floats(28, 128, 2048) == 28 * 32 * 130
-    assert lib.q4_attention_scratch_floats(28, 128, 2049) == 28 * 33 * 130
+    # the chunks' parts, then 512 arrival counters, one per 128-byte line
+    assert lib.q4_attention_scratch_floats(28, 128, 2048) == 28 * 32 * 130 + 512 * 32
+    assert lib.q4_attention_scratch_floats(28, 128, 2049) == 28 * 33 * 130 + 512 * 32
+    assert lib.q4_attention_dev(*([p] * 6), 520, 65, 128, 64, 0.1, None) == q4.Q4_EARG   # 520 query heads
 
 
 def test_wire_codec_argument_errors(lib):

@@ -194,10 +194,11 @@ def test_attention(torch, lib, nh, nkv):
 
 
 def test_attention_long_context(torch, lib):
-    """Contexts past the combine's prefetch (32 chunks of 64 positions per
-    part) and past one chunk per thread for m and l (256 chunks would be the
-    next step): up to 79 chunks, the ones beyond the prefetch merged by the
-    combine's fallback loop, against the fp64 reference."""
+    """Contexts past one round of the merge's loads (36 chunks of 64
+    positions): up to 79 chunks, the ones past the first round merged by
+    the loop after it, against the fp64 reference; the arrival counters
+    are back at zero after every call, and repeated calls give the same
+    bits whichever chunk arrives last."""
     rng = np.random.default_rng(9)
     nh, nkv, d, cap = 28, 4, 128, 5000
     scale = np.float32(d ** -0.5)
@@ -208,13 +209,19 @@ def test_attention_long_context(torch, lib):
     kc, vc, tq = (torch.from_numpy(a).to(dev) for a in (kc_np, vc_np, q_np))
     out = torch.empty(nh * d, device=dev)
     scratch = torch.zeros(lib.q4_attention_scratch_floats(nh, d, cap), device=dev)
-    for p in (2559, 2560, 2561, 4095, 4096, cap - 1):
+    for p in (2303, 2304, 2559, 2560, 2561, 4095, 4096, cap - 1):
         pos = torch.tensor([p], dtype=torch.int64, device=dev)
         rc = lib.q4_attention_dev(tq.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(),
                                   scratch.data_ptr(), nh, nkv, d, cap, float(scale), sp(torch))
         assert rc == 0, q4.last_error(lib)
         ref = attention_ref(q_np, kc_np, vc_np, p, nh, nkv, float(scale))
         assert oracle.normwise_rel(out.cpu().numpy(), ref) < ATTN_TOL, p
+        assert int(scratch[-512 * 32:].view(torch.int32).abs().sum().item()) == 0, p
+        first = out.clone()
+        for _ in range(4):
+            lib.q4_attention_dev(tq.data_ptr(), kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(),
+                                 scratch.data_ptr(), nh, nkv, d, cap, float(scale), sp(torch))
+            assert torch.equal(out.view(torch.int32), first.view(torch.int32)), p
 
 
 @pytest.mark.parametrize("nh,nkv", [(28, 4), (8, 8), (16, 2)])
