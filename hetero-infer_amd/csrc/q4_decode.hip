@@ -275,6 +275,14 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float2* __restr
 // The argmax partials: a fixed array in device memory, one per GPU.
 static __device__ __align__(256) float2 argmax_scratch[kArgmaxParts];
 
+// Threads of an add_rmsnorm_kernel workgroup: a word (8 values) each, whole
+// waves (the sum's order does not depend on the count: threads past the
+// row hold zeros).
+int norm_threads(int n) {
+    const int words = (n + kNormPer - 1) / kNormPer;
+    return ((words + 63) / 64) * 64;
+}
+
 int check_launch(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "%s launch: %s", what, hipGetErrorString(e));
@@ -319,8 +327,8 @@ int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, 
     if (!x || !w || !y) return fail(Q4_EARG, "q4_add_rmsnorm_dev: null pointer");
     if (n <= 0 || n > kNormPer * 1024) return fail(Q4_EARG, "q4_add_rmsnorm_dev: n = %d outside [1, %d]", n,
                                                    kNormPer * 1024);
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), x, delta, w,
-                       eps, y, n);
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(norm_threads(n)), 0, static_cast<hipStream_t>(stream), x,
+                       delta, w, eps, y, n);
     return check_launch("q4_add_rmsnorm_dev");
 }
 
@@ -330,8 +338,8 @@ int q4_add_rmsnorm_rows_dev(float* x, const float* delta, const float* w, float 
     if (rows < 0 || n <= 0 || n > kNormPer * 1024)
         return fail(Q4_EARG, "q4_add_rmsnorm_rows_dev: rows = %d, n = %d (n in [1, %d])", rows, n, kNormPer * 1024);
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(1024), 0, static_cast<hipStream_t>(stream), x, delta, w,
-                       eps, y, n);
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(norm_threads(n)), 0, static_cast<hipStream_t>(stream),
+                       x, delta, w, eps, y, n);
     return check_launch("q4_add_rmsnorm_rows_dev");
 }
 

@@ -60,18 +60,19 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-template <int G>
+template <int G, int D>
 __global__ __launch_bounds__(64 * kPRows) void prompt_attn_kernel(PromptAttnArgs a) {
     __shared__ uint4 k_s[kPTile][kPRowU4];
     __shared__ uint4 v_s[kPTile][kPRowU4];
     __shared__ float4 q_s[kPRows][G][kPMaxD / 4];
     __shared__ float4 p_s[kPRows][G][kPTile / 4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: the row's branches stay scalar
     const int kvh = blockIdx.y;
     const int r0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * kPRows;
     const int r = r0 + wave;                                   // this wave's query row
     const bool row_ok = r < a.rows;                            // wave-uniform
-    const int d = a.d, du4 = d >> 3, dp = d >> 1, dq = d >> 2;
+    constexpr int d = D, du4 = d >> 3, dp = d >> 1, dq = d >> 2;
     const int hd = a.nh * d;
     const int last_row = (r0 + kPRows < a.rows ? r0 + kPRows : a.rows) - 1;
     const int64_t wg_last = a.pos0 + last_row;                 // the last position a row of the workgroup sees
@@ -111,6 +112,7 @@ __global__ __launch_bounds__(64 * kPRows) void prompt_attn_kernel(PromptAttnArgs
         float acc[G];
 #pragma unroll
         for (int g = 0; g < G; g++) acc[g] = 0.0f;
+#pragma unroll
         for (int c = 0; c < du4; c++) {
             const uint4 kk = k_s[j][c];
             const float kf[8] = {p_h2f(kk.x), p_h2f(kk.x >> 16), p_h2f(kk.y), p_h2f(kk.y >> 16),
@@ -148,8 +150,9 @@ __global__ __launch_bounds__(64 * kPRows) void prompt_attn_kernel(PromptAttnArgs
         if (lane < dp) {
             const uint32_t* vw = reinterpret_cast<const uint32_t*>(&v_s[0][0]);
             constexpr int kRowW = kPRowU4 * 4;
-            const int span = my_last - c0 + 1 < kPTile ? static_cast<int>(my_last - c0 + 1) : kPTile;
-            for (int j0 = 0; j0 < span; j0 += 4) {
+            // every position of the tile: p is 0 past the row's last one
+#pragma unroll 4
+            for (int j0 = 0; j0 < kPTile; j0 += 4) {
                 uint32_t w2[4];
 #pragma unroll
                 for (int jj = 0; jj < 4; jj++) w2[jj] = vw[(j0 + jj) * kRowW + lane];
@@ -214,7 +217,9 @@ int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint1
     switch (n_heads / n_kv) {
 #define Q4_PROMPT_CASE(g)                                                                       \
     case g:                                                                                     \
-        hipLaunchKernelGGL(prompt_attn_kernel<g>, grid, dim3(64 * kPRows), 0, st, a);           \
+        if (head_dim == 128) hipLaunchKernelGGL((prompt_attn_kernel<g, 128>), grid, dim3(64 * kPRows), 0, st, a); \
+        else if (head_dim == 64) hipLaunchKernelGGL((prompt_attn_kernel<g, 64>), grid, dim3(64 * kPRows), 0, st, a); \
+        else hipLaunchKernelGGL((prompt_attn_kernel<g, 32>), grid, dim3(64 * kPRows), 0, st, a); \
         break;
         Q4_PROMPT_CASE(1) Q4_PROMPT_CASE(2) Q4_PROMPT_CASE(3) Q4_PROMPT_CASE(4)
         Q4_PROMPT_CASE(5) Q4_PROMPT_CASE(6) Q4_PROMPT_CASE(7) Q4_PROMPT_CASE(8)
