@@ -77,6 +77,15 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __fadd_rn(__fadd_rn(__fadd_rn(r0, r1), r2), r3);
 }
 
+// a in the low half, b in the high half, each rounded to bf16 to nearest
+// even: one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+    const f32x2 p = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(p, bf16x2v));
+}
+
 // SiLU(g) * u as hetero/cpu_model.py:169-170 and :291-292 compute it in
 // fp32: g / (1 + exp(-g)) * u (expf here; NumPy's float32 exp may differ in
 // the last place).
@@ -263,6 +272,11 @@ struct GemmMats {
 // matrix's columns.
 int gemm_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K, int bm, int S, int kt_split, int ldp,
             hipStream_t st);
+
+// Paired gate/up form (q4_gemm.hip): matrices 0 and 1 of gm, both n_out[0]
+// rows, every K step in one workgroup, h[M][n_out[0]] = bf16(SiLU(x Wg^T) *
+// (x Wu^T)).
+int gemm_w4_pair(const uint16_t* xb, const GemmMats& gm, uint16_t* h, int M, int K, hipStream_t st);
 
 // Stream-K form of the prefill GEMM: P workgroups in nx XCD groups (256 x
 // 256 tiles; P a multiple of nx, and P / nx at least a group's tile count,

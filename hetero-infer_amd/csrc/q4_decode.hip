@@ -53,40 +53,94 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* __restrict__
 // [rows][n]); n <= 8 * 1024.  Thread t owns the 8 consecutive values of
 // word t; the squares are summed in NumPy's order (row_sum_numpy), and the
 // streaming GEMV's norm prologue sums them the same way, so its input is y
-// bit for bit.
+// bit for bit.  VEC (n a multiple of 8, 16-byte aligned rows): the words
+// move as two 16-byte accesses.  BF: y is stored rounded to bf16 (nearest
+// even), the operand the prefill GEMM reads.
 constexpr int kNormPer = 8;
+template <bool VEC, bool BF>
 __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(float* __restrict__ x, const float* __restrict__ delta,
                                                           const float* __restrict__ w, float eps,
-                                                          float* __restrict__ y, int n) {
+                                                          void* __restrict__ y_out, int n) {
     __shared__ float red[16];
     __shared__ __attribute__((aligned(16))) float sq_s[kNormPer * 1024];
-    const int tid = threadIdx.x, nt = blockDim.x;
+    const int tid = threadIdx.x;
     const int i0 = tid * kNormPer;
     const size_t row = static_cast<size_t>(blockIdx.x) * n;
     x += row;
-    y += row;
     if (delta) delta += row;
-    float v[kNormPer], sq[kNormPer];
-#pragma unroll
-    for (int k = 0; k < kNormPer; k++) {
-        const int i = i0 + k;
-        v[k] = sq[k] = 0.0f;
-        if (i < n) {
-            float a = x[i];
+    float v[kNormPer], sq[kNormPer], wv[kNormPer];
+    if constexpr (VEC) {
+        const bool in = i0 < n;
+        float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0, w0 = a0, w1 = a0;
+        if (in) {
+            a0 = reinterpret_cast<const float4*>(x + i0)[0];
+            a1 = reinterpret_cast<const float4*>(x + i0)[1];
+            w0 = reinterpret_cast<const float4*>(w + i0)[0];
+            w1 = reinterpret_cast<const float4*>(w + i0)[1];
             if (delta) {
-                a = __fadd_rn(a, delta[i]);
-                x[i] = a;
+                const float4 d0 = reinterpret_cast<const float4*>(delta + i0)[0];
+                const float4 d1 = reinterpret_cast<const float4*>(delta + i0)[1];
+                a0 = make_float4(__fadd_rn(a0.x, d0.x), __fadd_rn(a0.y, d0.y), __fadd_rn(a0.z, d0.z),
+                                 __fadd_rn(a0.w, d0.w));
+                a1 = make_float4(__fadd_rn(a1.x, d1.x), __fadd_rn(a1.y, d1.y), __fadd_rn(a1.z, d1.z),
+                                 __fadd_rn(a1.w, d1.w));
+                reinterpret_cast<float4*>(x + i0)[0] = a0;
+                reinterpret_cast<float4*>(x + i0)[1] = a1;
             }
-            v[k] = a;
-            sq[k] = __fmul_rn(a, a);
+        }
+        const float va[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+        const float wa[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int k = 0; k < kNormPer; k++) {
+            v[k] = va[k];
+            wv[k] = wa[k];
+            sq[k] = __fmul_rn(va[k], va[k]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kNormPer; k++) {
+            const int i = i0 + k;
+            v[k] = sq[k] = wv[k] = 0.0f;
+            if (i < n) {
+                float a = x[i];
+                if (delta) {
+                    a = __fadd_rn(a, delta[i]);
+                    x[i] = a;
+                }
+                v[k] = a;
+                wv[k] = w[i];
+                sq[k] = __fmul_rn(a, a);
+            }
         }
     }
-    (void)nt;
     const float r = rms_factor(row_sum_numpy(sq, n, sq_s, red), n, eps);
+    float o[kNormPer];
 #pragma unroll
-    for (int k = 0; k < kNormPer; k++) {
-        const int i = i0 + k;
-        if (i < n) y[i] = __fmul_rn(__fmul_rn(v[k], r), w[i]);
+    for (int k = 0; k < kNormPer; k++) o[k] = __fmul_rn(__fmul_rn(v[k], r), wv[k]);
+    if constexpr (BF) {
+        uint16_t* y = static_cast<uint16_t*>(y_out) + row;
+        if constexpr (VEC) {
+            if (i0 < n)
+                *reinterpret_cast<uint4*>(y + i0) =
+                    make_uint4(bf16x2_rne(o[0], o[1]), bf16x2_rne(o[2], o[3]), bf16x2_rne(o[4], o[5]),
+                               bf16x2_rne(o[6], o[7]));
+        } else {
+#pragma unroll
+            for (int k = 0; k < kNormPer; k++)
+                if (i0 + k < n) y[i0 + k] = static_cast<uint16_t>(bf16x2_rne(o[k], o[k]) & 0xFFFFu);
+        }
+    } else {
+        float* y = static_cast<float*>(y_out) + row;
+        if constexpr (VEC) {
+            if (i0 < n) {
+                reinterpret_cast<float4*>(y + i0)[0] = make_float4(o[0], o[1], o[2], o[3]);
+                reinterpret_cast<float4*>(y + i0)[1] = make_float4(o[4], o[5], o[6], o[7]);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kNormPer; k++)
+                if (i0 + k < n) y[i0 + k] = o[k];
+        }
     }
 }
 
@@ -289,6 +343,24 @@ int check_launch(const char* what) {
     return 0;
 }
 
+// add_rmsnorm_kernel over `rows` rows, 16-byte accesses where n and every
+// pointer allow them.
+int launch_add_rmsnorm(float* x, const float* delta, const float* w, float eps, void* y, bool bf, int rows, int n,
+                       void* stream, const char* what) {
+    const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool vec = n % 8 == 0 && al(x) && al(w) && al(y) && (!delta || al(delta));
+    const dim3 grid(rows), block(norm_threads(n));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (vec) {
+        if (bf) hipLaunchKernelGGL((add_rmsnorm_kernel<true, true>), grid, block, 0, st, x, delta, w, eps, y, n);
+        else hipLaunchKernelGGL((add_rmsnorm_kernel<true, false>), grid, block, 0, st, x, delta, w, eps, y, n);
+    } else {
+        if (bf) hipLaunchKernelGGL((add_rmsnorm_kernel<false, true>), grid, block, 0, st, x, delta, w, eps, y, n);
+        else hipLaunchKernelGGL((add_rmsnorm_kernel<false, false>), grid, block, 0, st, x, delta, w, eps, y, n);
+    }
+    return check_launch(what);
+}
+
 }  // namespace
 }  // namespace q4k
 
@@ -327,9 +399,7 @@ int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, 
     if (!x || !w || !y) return fail(Q4_EARG, "q4_add_rmsnorm_dev: null pointer");
     if (n <= 0 || n > kNormPer * 1024) return fail(Q4_EARG, "q4_add_rmsnorm_dev: n = %d outside [1, %d]", n,
                                                    kNormPer * 1024);
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(norm_threads(n)), 0, static_cast<hipStream_t>(stream), x,
-                       delta, w, eps, y, n);
-    return check_launch("q4_add_rmsnorm_dev");
+    return launch_add_rmsnorm(x, delta, w, eps, y, false, 1, n, stream, "q4_add_rmsnorm_dev");
 }
 
 int q4_add_rmsnorm_rows_dev(float* x, const float* delta, const float* w, float eps, float* y, int rows, int n,
@@ -338,9 +408,17 @@ int q4_add_rmsnorm_rows_dev(float* x, const float* delta, const float* w, float 
     if (rows < 0 || n <= 0 || n > kNormPer * 1024)
         return fail(Q4_EARG, "q4_add_rmsnorm_rows_dev: rows = %d, n = %d (n in [1, %d])", rows, n, kNormPer * 1024);
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(norm_threads(n)), 0, static_cast<hipStream_t>(stream),
-                       x, delta, w, eps, y, n);
-    return check_launch("q4_add_rmsnorm_rows_dev");
+    return launch_add_rmsnorm(x, delta, w, eps, y, false, rows, n, stream, "q4_add_rmsnorm_rows_dev");
+}
+
+int q4_add_rmsnorm_rows_bf16_dev(float* x, const float* delta, const float* w, float eps, uint16_t* y, int rows,
+                                 int n, void* stream) {
+    if (!x || !w || !y) return fail(Q4_EARG, "q4_add_rmsnorm_rows_bf16_dev: null pointer");
+    if (rows < 0 || n <= 0 || n > kNormPer * 1024)
+        return fail(Q4_EARG, "q4_add_rmsnorm_rows_bf16_dev: rows = %d, n = %d (n in [1, %d])", rows, n,
+                    kNormPer * 1024);
+    if (rows == 0) return 0;
+    return launch_add_rmsnorm(x, delta, w, eps, y, true, rows, n, stream, "q4_add_rmsnorm_rows_bf16_dev");
 }
 
 int q4_rope_kv_dev(const float* q, const float* k, const float* v, const float* bias, const float* cos_t,

@@ -24,6 +24,11 @@
 // rows past M or N and steps past the workgroup's K range read 0 and cost
 // no access.  Split-K: blockIdx.z takes steps [z kt_split, (z+1) kt_split)
 // and writes its partial sums to out + z M ldo.
+// Paired tiles (gate/up of the MLP): the tile's 256 weight rows are rows
+// [n0, n0 + 128) of the gate matrix, then the same rows of the up matrix,
+// and wave w's 64 columns are gate rows n0 + 32 w .. and the same up rows,
+// so one lane holds gate and up of every output it writes: the epilogue
+// stores bf16(SiLU(gate) * up), the down projection's bf16 operand.
 #include "q4_common.h"
 
 namespace q4k {
@@ -57,20 +62,31 @@ __device__ __forceinline__ gemm_bf16x8 w4_dequant8(uint32_t w, float s, float b)
     return __builtin_bit_cast(gemm_bf16x8, p);
 }
 
+// The operands of one tile (M block mt, N block nt): buffer resources over
+// its rows of x, W, scales and biases.
+struct W4Tile {
+    __amdgpu_buffer_rsrc_t xr, wr, sr, br;
+    __amdgpu_buffer_rsrc_t wr2, sr2, br2;    // paired tiles: the up matrix's rows
+    int m0, n0;
+};
+
 // The copies of one K step (kt) into a stage of the LDS ring (a plain device
 // function: the copy builtin in a lambda of the kernel keeps the compiler
 // from emitting the kernel's host stub).  NW waves share them: A in 1 KiB
 // copies of 8 rows, B in 8 copies of 32 rows, the 256 scales and biases in
 // 4 copies of 64 rows each.  `live` false (a step past the workgroup's K
 // range) reads zeros without an access.
-template <int BM, int NW>
-__device__ __forceinline__ void w4_issue(char* st, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr,
-                                         __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t br,
-                                         const uint32_t* a_src, const uint32_t* b_src,
+template <int BM, int NW, bool PAIR>
+__device__ __forceinline__ void w4_issue(char* st, const W4Tile& t, const uint32_t* a_src, const uint32_t* b_src,
                                          uint32_t g_src, int kt, bool live, int wave) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
     constexpr int A_DMA = BM / (8 * NW), B_DMA = 8 / NW;
+    static_assert(!PAIR || NW == 4, "paired tiles: waves 0-1 copy the gate rows, 2-3 the up rows");
     const uint32_t dead = __builtin_amdgcn_readfirstlane(live ? 0u : kOutOfRange);
+    const __amdgpu_buffer_rsrc_t xr = t.xr;
+    const __amdgpu_buffer_rsrc_t wr = PAIR && wave >= 2 ? t.wr2 : t.wr;     // wave-uniform choice
+    const __amdgpu_buffer_rsrc_t sr = PAIR && wave >= 2 ? t.sr2 : t.sr;
+    const __amdgpu_buffer_rsrc_t br = PAIR && wave >= 2 ? t.br2 : t.br;
 #pragma unroll
     for (int i = 0; i < A_DMA; i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_ptr)(st + (wave * A_DMA + i) * 1024), 16,
@@ -92,13 +108,6 @@ __device__ __forceinline__ void w4_issue(char* st, __amdgpu_buffer_rsrc_t xr, __
     }
 }
 
-// The operands of one tile (M block mt, N block nt): buffer resources over
-// its rows of x, W, scales and biases.
-struct W4Tile {
-    __amdgpu_buffer_rsrc_t xr, wr, sr, br;
-    int m0, n0;
-};
-
 template <int BM>
 __device__ __forceinline__ W4Tile w4_tile(const uint16_t* xb, const uint32_t* w, const uint16_t* sc, const uint16_t* bi,
                                           int M, int N, int K, int mt, int nt) {
@@ -112,6 +121,31 @@ __device__ __forceinline__ W4Tile w4_tile(const uint16_t* xb, const uint32_t* w,
     t.wr = buf_rsrc(w + static_cast<size_t>(t.n0) * wpr, static_cast<uint32_t>(nrows * wpr) * 4u);
     t.sr = buf_rsrc(sc + static_cast<size_t>(t.n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
     t.br = buf_rsrc(bi + static_cast<size_t>(t.n0) * G, static_cast<uint32_t>(nrows * G) * 2u);
+    t.wr2 = t.wr;
+    t.sr2 = t.sr;
+    t.br2 = t.br;
+    return t;
+}
+
+// A paired tile: output columns [nt 128, nt 128 + 128) of N, weight rows of
+// matrix 0 (gate) and matrix 1 (up) of gm.
+template <int BM>
+__device__ __forceinline__ W4Tile w4_tile_pair(const uint16_t* xb, const GemmMats& gm, int M, int N, int K, int mt,
+                                               int nt) {
+    W4Tile t;
+    t.m0 = mt * BM;
+    t.n0 = nt * 128;
+    const int G = K >> 6, wpr = K >> 3;
+    const int mrows = M - t.m0 < BM ? M - t.m0 : BM, nrows = N - t.n0 < 128 ? N - t.n0 : 128;
+    const size_t wo = static_cast<size_t>(t.n0) * wpr, go = static_cast<size_t>(t.n0) * G;
+    const uint32_t wb = static_cast<uint32_t>(nrows * wpr) * 4u, gb = static_cast<uint32_t>(nrows * G) * 2u;
+    t.xr = buf_rsrc(xb + static_cast<size_t>(t.m0) * K, static_cast<uint32_t>(mrows * K) * 2u);
+    t.wr = buf_rsrc(gm.w[0] + wo, wb);
+    t.sr = buf_rsrc(gm.s[0] + go, gb);
+    t.br = buf_rsrc(gm.b[0] + go, gb);
+    t.wr2 = buf_rsrc(gm.w[1] + wo, wb);
+    t.sr2 = buf_rsrc(gm.s[1] + go, gb);
+    t.br2 = buf_rsrc(gm.b[1] + go, gb);
     return t;
 }
 
@@ -128,7 +162,7 @@ struct W4Src {
     uint32_t g;
 };
 
-template <int BM, int NW>
+template <int BM, int NW, bool PAIR>
 __device__ __forceinline__ void w4_src(W4Src<BM, NW>& src, int K, int wave, int lane) {
     constexpr int A_DMA = BM / (8 * NW), B_DMA = 8 / NW;
     const int G = K >> 6, wpr = K >> 3;
@@ -139,10 +173,10 @@ __device__ __forceinline__ void w4_src(W4Src<BM, NW>& src, int K, int wave, int 
     }
 #pragma unroll
     for (int q = 0; q < B_DMA; q++) {
-        const int r = (B_DMA * wave + q) * 32 + (lane >> 1);
+        const int r = ((B_DMA * wave + q) * 32 + (lane >> 1)) & (PAIR ? 127 : 255);   // row of its matrix
         src.b[q] = static_cast<uint32_t>(r * wpr + (lane & 1) * 4) * 4u;
     }
-    src.g = static_cast<uint32_t>(((NW == 4 ? wave : wave & 3) * 64 + lane) * G) * 2u;
+    src.g = static_cast<uint32_t>(((PAIR ? wave & 1 : NW == 4 ? wave : wave & 3) * 64 + lane) * G) * 2u;
 }
 
 // How NW waves split a BM x 256 tile: WM x WN waves of RW rows x WC
@@ -160,11 +194,19 @@ struct W4Layout {
 template <int BM, int NW>
 using W4Acc = gemm_f32x16[W4Layout<BM, NW>::TM][W4Layout<BM, NW>::TN];
 
+// The stage row (of 256) of weight column block j of wave column wn: WC
+// consecutive rows per wave; paired tiles: gate rows wn 32 .. (j = 0) and
+// the same up rows, 128 further (j = 1).
+template <bool PAIR, int WC>
+__device__ __forceinline__ int w4_brow(int wn, int j, int lane) {
+    return PAIR ? j * 128 + wn * 32 + (lane & 31) : wn * WC + j * 32 + (lane & 31);
+}
+
 // K steps [k0, k0 + nk) of one tile into acc (which it adds to): the copy
 // pipeline starts and drains inside, and on return every wave is past its
 // last LDS read and no copy is in flight, so the next segment may reuse the
 // ring.
-template <int BM, int NW>
+template <int BM, int NW, bool PAIR = false>
 __device__ __forceinline__ void w4_segment(W4Acc<BM, NW>& acc, char* lds, const W4Tile& t, const W4Src<BM, NW>& src,
                                            int k0, int nk, int wave, int lane) {
     using L = W4Layout<BM, NW>;
@@ -174,8 +216,8 @@ __device__ __forceinline__ void w4_segment(W4Acc<BM, NW>& acc, char* lds, const 
     constexpr int STAGE = w4_stage_bytes(BM);
     const int hb = lane >> 5;
     const int wm = wave / WN, wn = wave % WN;
-    w4_issue<BM, NW>(lds, t.xr, t.wr, t.sr, t.br, src.a, src.b, src.g, k0, 0 < nk, wave);
-    w4_issue<BM, NW>(lds + STAGE, t.xr, t.wr, t.sr, t.br, src.a, src.b, src.g, k0 + 1, 1 < nk, wave);
+    w4_issue<BM, NW, PAIR>(lds, t, src.a, src.b, src.g, k0, 0 < nk, wave);
+    w4_issue<BM, NW, PAIR>(lds + STAGE, t, src.a, src.b, src.g, k0 + 1, 1 < nk, wave);
     for (int it = 0; it < nk; it++) {
         // step it's copies are done (only step it + 1's may be in flight)
         __builtin_amdgcn_s_waitcnt(0x0F70 | PER_STEP);
@@ -183,8 +225,7 @@ __device__ __forceinline__ void w4_segment(W4Acc<BM, NW>& acc, char* lds, const 
         // wave is past step it - 1, whose stage step it + 2 refills (a fence
         // would also wait for the copies of step it + 1)
         __builtin_amdgcn_s_barrier();
-        w4_issue<BM, NW>(lds + ((it + 2) % 3) * STAGE, t.xr, t.wr, t.sr, t.br, src.a, src.b, src.g, k0 + it + 2,
-                         it + 2 < nk, wave);
+        w4_issue<BM, NW, PAIR>(lds + ((it + 2) % 3) * STAGE, t, src.a, src.b, src.g, k0 + it + 2, it + 2 < nk, wave);
         const char* st = lds + (it % 3) * STAGE;
         const uint16_t* As = reinterpret_cast<const uint16_t*>(st);
         const uint32_t* Bs = reinterpret_cast<const uint32_t*>(st + BM * 128);
@@ -193,7 +234,7 @@ __device__ __forceinline__ void w4_segment(W4Acc<BM, NW>& acc, char* lds, const 
         float sf[TN], bf[TN];
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int row = wn * WC + j * 32 + (lane & 31);
+            const int row = w4_brow<PAIR, WC>(wn, j, lane);
             sf[j] = h2f(static_cast<uint16_t>(Ss[row]));
             bf[j] = h2f(static_cast<uint16_t>(Ts[row]));
         }
@@ -202,7 +243,7 @@ __device__ __forceinline__ void w4_segment(W4Acc<BM, NW>& acc, char* lds, const 
             gemm_bf16x8 av[TM], bv[TN];
 #pragma unroll
             for (int j = 0; j < TN; j++) {
-                const int row = wn * WC + j * 32 + (lane & 31);
+                const int row = w4_brow<PAIR, WC>(wn, j, lane);
                 bv[j] = w4_dequant8(Bs[row * 8 + 2 * ks + hb], sf[j], bf[j]);
             }
 #pragma unroll
@@ -305,7 +346,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
     const int N = gm.n_out[k];
     const W4Tile t = w4_tile<BM>(xb, gm.w[k], gm.s[k], gm.b[k], M, N, K, blockIdx.x, blockIdx.y - gm.nb0[k]);
     W4Src<BM, NW> src;
-    w4_src<BM, NW>(src, K, wave, lane);
+    w4_src<BM, NW, false>(src, K, wave, lane);
     W4Acc<BM, NW> acc;
     w4_zero<BM, NW>(acc);
     w4_segment<BM, NW>(acc, lds, t, src, kt0, nk, wave, lane);
@@ -314,6 +355,41 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_kernel(const uint16_t* __rest
                          lane);
     else
         w4_store<BM, NW>(acc, gm.out[k], t, M, N, N, 0, wave, lane);
+}
+
+// Paired gate/up tiles (blockIdx.y = block of 128 output columns), every K
+// step: h[r][c] = bf16(SiLU(x W_gate^T) * (x W_up^T)), rounded to nearest
+// even -- the fp32 products of two gemm_w4_kernel calls through silu_mul,
+// then the bf16 rounding the down projection applies to its x.
+template <int BM, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_w4_pair_kernel(const uint16_t* __restrict__ xb, GemmMats gm,
+                                                               uint16_t* __restrict__ h, int M, int K) {
+    static_assert(BM == 256 && NW == 4, "paired tiles: 4 waves of 256 x (32 gate + 32 up) columns");
+    using L = W4Layout<BM, NW>;
+    constexpr int TM = L::TM;
+    extern __shared__ uint4 w4_lds[];
+    char* lds = reinterpret_cast<char*>(w4_lds);
+    const int lane = threadIdx.x & 63, hb = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int N = gm.n_out[0];
+    const W4Tile t = w4_tile_pair<BM>(xb, gm, M, N, K, blockIdx.x, blockIdx.y);
+    W4Src<BM, NW> src;
+    w4_src<BM, NW, true>(src, K, wave, lane);
+    W4Acc<BM, NW> acc;
+    w4_zero<BM, NW>(acc);
+    w4_segment<BM, NW, true>(acc, lds, t, src, 0, K >> 6, wave, lane);
+    const int col = t.n0 + wave * 32 + (lane & 31);
+    if (col >= N) return;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int row = t.m0 + i * 32 + 8 * (v >> 2) + 4 * hb + (v & 3);
+            if (row < M) {
+                const float a = silu_mul(acc[i][0][v], acc[i][1][v]);
+                h[static_cast<size_t>(row) * N + col] = static_cast<uint16_t>(w4_pack_bf16(a, a) & 0xFFFFu);
+            }
+        }
 }
 
 // Stream-K: the tiles (m block major) are split into nx contiguous groups,
@@ -501,7 +577,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __r
     unsigned* errors = ctl + kSkCtlErrors;
     if (begin < end) {
         W4Src<BM, NW> src;
-        w4_src<BM, NW>(src, K, wave, lane);
+        w4_src<BM, NW, false>(src, K, wave, lane);
         const long cut = (begin / G + 1) * G;                     // end of the first tile
         if (end > cut) {
             w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, epoch, M, K, gp, cut, end, src, tid, wave, lane);
@@ -556,6 +632,17 @@ int launch_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* 
     hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, gm, part, flags, ctl, M, K, nx);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "prefill gemm (stream-K) launch: %s", hipGetErrorString(e));
+    return 0;
+}
+
+int gemm_w4_pair(const uint16_t* xb, const GemmMats& gm, uint16_t* h, int M, int K, hipStream_t st) {
+    auto kern = gemm_w4_pair_kernel<256, 4>;
+    const size_t lds = w4_lds_bytes<256, 4>();
+    static std::atomic<uint64_t> lds_raised{0};
+    if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
+    hipLaunchKernelGGL(kern, dim3((M + 255) / 256, (gm.n_out[0] + 127) / 128), dim3(256), lds, st, xb, gm, h, M, K);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(Q4_EHIP, "prefill gate/up gemm launch: %s", hipGetErrorString(e));
     return 0;
 }
 

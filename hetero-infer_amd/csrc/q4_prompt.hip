@@ -41,7 +41,7 @@ struct PromptAttnArgs {
     const float* q;          // [rows][nh * d], rotated queries
     const uint16_t* kc;      // [nkv][cap][d] fp16
     const uint16_t* vc;
-    float* out;              // [rows][nh * d]
+    void* out;               // [rows][nh * d], fp32 or (BF) bf16
     int rows;
     int64_t pos0;
     int nh, nkv, d, cap;
@@ -60,7 +60,7 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-template <int G, int D>
+template <int G, int D, bool BF>
 __global__ __launch_bounds__(64 * kPRows) void prompt_attn_kernel(PromptAttnArgs a) {
     __shared__ uint4 k_s[kPTile][kPRowU4];
     __shared__ uint4 v_s[kPTile][kPRowU4];
@@ -174,11 +174,17 @@ __global__ __launch_bounds__(64 * kPRows) void prompt_attn_kernel(PromptAttnArgs
         wave_lds_sync();
     }
     if (row_ok && lane < dp) {
-        float* dst = a.out + static_cast<size_t>(r) * hd + static_cast<size_t>(kvh) * G * d + 2 * lane;
+        const size_t at = static_cast<size_t>(r) * hd + static_cast<size_t>(kvh) * G * d + 2 * lane;
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            dst[g * d] = __fdiv_rn(o0[g], l[g]);
-            dst[g * d + 1] = __fdiv_rn(o1[g], l[g]);
+            const float v0 = __fdiv_rn(o0[g], l[g]), v1 = __fdiv_rn(o1[g], l[g]);
+            if constexpr (BF) {
+                *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.out) + at + g * d) = bf16x2_rne(v0, v1);
+            } else {
+                float* dst = static_cast<float*>(a.out) + at + g * d;
+                dst[0] = v0;
+                dst[1] = v1;
+            }
         }
     }
 }
@@ -194,11 +200,10 @@ int launch_failed(const char* what) {
 
 using namespace q4k;
 
-#pragma GCC visibility push(default)
-extern "C" {
+namespace {
 
-int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int rows,
-                            int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream) {
+int prompt_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, void* out, bool bf, int rows,
+                     int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream) {
     if (!q || !k_cache || !v_cache || !out) return fail(Q4_EARG, "q4_prompt_attention_dev: null pointer");
     if (n_heads <= 0 || n_kv <= 0 || n_heads % n_kv || n_heads / n_kv > kPMaxG ||
         (head_dim != 32 && head_dim != 64 && head_dim != 128) || cap <= 0)
@@ -215,18 +220,38 @@ int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint1
     const dim3 grid((rows + kPRows - 1) / kPRows, n_kv);
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch (n_heads / n_kv) {
-#define Q4_PROMPT_CASE(g)                                                                       \
-    case g:                                                                                     \
-        if (head_dim == 128) hipLaunchKernelGGL((prompt_attn_kernel<g, 128>), grid, dim3(64 * kPRows), 0, st, a); \
-        else if (head_dim == 64) hipLaunchKernelGGL((prompt_attn_kernel<g, 64>), grid, dim3(64 * kPRows), 0, st, a); \
-        else hipLaunchKernelGGL((prompt_attn_kernel<g, 32>), grid, dim3(64 * kPRows), 0, st, a); \
+#define Q4_PROMPT_D(g, dd)                                                                                  \
+    if (bf) hipLaunchKernelGGL((prompt_attn_kernel<g, dd, true>), grid, dim3(64 * kPRows), 0, st, a);          \
+    else hipLaunchKernelGGL((prompt_attn_kernel<g, dd, false>), grid, dim3(64 * kPRows), 0, st, a);
+#define Q4_PROMPT_CASE(g)                                                                                   \
+    case g:                                                                                                 \
+        if (head_dim == 128) { Q4_PROMPT_D(g, 128) }                                                         \
+        else if (head_dim == 64) { Q4_PROMPT_D(g, 64) }                                                      \
+        else { Q4_PROMPT_D(g, 32) }                                                                          \
         break;
         Q4_PROMPT_CASE(1) Q4_PROMPT_CASE(2) Q4_PROMPT_CASE(3) Q4_PROMPT_CASE(4)
         Q4_PROMPT_CASE(5) Q4_PROMPT_CASE(6) Q4_PROMPT_CASE(7) Q4_PROMPT_CASE(8)
 #undef Q4_PROMPT_CASE
+#undef Q4_PROMPT_D
         default: break;
     }
     return launch_failed("q4_prompt_attention_dev");
+}
+
+}  // namespace
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int rows,
+                            int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream) {
+    return prompt_attention(q, k_cache, v_cache, out, false, rows, pos0, n_heads, n_kv, head_dim, cap, scale, stream);
+}
+
+int q4_prompt_attention_bf16_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                                 int rows, int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale,
+                                 void* stream) {
+    return prompt_attention(q, k_cache, v_cache, out, true, rows, pos0, n_heads, n_kv, head_dim, cap, scale, stream);
 }
 
 }  // extern "C"

@@ -360,6 +360,11 @@ __global__ void silu_mul_kernel(const float* __restrict__ g, const float* __rest
     if (i < n) h[i] = silu_mul(g[i], u[i]);
 }
 
+__global__ void fill_zero_u16_kernel(uint16_t* __restrict__ p, long n) {
+    const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
 __global__ void fill_zero_kernel(float* __restrict__ p, long n) {
     const long i = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.0f;
@@ -1626,9 +1631,15 @@ int q4_mlp_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* g
 }
 
 
-int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* const* scales,
-                           const uint16_t* const* biases, float* const* out, const int* n_out, const float* x,
-                           int m, int n_in, int gs, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// q4_gemm_bf16_multi_dev on x given in fp32 (x, rounded to bf16 into the
+// workspace first) or already in bf16 (xb).
+int gemm_bf16_multi(int count, const uint32_t* const* w, const uint16_t* const* scales,
+                    const uint16_t* const* biases, float* const* out, const int* n_out, const float* x,
+                    const uint16_t* xb_in, int m, int n_in, int gs, void* stream) {
     if (count < 1 || count > 4) return fail(Q4_EARG, "count=%d (1..4)", count);
     if (!w || !scales || !biases || !out || !n_out) return fail(Q4_EARG, "null array");
     int rc;
@@ -1657,7 +1668,8 @@ int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
         if (!gm.w[k] || !gm.s[k] || !gm.b[k] || !gm.out[k]) return fail(Q4_EARG, "null pointer");
         if (reinterpret_cast<uintptr_t>(gm.w[k]) & 15) return fail(Q4_EARG, "w and x must be 16-byte aligned");
     }
-    if (!x || (reinterpret_cast<uintptr_t>(x) & 15)) return fail(Q4_EARG, "w and x must be 16-byte aligned");
+    const void* xin = xb_in ? static_cast<const void*>(xb_in) : static_cast<const void*>(x);
+    if (!xin || (reinterpret_cast<uintptr_t>(xin) & 15)) return fail(Q4_EARG, "w and x must be 16-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (n_in == 0) {
         for (int k = 0; k < gm.count; k++) {
@@ -1677,7 +1689,7 @@ int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
     PrefillPlan plan;
     if ((rc = plan_prefill(m, nblocks, ncols, n_in, &plan))) return rc;
     const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * ncols;
-    if ((rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
+    if (!xb_in && (rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
     if (plan.sk_p > 0) {
         // the flags of up to one workgroup per CU (sk_ok: P <= CUs), then the control words
         const size_t flag_words = static_cast<size_t>(num_cus()) * 32 + kSkCtlWordsHost;
@@ -1696,11 +1708,14 @@ int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
     } else if (plan.S > 1 && (rc = grow(*ws, ws->part, kWsPart, plan.S * mn * 4, st, "prefill"))) {
         return rc;
     }
-    const long n8 = static_cast<long>(mk / 8);
-    hipLaunchKernelGGL(x_to_bf16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, st, x,
-                       static_cast<uint4*>(ws->xbf), n8);
-    HIP_TRY(hipGetLastError());
-    const uint16_t* xb = static_cast<const uint16_t*>(ws->xbf);
+    const uint16_t* xb = xb_in;
+    if (!xb) {
+        const long n8 = static_cast<long>(mk / 8);
+        hipLaunchKernelGGL(x_to_bf16_kernel, dim3(static_cast<unsigned>((n8 + 255) / 256)), dim3(256), 0, st, x,
+                           static_cast<uint4*>(ws->xbf), n8);
+        HIP_TRY(hipGetLastError());
+        xb = static_cast<const uint16_t*>(ws->xbf);
+    }
     if (plan.sk_p > 0) {
         return gemm_w4_sk(xb, gm, static_cast<float*>(ws->part), ws->sk, sk_ctl(*ws), m, n_in, plan.sk_p,
                           plan.sk_nx, st);
@@ -1714,6 +1729,55 @@ int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* 
                        static_cast<const float*>(ws->part), gm, m, ncols, S);
     HIP_TRY(hipGetLastError());
     return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int q4_gemm_bf16_multi_dev(int count, const uint32_t* const* w, const uint16_t* const* scales,
+                           const uint16_t* const* biases, float* const* out, const int* n_out, const float* x,
+                           int m, int n_in, int gs, void* stream) {
+    return gemm_bf16_multi(count, w, scales, biases, out, n_out, x, nullptr, m, n_in, gs, stream);
+}
+
+int q4_gemm_bf16in_multi_dev(int count, const uint32_t* const* w, const uint16_t* const* scales,
+                             const uint16_t* const* biases, float* const* out, const int* n_out, const uint16_t* xb,
+                             int m, int n_in, int gs, void* stream) {
+    return gemm_bf16_multi(count, w, scales, biases, out, n_out, nullptr, xb, m, n_in, gs, stream);
+}
+
+int q4_gemm_bf16in_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,
+                                    const uint32_t* up_w, const uint16_t* up_s, const uint16_t* up_b,
+                                    const uint16_t* xb, uint16_t* h, int m, int n_inter, int n_in, int gs,
+                                    void* stream) {
+    int rc = check_gemv_shape(n_inter, n_in, gs);
+    if (rc) return rc;
+    if (gs != 64) return fail(Q4_EARG, "the prefill GEMM takes gs = 64 (got %d)", gs);
+    if (m < 0) return fail(Q4_EARG, "m=%d", m);
+    if (!gate_w || !gate_s || !gate_b || !up_w || !up_s || !up_b || !xb || !h)
+        return fail(Q4_EARG, "q4_gemm_bf16in_gate_up_silu_dev: null pointer");
+    if ((reinterpret_cast<uintptr_t>(gate_w) & 15) || (reinterpret_cast<uintptr_t>(up_w) & 15) ||
+        (reinterpret_cast<uintptr_t>(xb) & 15))
+        return fail(Q4_EARG, "w and x must be 16-byte aligned");
+    if (m == 0 || n_inter == 0) return 0;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (n_in == 0) {                                   // SiLU(0) * 0
+        const long n = static_cast<long>(m) * n_inter;
+        hipLaunchKernelGGL(fill_zero_u16_kernel, dim3((n + 255) / 256), dim3(256), 0, st, h, n);
+        HIP_TRY(hipGetLastError());
+        return 0;
+    }
+    GemmMats gm{};
+    gm.w[0] = gate_w;
+    gm.s[0] = gate_s;
+    gm.b[0] = gate_b;
+    gm.w[1] = up_w;
+    gm.s[1] = up_s;
+    gm.b[1] = up_b;
+    gm.n_out[0] = gm.n_out[1] = n_inter;
+    gm.count = 2;
+    return gemm_w4_pair(xb, gm, h, m, n_in, st);
 }
 
 int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

@@ -385,29 +385,34 @@ class GpuStage:
         ew, es, eb = self.embed
         x = f32(rows, h)
         ck(lib.q4_embed_rows_dev(P(ew), P(es), P(eb), P(ids), rows, P(x), ew.shape[0], h, self.gs, st), "embed rows")
-        hn, attn, o = f32(rows, h), f32(rows, h), f32(rows, h)
+        # above 16 rows the projections are bf16 matrix-core GEMMs: the norms,
+        # the attention and the gate/up epilogue store their outputs in bf16
+        # (rounded as the GEMM would round them), and SiLU * up is the
+        # gate/up GEMM's epilogue
+        gemm = rows > 16
+        act = (lambda *shape: torch.empty(shape, dtype=torch.bfloat16, device=dev)) if gemm else f32
+        norm_rows = lib.q4_add_rmsnorm_rows_bf16_dev if gemm else lib.q4_add_rmsnorm_rows_dev
+        attention = lib.q4_prompt_attention_bf16_dev if gemm else lib.q4_prompt_attention_dev
+        hn, attn, o = act(rows, h), act(rows, h), f32(rows, h)
         kvd = self.nkv * self.hd
         q, k, v, qr = f32(rows, h), f32(rows, kvd), f32(rows, kvd), f32(rows, h)
-        hb, mlp = f32(rows, self.inter), f32(rows, h)
-        gu = (f32(rows, self.inter), f32(rows, self.inter)) if rows > 16 else None
+        hb, mlp = act(rows, self.inter), f32(rows, h)
         delta = None
         for L in self.layers:                                           # cpu_model.py:304-306
-            ck(lib.q4_add_rmsnorm_rows_dev(P(x), None if delta is None else P(delta), P(L["in_w"]), self.eps,
-                                           P(hn), rows, h, st), "input norm")
+            ck(norm_rows(P(x), None if delta is None else P(delta), P(L["in_w"]), self.eps, P(hn), rows, h, st),
+               "input norm")
             self._proj(L["qkv"], hn, [q, k, v])
             ck(lib.q4_rope_kv_rows_dev(P(q), P(k), P(v), P(L["qkv_bias"]), P(self.cos), P(self.sin), pos0, rows,
                                        P(L["k_cache"]), P(L["v_cache"]), P(qr), self.nh, self.nkv, self.hd,
                                        self.cap, st), "rope/kv rows")
-            ck(lib.q4_prompt_attention_dev(P(qr), P(L["k_cache"]), P(L["v_cache"]), P(attn), rows, pos0, self.nh,
-                                           self.nkv, self.hd, self.cap, self.scale, st), "prompt attention")
+            ck(attention(P(qr), P(L["k_cache"]), P(L["v_cache"]), P(attn), rows, pos0, self.nh, self.nkv, self.hd,
+                         self.cap, self.scale, st), "prompt attention")
             self._proj([L["o"]], attn, [o])
-            ck(lib.q4_add_rmsnorm_rows_dev(P(x), P(o), P(L["post_w"]), self.eps, P(hn), rows, h, st),
-               "post-attention norm")
-            if gu is None:
-                q4.gate_up_silu_dev(L["gate"], L["up"], hn, h=hb, lib=lib)
+            ck(norm_rows(P(x), P(o), P(L["post_w"]), self.eps, P(hn), rows, h, st), "post-attention norm")
+            if gemm:
+                q4.gemm_bf16_gate_up_silu_dev(L["gate"], L["up"], hn, h=hb, lib=lib)
             else:
-                self._proj([L["gate"], L["up"]], hn, list(gu))
-                ck(lib.q4_silu_mul_dev(P(gu[0]), P(gu[1]), P(hb), rows * self.inter, st), "silu * up")
+                q4.gate_up_silu_dev(L["gate"], L["up"], hn, h=hb, lib=lib)
             self._proj([L["down"]], hb, [mlp])
             delta = mlp
         if last:

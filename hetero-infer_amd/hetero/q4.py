@@ -21,7 +21,8 @@ LIB_PATH = os.path.join(PKG_PARENT, "kernel", "libq4gemv.so")
 
 EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release_all",
            "q4_last_error", "q4_gemv_dev", "q4_gemv_noalloc_dev", "q4_gemv_multi_dev", "q4_gate_up_silu_dev",
-           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_gemm_bf16_multi_dev", "q4_set_rows", "q4_prefill_errors",
+           "q4_mlp_dev", "q4_gemm_bf16_dev", "q4_gemm_bf16_multi_dev", "q4_gemm_bf16in_multi_dev",
+           "q4_gemm_bf16in_gate_up_silu_dev", "q4_set_rows", "q4_prefill_errors",
            "q4_dequant_dev",
            "q4_dequant_bf16_dev",
            # decode-step kernels (include/q4decode.h)
@@ -30,7 +31,7 @@ EXPORTS = ("q4_gemv", "q4_dequant", "q4_gemv_batched", "q4_release", "q4_release
            "q4_norm_gemv_multi_dev", "q4_norm_gate_up_silu_dev", "q4_norm_gemv_argmax_dev",
            # the prompt forward (include/q4decode.h)
            "q4_embed_rows_dev", "q4_add_rmsnorm_rows_dev", "q4_rope_kv_rows_dev", "q4_silu_mul_dev",
-           "q4_prompt_attention_dev",
+           "q4_prompt_attention_dev", "q4_add_rmsnorm_rows_bf16_dev", "q4_prompt_attention_bf16_dev",
            # activation wire codec (include/q4wire.h)
            "q4_wire_payload_bytes", "q4_wire_encode_dev", "q4_wire_decode_dev",
            # chained GEMV programs (include/q4chain.h)
@@ -70,6 +71,10 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_gemm_bf16_dev.restype = _I
         lib.q4_gemm_bf16_multi_dev.argtypes = [_I] + [_VP] * 6 + [_I] * 3 + [_VP]
         lib.q4_gemm_bf16_multi_dev.restype = _I
+        lib.q4_gemm_bf16in_multi_dev.argtypes = [_I] + [_VP] * 6 + [_I] * 3 + [_VP]
+        lib.q4_gemm_bf16in_multi_dev.restype = _I
+        lib.q4_gemm_bf16in_gate_up_silu_dev.argtypes = [_VP] * 8 + [_I] * 4 + [_VP]
+        lib.q4_gemm_bf16in_gate_up_silu_dev.restype = _I
         lib.q4_set_rows.argtypes = [_I]
         lib.q4_set_rows.restype = _I
         lib.q4_prefill_errors.argtypes = [_VP]
@@ -110,6 +115,10 @@ def declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         lib.q4_silu_mul_dev.restype = _I
         lib.q4_prompt_attention_dev.argtypes = [_VP] * 4 + [_I, ctypes.c_int64] + [_I] * 4 + [_F, _VP]
         lib.q4_prompt_attention_dev.restype = _I
+        lib.q4_add_rmsnorm_rows_bf16_dev.argtypes = [_VP] * 3 + [_F, _VP, _I, _I, _VP]
+        lib.q4_add_rmsnorm_rows_bf16_dev.restype = _I
+        lib.q4_prompt_attention_bf16_dev.argtypes = [_VP] * 4 + [_I, ctypes.c_int64] + [_I] * 4 + [_F, _VP]
+        lib.q4_prompt_attention_bf16_dev.restype = _I
     if hasattr(lib, "q4_wire_encode_dev"):
         lib.q4_wire_payload_bytes.argtypes = [_I] * 3
         lib.q4_wire_payload_bytes.restype = ctypes.c_longlong
@@ -326,7 +335,8 @@ def gemm_bf16_dev(w, scales, biases, x, out=None, stream=None, lib=None):
 
 
 def gemm_bf16_multi_dev(mats, x, outs=None, stream=None, lib=None):
-    """Prefill for several (w, scales, biases) sharing x in one launch; returns the outputs."""
+    """Prefill for several (w, scales, biases) sharing x in one launch; returns
+    the outputs.  x in fp32 (rounded to bf16 by the call) or already bf16."""
     import torch
     lib = lib or load()
     n_in = mats[0][0].shape[1] * 8
@@ -337,12 +347,31 @@ def gemm_bf16_multi_dev(mats, x, outs=None, stream=None, lib=None):
         outs = [torch.empty((m, w.shape[0]), dtype=torch.float32, device=x.device) for w, _, _ in mats]
     k = len(mats)
     arr = lambda vals: (ctypes.c_void_p * k)(*vals)
-    rc = lib.q4_gemm_bf16_multi_dev(k, arr([_ptr(a[0]) for a in mats]), arr([_ptr(a[1]) for a in mats]),
-                                    arr([_ptr(a[2]) for a in mats]), arr([_ptr(o) for o in outs]),
-                                    (ctypes.c_int * k)(*[a[0].shape[0] for a in mats]),
-                                    _ptr(x2), m, n_in, gs, _stream(stream))
-    check(lib, rc, "q4_gemm_bf16_multi_dev")
+    fn = lib.q4_gemm_bf16in_multi_dev if x2.dtype == torch.bfloat16 else lib.q4_gemm_bf16_multi_dev
+    rc = fn(k, arr([_ptr(a[0]) for a in mats]), arr([_ptr(a[1]) for a in mats]),
+            arr([_ptr(a[2]) for a in mats]), arr([_ptr(o) for o in outs]),
+            (ctypes.c_int * k)(*[a[0].shape[0] for a in mats]),
+            _ptr(x2), m, n_in, gs, _stream(stream))
+    check(lib, rc, fn.__name__)
     return outs
+
+
+def gemm_bf16_gate_up_silu_dev(gate, up, xb, h=None, stream=None, lib=None):
+    """Prefill MLP activations from bf16 x: h[m, n_inter] = bf16(SiLU(x @
+    gate^T) * (x @ up^T)), the down projection's bf16 operand."""
+    import torch
+    lib = lib or load()
+    n_inter, n_in = gate[0].shape[0], gate[0].shape[1] * 8
+    gs = n_in // gate[1].shape[1]
+    x2 = xb.reshape(-1, n_in)
+    if x2.dtype != torch.bfloat16:
+        raise TypeError("gemm_bf16_gate_up_silu_dev takes x in bf16")
+    if h is None:
+        h = torch.empty((x2.shape[0], n_inter), dtype=torch.bfloat16, device=xb.device)
+    rc = lib.q4_gemm_bf16in_gate_up_silu_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), _ptr(x2), _ptr(h),
+                                             x2.shape[0], n_inter, n_in, gs, _stream(stream))
+    check(lib, rc, "q4_gemm_bf16in_gate_up_silu_dev")
+    return h
 
 
 def set_rows(rows: int, lib=None) -> int:

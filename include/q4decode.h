@@ -49,6 +49,13 @@ int q4_add_rmsnorm_dev(float* x, const float* delta, const float* w, float eps, 
 int q4_add_rmsnorm_rows_dev(float* x, const float* delta, const float* w, float eps, float* y, int rows, int n,
                             void* stream);
 
+/* q4_add_rmsnorm_rows_dev with y stored as bf16 bit patterns, each value
+ * rounded to nearest even: the x operand the prefill GEMM would round it to
+ * (q4_gemm_bf16in_multi_dev, q4_gemm_bf16in_gate_up_silu_dev), written by
+ * the norm instead of a separate conversion.  x, delta and w as there. */
+int q4_add_rmsnorm_rows_bf16_dev(float* x, const float* delta, const float* w, float eps, uint16_t* y, int rows,
+                                 int n, void* stream);
+
 /* The GEMVs that follow a residual add + RMSNorm, with the norm folded into
  * their prologue (every workgroup normalises the input itself, so the
  * separate q4_add_rmsnorm_dev launch goes away):
@@ -111,6 +118,13 @@ int q4_silu_mul_dev(const float* g, const float* u, float* h, long n, void* stre
  * pos0 + rows <= cap; q, out and the caches 16-byte aligned. */
 int q4_prompt_attention_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out, int rows,
                             int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale, void* stream);
+
+/* q4_prompt_attention_dev with out stored as bf16 bit patterns (each value
+ * rounded to nearest even), the x operand of the o projection's prefill
+ * GEMM (q4_gemm_bf16in_multi_dev). */
+int q4_prompt_attention_bf16_dev(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                                 int rows, int64_t pos0, int n_heads, int n_kv, int head_dim, int cap, float scale,
+                                 void* stream);
 
 /* Floats of scratch memory q4_attention_dev needs for these sizes: the
  * chunks' partial results and, at the end, 512 arrival counters (one per

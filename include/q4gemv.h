@@ -170,6 +170,30 @@ int q4_gemm_bf16_multi_dev(int count, const uint32_t *const *w, const uint16_t *
                            const uint16_t *const *biases, float *const *out, const int *n_out,
                            const float *x, int m, int n_in, int gs, void *stream);
 
+/* q4_gemm_bf16_multi_dev with x given as bf16 bit patterns [m][n_in] (16-byte
+ * aligned): the call skips its own rounding of x, so for x = bf16(x32)
+ * (nearest even) the outputs are those of q4_gemm_bf16_multi_dev on x32, bit
+ * for bit.  For producers that write bf16 (q4_add_rmsnorm_rows_bf16_dev,
+ * q4_prompt_attention_bf16_dev, q4_gemm_bf16in_gate_up_silu_dev).  Same
+ * reference contraction: hetero/cpu_model.py:119-136. */
+int q4_gemm_bf16in_multi_dev(int count, const uint32_t *const *w, const uint16_t *const *scales,
+                             const uint16_t *const *biases, float *const *out, const int *n_out,
+                             const uint16_t *xb, int m, int n_in, int gs, void *stream);
+
+/* The prompt's MLP activations from bf16 x [m][n_in] (hetero/cpu_model.py:
+ * 149-153 and :169-170 with both projections as QLinear._gemm, :119-136):
+ * h[m][n_inter] = bf16(SiLU(x . Wg^T) * (x . Wu^T)) as bf16 bit patterns,
+ * rounded to nearest even -- the down projection's operand.  One launch:
+ * each tile holds the same 128 rows of both matrices, so the SiLU * mul is
+ * the GEMM's epilogue; the fp32 sums are those of q4_gemm_bf16in_multi_dev
+ * on {gate, up} when it runs without split-K (as it does when the two
+ * matrices give at least one tile per CU).  gs must be 64; w and x 16-byte
+ * aligned.  No workspace. */
+int q4_gemm_bf16in_gate_up_silu_dev(const uint32_t *gate_w, const uint16_t *gate_s, const uint16_t *gate_b,
+                                    const uint32_t *up_w, const uint16_t *up_s, const uint16_t *up_b,
+                                    const uint16_t *xb, uint16_t *h, int m, int n_inter, int n_in, int gs,
+                                    void *stream);
+
 /* Set the reference ROWS whose tail rows the plain GEMV entry points
  * reproduce (1..64; 1 = every row by the integer path).  Returns the
  * previous setting, or Q4_EARG.  No counterpart in the reference's ABI: the
