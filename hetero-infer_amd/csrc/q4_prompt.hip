@@ -189,6 +189,236 @@ __global__ __launch_bounds__(64 * kPRows) void prompt_attn_kernel(PromptAttnArgs
     }
 }
 
+// ---------------------------------------------------------------------
+// head_dim 128 on the matrix cores (v_mfma_f32_16x16x32_f16).  A workgroup
+// takes one kv head and 16 consecutive query rows, a wave per query head of
+// the kv head (G waves), and walks the cache in tiles of 64 positions; the
+// tile's K rows (k_s, row-major) and V rows (vt_s, transposed: [dim][pos])
+// are staged in LDS once for the G heads, the next tile's loads in flight
+// while the current one is multiplied.
+//
+// Per tile and wave, with lane l: c = l % 16 (a query row of the block),
+// qd = l / 16:
+//   S^T = K Q^T: 4 x 4 MFMAs; lane l ends with query row c's scores at
+//     positions 16 mt + 4 qd + v (mt, v = 0..3);
+//   the running softmax of row c (its 64 scores sit in lanes c, c + 16,
+//     c + 32, c + 48: a max and a sum over the lane's 16, then across the
+//     four lanes);
+//   O^T += V^T P^T: 8 x 2 MFMAs; lane l holds query row c's outputs at
+//     dims 16 dt + 4 qd + v, rescaled by the row's correction in place.
+// The MFMA operands are fp16, the sums fp32.  Exact fp16 operands: the
+// cache is fp16, and q and p enter as two fp16 terms each (pa_split), two
+// MFMAs per product -- x to about 2^-21 of its value (or 2^-25
+// absolutely), so the scores and weighted sums keep fp32 accuracy.  q is multiplied by scale * log2(e) first and the softmax
+// taken with exp2, which is exp of the scaled score.
+constexpr int kMRows = 16;                  // query rows per workgroup
+constexpr int kKRowH = kPMaxD + 8;          // k_s row: 128 fp16 + 8 pad (272 bytes: 16-byte reads spread)
+constexpr int kVRowH = kPTile + 4;          // vt_s row: 64 fp16 + 4 pad (136 bytes)
+constexpr int kKChunks = kPTile * kPMaxD / 8;      // 16-byte chunks of a K tile (1024)
+constexpr int kVPairs = kPTile / 2 * kPMaxD / 8;   // (position pair, 8 dims) items of a V tile (512)
+
+typedef _Float16 pa_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pa_h4 __attribute__((ext_vector_type(4)));
+typedef float pa_f4 __attribute__((ext_vector_type(4)));
+
+template <int NT>
+struct PaStage {                            // one thread's share of a tile's loads
+    uint4 k[(kKChunks + NT - 1) / NT];
+    uint4 v0[(kVPairs + NT - 1) / NT], v1[(kVPairs + NT - 1) / NT];
+};
+
+template <int NT>
+__device__ __forceinline__ void pa_load(PaStage<NT>& st, const PromptAttnArgs& a, size_t head_row0, int64_t c0,
+                                        int valid, int tid) {
+    const uint32_t bytes = static_cast<uint32_t>(valid) * kPMaxD * 2u;
+    const __amdgpu_buffer_rsrc_t kr = buf_rsrc(a.kc + (head_row0 + c0) * kPMaxD, bytes);
+    const __amdgpu_buffer_rsrc_t vr = buf_rsrc(a.vc + (head_row0 + c0) * kPMaxD, bytes);
+#pragma unroll
+    for (int i = 0; i < (kKChunks + NT - 1) / NT; i++) {
+        const int e = tid + i * NT;
+        const uint32_t off = e < kKChunks ? static_cast<uint32_t>(e) * 16u : kOutOfRange;
+        st.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < (kVPairs + NT - 1) / NT; i++) {
+        const int e = tid + i * NT;                 // pair pp = e / 16 (positions 2 pp, 2 pp + 1), dims 8 (e % 16) ..
+        const uint32_t off = e < kVPairs ? static_cast<uint32_t>((e >> 4) * 2 * kPMaxD + (e & 15) * 8) * 2u
+                                         : kOutOfRange;
+        st.v0[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
+        st.v1[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, off + kPMaxD * 2, 0, 0));
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void pa_store(const PaStage<NT>& st, _Float16* k_s, _Float16* vt_s, int tid) {
+#pragma unroll
+    for (int i = 0; i < (kKChunks + NT - 1) / NT; i++) {
+        const int e = tid + i * NT;
+        if (e < kKChunks) *reinterpret_cast<uint4*>(k_s + (e >> 4) * kKRowH + (e & 15) * 8) = st.k[i];
+    }
+#pragma unroll
+    for (int i = 0; i < (kVPairs + NT - 1) / NT; i++) {
+        const int e = tid + i * NT;
+        if (e < kVPairs) {
+            const int pp = e >> 4, d0 = (e & 15) * 8;
+            const uint32_t a[4] = {st.v0[i].x, st.v0[i].y, st.v0[i].z, st.v0[i].w};
+            const uint32_t b[4] = {st.v1[i].x, st.v1[i].y, st.v1[i].z, st.v1[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                // dims d0 + 2j and d0 + 2j + 1: (pos 2pp, pos 2pp + 1) each
+                *reinterpret_cast<uint32_t*>(vt_s + (d0 + 2 * j) * kVRowH + 2 * pp) =
+                    __builtin_amdgcn_perm(b[j], a[j], 0x05040100u);
+                *reinterpret_cast<uint32_t*>(vt_s + (d0 + 2 * j + 1) * kVRowH + 2 * pp) =
+                    __builtin_amdgcn_perm(b[j], a[j], 0x07060302u);
+            }
+        }
+    }
+}
+
+// x = hi + lo in fp16: hi is x with its low 13 significand bits cleared,
+// which fp16 holds exactly whenever |x| >= 2^-14, so no conversion of it can
+// round (the compiler may convert it again, packed, for the MFMA operand:
+// any rounding mode gives the same value); lo = fp16(x - hi), x - hi exact
+// in fp32.  Below 2^-14 the pair is within 2^-25 of x.
+__device__ __forceinline__ void pa_split(float x, _Float16& hi, _Float16& lo) {
+    const float h = __uint_as_float(__float_as_uint(x) & 0xFFFFE000u);
+    hi = static_cast<_Float16>(h);
+    lo = static_cast<_Float16>(__fsub_rn(x, h));
+}
+
+template <int G, bool BF>
+__global__ __launch_bounds__(64 * G) void prompt_attn_mfma_kernel(PromptAttnArgs a) {
+    constexpr int NT = 64 * G, D = kPMaxD;
+    __shared__ __attribute__((aligned(16))) _Float16 k_s[kPTile * kKRowH];
+    __shared__ __attribute__((aligned(16))) _Float16 vt_s[D * kVRowH];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int h = __builtin_amdgcn_readfirstlane(tid >> 6);     // query head h of the kv head
+    const int c = lane & 15, qd = lane >> 4;
+    const int kvh = blockIdx.y;
+    const int r0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * kMRows;
+    const int last_row = (r0 + kMRows < a.rows ? r0 + kMRows : a.rows) - 1;
+    const int64_t wg_last = a.pos0 + last_row;
+    const int r = r0 + c;                                      // lane's query row
+    const int64_t my_last = a.pos0 + (r < last_row ? r : last_row);
+    const int n_tiles = static_cast<int>(wg_last / kPTile) + 1;
+    const int hd = a.nh * D;
+    const size_t head_row0 = static_cast<size_t>(kvh) * a.cap;
+
+    PaStage<NT> st;
+    pa_load<NT>(st, a, head_row0, 0, static_cast<int>(wg_last + 1 < kPTile ? wg_last + 1 : kPTile), tid);
+
+    // q of row r, head kvh G + h, as the B operand of S^T: dims 32 ks + 8 qd ..
+    const float qs = __fmul_rn(a.scale, 1.44269504088896341f);
+    pa_h8 qh[4], ql[4];
+    {
+        const float* src = a.q + static_cast<size_t>(r) * hd + static_cast<size_t>(kvh * G + h) * D + 8 * qd;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+            if (r < a.rows) {
+                x0 = reinterpret_cast<const float4*>(src + 32 * ks)[0];
+                x1 = reinterpret_cast<const float4*>(src + 32 * ks)[1];
+            }
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                _Float16 hi, lo;
+                pa_split(__fmul_rn(xv[i], qs), hi, lo);
+                qh[ks][i] = hi;
+                ql[ks][i] = lo;
+            }
+        }
+    }
+    pa_f4 o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[dt] = pa_f4{0.f, 0.f, 0.f, 0.f};
+    float m = -__builtin_inff(), l = 0.0f;
+
+    for (int t = 0; t < n_tiles; t++) {
+        const int64_t c0 = static_cast<int64_t>(t) * kPTile;
+        __syncthreads();                                       // every wave is done with the last tile
+        pa_store<NT>(st, k_s, vt_s, tid);
+        __syncthreads();
+        if (t + 1 < n_tiles) {
+            const int64_t c1 = c0 + kPTile;
+            pa_load<NT>(st, a, head_row0, c1, static_cast<int>(wg_last + 1 - c1 < kPTile ? wg_last + 1 - c1 : kPTile),
+                        tid);
+        }
+        // S^T = K Q^T: s[mt][v] = score of row r at position c0 + 16 mt + 4 qd + v
+        pa_f4 s[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            s[mt] = pa_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const pa_h8 kf = *reinterpret_cast<const pa_h8*>(k_s + (16 * mt + c) * kKRowH + 32 * ks + 8 * qd);
+                s[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[ks], s[mt], 0, 0, 0);
+                s[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[ks], s[mt], 0, 0, 0);
+            }
+        }
+        // the running softmax of row r
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const bool vis = c0 + 16 * mt + 4 * qd + v <= my_last;
+                s[mt][v] = vis ? s[mt][v] : -__builtin_inff();
+                mx = fmaxf(mx, s[mt][v]);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);                         // finite: position 0 is in every row's first tile
+        const float corr = __builtin_amdgcn_exp2f(__fsub_rn(m, mn));
+        m = mn;
+        float ps = 0.0f;
+        pa_h8 ph[2], pl[2];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float p = __builtin_amdgcn_exp2f(__fsub_rn(s[mt][v], mn));   // 0 where masked
+                ps = __fadd_rn(ps, p);
+                _Float16 hi, lo;
+                pa_split(p, hi, lo);
+                ph[mt >> 1][(mt & 1) * 4 + v] = hi;
+                pl[mt >> 1][(mt & 1) * 4 + v] = lo;
+            }
+        ps = __fadd_rn(ps, __shfl_xor(ps, 16));
+        ps = __fadd_rn(ps, __shfl_xor(ps, 32));
+        l = __fadd_rn(__fmul_rn(l, corr), ps);
+        // O^T = O^T corr + V^T P^T; k index 8 qd + i of step kk is position
+        // 32 kk + 4 qd + i (i < 4) or 32 kk + 16 + 4 qd + i - 4
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            o[dt] *= corr;
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                const _Float16* vrow = vt_s + (16 * dt + c) * kVRowH + 32 * kk + 4 * qd;
+                const pa_h4 v0 = *reinterpret_cast<const pa_h4*>(vrow);
+                const pa_h4 v1 = *reinterpret_cast<const pa_h4*>(vrow + 16);
+                const pa_h8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph[kk], o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl[kk], o[dt], 0, 0, 0);
+            }
+        }
+    }
+    if (r < a.rows) {
+        const size_t at = static_cast<size_t>(r) * hd + static_cast<size_t>(kvh * G + h) * D + 4 * qd;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const float v0 = __fdiv_rn(o[dt][0], l), v1 = __fdiv_rn(o[dt][1], l);
+            const float v2 = __fdiv_rn(o[dt][2], l), v3 = __fdiv_rn(o[dt][3], l);
+            if constexpr (BF) {
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + at + 16 * dt) =
+                    make_uint2(bf16x2_rne(v0, v1), bf16x2_rne(v2, v3));
+            } else {
+                *reinterpret_cast<float4*>(static_cast<float*>(a.out) + at + 16 * dt) = make_float4(v0, v1, v2, v3);
+            }
+        }
+    }
+}
+
 int launch_failed(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "%s launch: %s", what, hipGetErrorString(e));
@@ -219,6 +449,21 @@ int prompt_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_
     const PromptAttnArgs a{q, k_cache, v_cache, out, rows, pos0, n_heads, n_kv, head_dim, cap, scale};
     const dim3 grid((rows + kPRows - 1) / kPRows, n_kv);
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (head_dim == 128) {
+        const dim3 mgrid((rows + kMRows - 1) / kMRows, n_kv);
+        switch (n_heads / n_kv) {
+#define Q4_PROMPT_M(g)                                                                                         \
+    case g:                                                                                                    \
+        if (bf) hipLaunchKernelGGL((prompt_attn_mfma_kernel<g, true>), mgrid, dim3(64 * g), 0, st, a);        \
+        else hipLaunchKernelGGL((prompt_attn_mfma_kernel<g, false>), mgrid, dim3(64 * g), 0, st, a);          \
+        break;
+            Q4_PROMPT_M(1) Q4_PROMPT_M(2) Q4_PROMPT_M(3) Q4_PROMPT_M(4)
+            Q4_PROMPT_M(5) Q4_PROMPT_M(6) Q4_PROMPT_M(7) Q4_PROMPT_M(8)
+#undef Q4_PROMPT_M
+            default: break;
+        }
+        return launch_failed("q4_prompt_attention_dev");
+    }
     switch (n_heads / n_kv) {
 #define Q4_PROMPT_D(g, dd)                                                                                  \
     if (bf) hipLaunchKernelGGL((prompt_attn_kernel<g, dd, true>), grid, dim3(64 * kPRows), 0, st, a);          \
