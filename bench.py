@@ -145,10 +145,14 @@ def group128_bench(torch, lib, dev, reps=5):
 
 def prefill_bench(torch, lib, layers, dev, reps=3):
     """M=512 prompt over the 28 layers' projections: bf16 MFMA GEMM with the
-    dequant fused into the weight-tile load.  Two launch patterns over the
-    same work: one q4_gemm_bf16_dev per projection, and the grouped form
+    dequant fused into the weight-tile load.  Three launch patterns over the
+    same work: one q4_gemm_bf16_dev per projection; the grouped form
     (q4_gemm_bf16_multi_dev over [q, k, v] and over [gate, up], which share
-    their input, then o_proj and down_proj alone)."""
+    their input, then o_proj and down_proj alone); and the prompt forward's
+    form, x already in bf16 (q4_gemm_bf16in_multi_dev) and gate/up as paired
+    tiles with SiLU * up in the epilogue, whose bf16 output is down's x
+    (q4_gemm_bf16in_gate_up_silu_dev) -- the SiLU * mul is inside the timed
+    work, its flops are not counted."""
     from hetero import q4
     m = 512
     xs = {k: torch.randn((m, k), device=dev) for k in (3584, 18944)}
@@ -176,6 +180,16 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
             q4.gemm_bf16_multi_dev(layer[4:6], xs[3584], outs=gouts[3:5], stream=stream, lib=lib)
             q4.gemm_bf16_dev(*layer[6], xs[18944], out=outs[3584], stream=stream, lib=lib)
 
+    xbs = {k: v.to(torch.bfloat16) for k, v in xs.items()}
+    hb = torch.empty((m, 18944), dtype=torch.bfloat16, device=dev)
+
+    def step_bf16():
+        for layer in layers:
+            q4.gemm_bf16_multi_dev(layer[0:3], xbs[3584], outs=gouts[0:3], stream=stream, lib=lib)
+            q4.gemm_bf16_multi_dev([layer[3]], xbs[3584], outs=[outs[3584]], stream=stream, lib=lib)
+            q4.gemm_bf16_gate_up_silu_dev(layer[4], layer[5], xbs[3584], h=hb, stream=stream, lib=lib)
+            q4.gemm_bf16_multi_dev([layer[6]], hb, outs=[outs[3584]], stream=stream, lib=lib)
+
     def timed(fn):
         with torch.cuda.stream(stream):
             fn()
@@ -199,8 +213,10 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
             flops += 2 * m * w.shape[0] * w.shape[1] * 8
     ms = timed(step)
     ms_grouped = timed(step_grouped)
+    ms_bf16 = timed(step_bf16)
     tf = flops / (ms * 1e-3) / 1e12
     tf_grouped = flops / (ms_grouped * 1e-3) / 1e12
+    tf_bf16 = flops / (ms_bf16 * 1e-3) / 1e12
     # error vs the reference contraction, fp32 dequant-matmul (hetero/cpu_model.py:119-136), on
     # each projection shape of layer 0: max |err| / max |ref| and norm-wise
     errs = {}
@@ -220,6 +236,9 @@ def prefill_bench(torch, lib, layers, dev, reps=3):
             "grouped": {"ms": round(ms_grouped, 3), "tflops": round(tf_grouped, 1),
                         "frac_mfma_peak": round(tf_grouped / 2500.0, 4),
                         "launches_per_layer": 4},
+            "bf16_operands": {"ms": round(ms_bf16, 3), "tflops": round(tf_bf16, 1),
+                              "frac_mfma_peak": round(tf_bf16 / 2500.0, 4), "launches_per_layer": 4,
+                              "note": "x in bf16 from its producer; gate/up paired with the SiLU * up epilogue"},
             "peak_tflops_bf16_dense": 2500.0, "flops": flops,
             "max_rel_err_vs_fp32_dequant_matmul": round(worst, 6),
             "err_per_shape": {k: {kk: round(vv, 7) for kk, vv in v.items()} for k, v in errs.items()}}

@@ -287,6 +287,12 @@ int gemm_w4_pair(const uint16_t* xb, const GemmMats& gm, uint16_t* h, int M, int
 // ctl are zero when first used and are left consistent by every launch.
 int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, int M, int K,
                int P, int nx, hipStream_t st);
+
+// gemm_w4_pair over a stream-K split of its tiles (the ranges of gemm_w4_sk,
+// P workgroups in nx groups, any P up to the CUs and the iterations): the
+// owner of each paired tile stores h as gemm_w4_pair does.
+int gemm_w4_sk_pair(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, uint16_t* h,
+                    int M, int K, int P, int nx, hipStream_t st);
 constexpr int kSkCtlWordsHost = 96;   // the control words after the flags (q4_gemm.hip: kSkCtlWords)
 constexpr int kSkCtlErrorsHost = 64;  // the error counter among them (kSkCtlErrors)
 

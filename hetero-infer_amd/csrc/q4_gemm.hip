@@ -395,17 +395,20 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_pair_kernel(const uint16_t* _
 // Stream-K: the tiles (m block major) are split into nx contiguous groups,
 // one per XCD, and each group's T = tiles x G (tile, K step) iterations,
 // tile-major and K-minor, into P equal contiguous ranges, one per workgroup
-// of that XCD.  A range is at most G iterations long (the host launches at
-// least as many workgroups per group as the group has tiles), so it covers
-// at most two segments, a tile's tail and the next tile's head; the
-// workgroup runs the head first.  A segment that does not reach its tile's
-// end is a partial: it goes to the workgroup's slot in `part` at device
-// scope, then its flag is set to the launch's epoch.  The segment that ends
-// a tile (its owner's) adds the partials of the workgroups before it in its
-// group that cover the rest of the tile, nearest first, and stores the
-// tile.  Waits point only to lower-numbered workgroups, which are
-// dispatched first, and a partial is a workgroup's first segment whenever it
-// has two, so an owner, which reaches its tail last, rarely waits.
+// of that XCD.  A range splits at tile boundaries into segments: a tile's
+// tail, whole tiles, the next tile's head; the workgroup runs them last to
+// first.  A segment that does not reach its tile's end (only a range's last
+// one can be such) is a partial: it goes to the workgroup's slot in `part`
+// at device scope, then its flag is set to the launch's epoch.  The segment
+// that ends a tile (its owner's) adds the partials of the workgroups before
+// it in its group that cover the rest of the tile, nearest first, and
+// stores the tile.  Waits point only to lower-numbered workgroups, which
+// are dispatched first, and a partial is a workgroup's first segment, so an
+// owner, which reaches its first segment last, rarely waits.  With at
+// least as many workgroups as tiles a range is at most G iterations long
+// (two segments); with fewer, each tile has at most one partial.
+// Paired gate/up tiles (PAIR) take the same route, the owner's store being
+// the SiLU * up epilogue of gemm_w4_pair_kernel.
 //
 // The epoch makes a flag mean "this launch's partial is in": every
 // workgroup reads it from ctl[0] when it starts, and the last workgroup to
@@ -439,19 +442,45 @@ struct SkGroup {
     __device__ int phys(int s) const { return xcd + nx * s; }
 };
 
+// Part hp of NP of a paired tile's outputs: h = bf16(SiLU(gate) * up) of
+// the accumulator rows i with i TN / (TM TN / NP) = hp; NaN if `poison`.
+template <int BM, int NW, int NP>
+__device__ __forceinline__ void w4_store_pair_rows(const W4Acc<BM, NW>& acc, uint16_t* h, const W4Tile& t, int M,
+                                                   int N, int hp, bool poison, int wave, int lane) {
+    constexpr int TM = W4Layout<BM, NW>::TM, TN = W4Layout<BM, NW>::TN;
+    static_assert(TN == 2, "paired tiles hold a gate and an up block per wave");
+    const int hb = lane >> 5;
+    const int col = t.n0 + wave * 32 + (lane & 31);
+    if (col >= N) return;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        if ((i * TN) / (TM * TN / NP) != hp) continue;
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int row = t.m0 + i * 32 + 8 * (v >> 2) + 4 * hb + (v & 3);
+            if (row < M) {
+                const float a = silu_mul(acc[i][0][v], acc[i][1][v]);
+                h[static_cast<size_t>(row) * N + col] =
+                    poison ? static_cast<uint16_t>(0x7FC0u) : static_cast<uint16_t>(w4_pack_bf16(a, a) & 0xFFFFu);
+            }
+        }
+    }
+}
+
 // Segment [it, stop) of a stream-K range (stop at most its tile's end).
-template <int BM, int NW>
+// NTL: tiles per block row (the N blocks of gm, or of the paired columns).
+template <int BM, int NW, bool PAIR>
 __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, const GemmMats& gm, float* part,
-                                              unsigned* flags, unsigned* errors, unsigned epoch, int M, int K,
-                                              const SkGroup& gp, long it, long stop, const W4Src<BM, NW>& src,
-                                              int tid, int wave, int lane) {
+                                              uint16_t* hout, unsigned* flags, unsigned* errors, unsigned epoch,
+                                              int M, int K, int NTL, const SkGroup& gp, long it, long stop,
+                                              const W4Src<BM, NW>& src, int tid, int wave, int lane) {
     typedef __attribute__((address_space(3))) void* lds_ptr;
     constexpr int TM = W4Layout<BM, NW>::TM, TN = W4Layout<BM, NW>::TN, NB = TM * TN;
     constexpr int NT = 64 * NW;
     constexpr int kDevice = 16;                                    // sc1: device-coherent
     constexpr uint32_t kSlotBytes = 256u * 256u * 4u;
     using u32x4 = unsigned int __attribute__((__vector_size__(16)));
-    const int G = K >> 6, NTL = gm.nb0[gm.count];
+    const int G = K >> 6;
     const long T = gp.T;
     const int P = gp.P, wg = gp.slot;
     W4Acc<BM, NW> acc;
@@ -459,12 +488,13 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
     const int nk = static_cast<int>(stop - it);
     const long tile_start = it - k0;                               // in the group's iterations
     const int tile = gp.t0 + static_cast<int>(it / G);
-    const int nt = tile % NTL, mk = gm_mat(gm, nt);
+    const int nt = tile % NTL, mk = PAIR ? 0 : gm_mat(gm, nt);
     const int N = gm.n_out[mk];
     float* const out = gm.out[mk];
-    const W4Tile t = w4_tile<BM>(xb, gm.w[mk], gm.s[mk], gm.b[mk], M, N, K, tile / NTL, nt - gm.nb0[mk]);
+    const W4Tile t = PAIR ? w4_tile_pair<BM>(xb, gm, M, N, K, tile / NTL, nt)
+                          : w4_tile<BM>(xb, gm.w[mk], gm.s[mk], gm.b[mk], M, N, K, tile / NTL, nt - gm.nb0[mk]);
     w4_zero<BM, NW>(acc);
-    w4_segment<BM, NW>(acc, lds, t, src, k0, nk, wave, lane);
+    w4_segment<BM, NW, PAIR>(acc, lds, t, src, k0, nk, wave, lane);
     if (stop < tile_start + G) {
         const __amdgpu_buffer_rsrc_t pr =
             buf_rsrc(part + static_cast<size_t>(gp.phys(wg)) * (kSlotBytes / 4), kSlotBytes);
@@ -546,22 +576,25 @@ __device__ __forceinline__ void w4_sk_segment(char* lds, const uint16_t* xb, con
                     }
                 __syncthreads();                               // before the next copies overwrite LDS
             }
-            w4_store_rows<BM, NW, kSkParts>(acc, out, t, M, N, h, poison, wave, lane);
+            if constexpr (PAIR) w4_store_pair_rows<BM, NW, kSkParts>(acc, hout, t, M, N, h, poison, wave, lane);
+            else w4_store_rows<BM, NW, kSkParts>(acc, out, t, M, N, h, poison, wave, lane);
         }
     }
 }
 
-template <int BM, int NW>
+template <int BM, int NW, bool PAIR>
 __global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __restrict__ xb, GemmMats gm,
                                                              float* __restrict__ part, unsigned* __restrict__ flags,
-                                                             unsigned* __restrict__ ctl, int M, int K, int nx) {
+                                                             unsigned* __restrict__ ctl, int M, int K, int nx,
+                                                             uint16_t* __restrict__ hout) {
     static_assert(BM == 256 && NW == 4, "stream-K slots assume 256 x 256 tiles of 4 waves");
     extern __shared__ uint4 w4_lds[];
     char* lds = reinterpret_cast<char*>(w4_lds);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = K >> 6;
-    const int tiles = ((M + BM - 1) / BM) * gm.nb0[gm.count];
+    const int NTL = PAIR ? (gm.n_out[0] + 127) / 128 : gm.nb0[gm.count];
+    const int tiles = ((M + BM - 1) / BM) * NTL;
     SkGroup gp;
     gp.xcd = blockIdx.x % nx;
     gp.nx = nx;
@@ -577,15 +610,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_w4_sk_kernel(const uint16_t* __r
     unsigned* errors = ctl + kSkCtlErrors;
     if (begin < end) {
         W4Src<BM, NW> src;
-        w4_src<BM, NW, false>(src, K, wave, lane);
-        const long cut = (begin / G + 1) * G;                     // end of the first tile
-        if (end > cut) {
-            w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, epoch, M, K, gp, cut, end, src, tid, wave, lane);
-            w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, epoch, M, K, gp, begin, cut, src, tid, wave,
-                                  lane);
-        } else {
-            w4_sk_segment<BM, NW>(lds, xb, gm, part, flags, errors, epoch, M, K, gp, begin, end, src, tid, wave,
-                                  lane);
+        w4_src<BM, NW, PAIR>(src, K, wave, lane);
+        // the segments, last to first: [max(tile start, begin), seg_end)
+        for (long seg_end = end; seg_end > begin;) {
+            const long tile_start = (seg_end - 1) / G * G;
+            const long seg_start = tile_start > begin ? tile_start : begin;
+            w4_sk_segment<BM, NW, PAIR>(lds, xb, gm, part, hout, flags, errors, epoch, M, K, NTL, gp, seg_start,
+                                        seg_end, src, tid, wave, lane);
+            seg_end = seg_start;
         }
     }
     // the last workgroup to leave advances the epoch (every workgroup has
@@ -621,15 +653,15 @@ int launch_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K,
     return 0;
 }
 
-template <int BM, int NW>
+template <int BM, int NW, bool PAIR>
 int launch_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, int M, int K,
-                 int P, int nx, hipStream_t st) {
-    auto kern = gemm_w4_sk_kernel<BM, NW>;
+                 int P, int nx, uint16_t* hout, hipStream_t st) {
+    auto kern = gemm_w4_sk_kernel<BM, NW, PAIR>;
     const size_t lds = w4_lds_bytes<BM, NW>();
     static_assert(256 * 256 * 4 / kSkParts <= 3 * w4_stage_bytes(BM), "a part of a slot fits the LDS ring");
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), lds, lds_raised)) return rc;
-    hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, gm, part, flags, ctl, M, K, nx);
+    hipLaunchKernelGGL(kern, dim3(P), dim3(64 * NW), lds, st, xb, gm, part, flags, ctl, M, K, nx, hout);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "prefill gemm (stream-K) launch: %s", hipGetErrorString(e));
     return 0;
@@ -656,7 +688,12 @@ int gemm_w4(const uint16_t* xb, const GemmMats& gm, float* part, int M, int K, i
 
 int gemm_w4_sk(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, int M, int K,
                int P, int nx, hipStream_t st) {
-    return launch_w4_sk<256, 4>(xb, gm, part, flags, ctl, M, K, P, nx, st);
+    return launch_w4_sk<256, 4, false>(xb, gm, part, flags, ctl, M, K, P, nx, nullptr, st);
+}
+
+int gemm_w4_sk_pair(const uint16_t* xb, const GemmMats& gm, float* part, unsigned* flags, unsigned* ctl, uint16_t* h,
+                    int M, int K, int P, int nx, hipStream_t st) {
+    return launch_w4_sk<256, 4, true>(xb, gm, part, flags, ctl, M, K, P, nx, h, st);
 }
 
 }  // namespace q4k

@@ -1635,6 +1635,34 @@ int q4_mlp_dev(const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* g
 
 namespace {
 
+// The calling stream's workspace on the current device.
+int stream_workspace(hipStream_t st, Workspace** ws) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    int dev;
+    if (int rc = current_device(&dev)) return rc;
+    *ws = &g_dev[dev].ws[st];
+    return 0;
+}
+
+// Room for P stream-K partial slots (256 x 256 floats each) and the flags
+// of up to one workgroup per CU, then the control words; flags and control
+// words start at zero once, and every launch leaves them consistent (the
+// epoch scheme of q4_gemm.hip).
+int sk_workspace(Workspace& ws, int P, hipStream_t st) {
+    int rc;
+    const size_t flag_words = static_cast<size_t>(num_cus()) * 32 + kSkCtlWordsHost;
+    if ((rc = grow(ws, ws.part, kWsPart, static_cast<size_t>(P) * 256 * 256 * 4, st, "prefill"))) return rc;
+    const size_t cap_before = ws.cap[kWsSk];
+    if ((rc = grow(ws, ws.sk, kWsSk, flag_words * 4, st, "prefill"))) return rc;
+    if (ws.cap[kWsSk] != cap_before) {
+        const long n = static_cast<long>(ws.cap[kWsSk] / 4);
+        hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st, reinterpret_cast<float*>(ws.sk),
+                           n);
+        HIP_TRY(hipGetLastError());
+    }
+    return 0;
+}
+
 // q4_gemm_bf16_multi_dev on x given in fp32 (x, rounded to bf16 into the
 // workspace first) or already in bf16 (xb).
 int gemm_bf16_multi(int count, const uint32_t* const* w, const uint16_t* const* scales,
@@ -1680,31 +1708,13 @@ int gemm_bf16_multi(int count, const uint32_t* const* w, const uint16_t* const* 
         return 0;
     }
     Workspace* ws;
-    {
-        std::lock_guard<std::mutex> lock(g_mu);
-        int dev;
-        if ((rc = current_device(&dev))) return rc;
-        ws = &g_dev[dev].ws[st];
-    }
+    if ((rc = stream_workspace(st, &ws))) return rc;
     PrefillPlan plan;
     if ((rc = plan_prefill(m, nblocks, ncols, n_in, &plan))) return rc;
     const size_t mk = static_cast<size_t>(m) * n_in, mn = static_cast<size_t>(m) * ncols;
     if (!xb_in && (rc = grow(*ws, ws->xbf, kWsXbf, mk * 2, st, "prefill"))) return rc;
     if (plan.sk_p > 0) {
-        // the flags of up to one workgroup per CU (sk_ok: P <= CUs), then the control words
-        const size_t flag_words = static_cast<size_t>(num_cus()) * 32 + kSkCtlWordsHost;
-        if ((rc = grow(*ws, ws->part, kWsPart, static_cast<size_t>(plan.sk_p) * 256 * 256 * 4, st, "prefill")))
-            return rc;
-        const size_t cap_before = ws->cap[kWsSk];
-        if ((rc = grow(*ws, ws->sk, kWsSk, flag_words * 4, st, "prefill"))) return rc;
-        if (ws->cap[kWsSk] != cap_before) {
-            // flags and control words start at zero once; every launch
-            // leaves them consistent (the epoch scheme of q4_gemm.hip)
-            const long n = static_cast<long>(ws->cap[kWsSk] / 4);
-            hipLaunchKernelGGL(fill_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, st,
-                               reinterpret_cast<float*>(ws->sk), n);
-            HIP_TRY(hipGetLastError());
-        }
+        if ((rc = sk_workspace(*ws, plan.sk_p, st))) return rc;
     } else if (plan.S > 1 && (rc = grow(*ws, ws->part, kWsPart, plan.S * mn * 4, st, "prefill"))) {
         return rc;
     }
@@ -1777,7 +1787,28 @@ int q4_gemm_bf16in_gate_up_silu_dev(const uint32_t* gate_w, const uint16_t* gate
     gm.b[1] = up_b;
     gm.n_out[0] = gm.n_out[1] = n_inter;
     gm.count = 2;
-    return gemm_w4_pair(xb, gm, h, m, n_in, st);
+    // one 256 x (128 + 128) tile per workgroup while the tiles fit the CUs
+    // in one round; past that, stream-K over one workgroup per CU, so that
+    // a last partial round does not double the time (Q4_PAIR_PLAN=dp or
+    // sk:<P> chooses)
+    const int cus = num_cus();
+    const long tiles = static_cast<long>((m + 255) / 256) * ((n_inter + 127) / 128);
+    const long T = tiles * (n_in / 64);
+    int P = tiles > cus ? static_cast<int>(std::min<long>(cus >= 8 ? cus / 8 * 8 : cus, T)) : 0;
+    if (const char* env = getenv("Q4_PAIR_PLAN")) {
+        char tail = 0;
+        int p = 0;
+        if (std::strcmp(env, "dp") == 0) P = 0;
+        else if (sscanf(env, "sk:%d%c", &p, &tail) == 1 && p >= 1 && p <= cus && p <= T) P = p;
+        else return fail(Q4_EARG, "Q4_PAIR_PLAN=%s: expected dp or sk:<P> with P in [1, %ld]", env,
+                         std::min<long>(cus, T));
+    }
+    if (P == 0) return gemm_w4_pair(xb, gm, h, m, n_in, st);
+    Workspace* ws;
+    if ((rc = stream_workspace(st, &ws))) return rc;
+    if ((rc = sk_workspace(*ws, P, st))) return rc;
+    return gemm_w4_sk_pair(xb, gm, static_cast<float*>(ws->part), ws->sk, sk_ctl(*ws), h, m, n_in, P,
+                           sk_groups(P, tiles), st);
 }
 
 int q4_gemm_bf16_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases,

@@ -185,10 +185,16 @@ int q4_gemm_bf16in_multi_dev(int count, const uint32_t *const *w, const uint16_t
  * h[m][n_inter] = bf16(SiLU(x . Wg^T) * (x . Wu^T)) as bf16 bit patterns,
  * rounded to nearest even -- the down projection's operand.  One launch:
  * each tile holds the same 128 rows of both matrices, so the SiLU * mul is
- * the GEMM's epilogue; the fp32 sums are those of q4_gemm_bf16in_multi_dev
- * on {gate, up} when it runs without split-K (as it does when the two
- * matrices give at least one tile per CU).  gs must be 64; w and x 16-byte
- * aligned.  No workspace. */
+ * the GEMM's epilogue.  While the 256 x 128 output tiles fit the CUs in
+ * one round, each tile is one workgroup and the fp32 sums are those of
+ * q4_gemm_bf16in_multi_dev on {gate, up} without split-K (bit for bit);
+ * past that (a 512-token prompt at n_inter 18944 has 296 tiles) the tiles'
+ * K steps are shared out stream-K over one workgroup per CU and a tile's
+ * partial sums are added in a fixed order, which may move a value by one
+ * bf16 unit.  Q4_PAIR_PLAN=dp or sk:<P> forces either form.  gs must be
+ * 64; w and x 16-byte aligned.  The stream-K form uses the calling
+ * stream's workspace, which grows on first use (run the largest call once
+ * before capturing it in a graph). */
 int q4_gemm_bf16in_gate_up_silu_dev(const uint32_t *gate_w, const uint16_t *gate_s, const uint16_t *gate_b,
                                     const uint32_t *up_w, const uint16_t *up_s, const uint16_t *up_b,
                                     const uint16_t *xb, uint16_t *h, int m, int n_inter, int n_in, int gs,

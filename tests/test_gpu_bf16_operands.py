@@ -9,7 +9,11 @@ conversion, the rule of x_to_bf16_kernel):
   * q4_gemm_bf16in_multi_dev(bf16(x)) == q4_gemm_bf16_multi_dev(x);
   * q4_gemm_bf16in_gate_up_silu_dev(bf16(x)) == bf16(SiLU(g) * u) with g, u
     from q4_gemm_bf16_multi_dev on {gate, up} under the unsplit plan and
-    SiLU * u from q4_silu_mul_dev;
+    SiLU * u from q4_silu_mul_dev, in its one-workgroup-per-tile form; its
+    stream-K form (tiles past one round of CUs, or forced) adds a tile's
+    partial sums, so it is held next to that (a bf16 unit, more where a
+    sum cancels), and to
+    the float64 product of the same bf16 operands;
   * q4_add_rmsnorm_rows_bf16_dev == bf16(q4_add_rmsnorm_rows_dev), the
     residual written back the same, on the 16-byte and the scalar path;
   * q4_prompt_attention_bf16_dev == bf16(q4_prompt_attention_dev).
@@ -56,6 +60,13 @@ def _plan(monkeypatch, plan):
         monkeypatch.setenv("Q4_GEMM_PLAN", plan)
 
 
+def _pair_plan(monkeypatch, plan):
+    if plan is None:
+        monkeypatch.delenv("Q4_PAIR_PLAN", raising=False)
+    else:
+        monkeypatch.setenv("Q4_PAIR_PLAN", plan)
+
+
 def _bits(t):
     import torch
     return t.contiguous().view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
@@ -91,13 +102,58 @@ def test_gate_up_silu_epilogue_equals_separate_calls(torch, lib, monkeypatch, m,
     _plan(monkeypatch, None)
     h32 = torch.empty_like(g)
     assert lib.q4_silu_mul_dev(g.data_ptr(), u.data_ptr(), h32.data_ptr(), g.numel(), _sp(torch)) == 0
+    _pair_plan(monkeypatch, "dp")
     got = q4.gemm_bf16_gate_up_silu_dev(gate, up, xb)
     again = q4.gemm_bf16_gate_up_silu_dev(gate, up, xb)
+    _pair_plan(monkeypatch, None)
     torch.cuda.synchronize()
     assert got.dtype == torch.bfloat16 and got.shape == (m, n_inter)
     assert torch.isfinite(got.float()).all()
     assert torch.equal(_bits(got), _bits(h32.to(torch.bfloat16)))
     assert torch.equal(_bits(got), _bits(again))
+
+
+# the default plan of a 512-token prompt (296 tiles: stream-K over the
+# CUs), and forced stream-K plans on small shapes: 8 and 5 workgroups
+# (fewer than the tiles: ranges of several tiles), 64 (more than the
+# tiles: several partials per tile), 3 over a single tile row
+@pytest.mark.parametrize("m,n_inter,n_in,plan", [(512, 18944, 3584, None), (300, 1000, 1024, "sk:8"),
+                                                 (300, 1000, 1024, "sk:5"), (300, 1000, 1024, "sk:64"),
+                                                 (37, 200, 512, "sk:3")])
+def test_gate_up_silu_stream_k(torch, lib, monkeypatch, m, n_inter, n_in, plan):
+    print(f"gate/up silu stream-K m={m} n={n_inter} k={n_in} plan={plan}", flush=True)
+    gate, up = _mats(torch, 940, (n_inter, n_inter), n_in)
+    xb = torch.from_numpy(synth.activations(941 + m, m, n_in)).cuda().to(torch.bfloat16)
+    _pair_plan(monkeypatch, "dp")
+    want = q4.gemm_bf16_gate_up_silu_dev(gate, up, xb)
+    _pair_plan(monkeypatch, plan)
+    got = q4.gemm_bf16_gate_up_silu_dev(gate, up, xb)
+    again = q4.gemm_bf16_gate_up_silu_dev(gate, up, xb)
+    _pair_plan(monkeypatch, None)
+    torch.cuda.synchronize()
+    assert lib.q4_prefill_errors(_sp(torch)) == 0
+    assert torch.equal(_bits(got), _bits(again))
+    assert torch.isfinite(got.float()).all()
+    # next to the one-workgroup-per-tile result: the fp32 sums differ in
+    # their last places (relative to the sum of the terms' magnitudes, so
+    # more near a cancelling sum), and the bf16 rounding may then move by a
+    # unit: |diff| <= 2^-7 |want| + 1e-5 max |want|
+    g32, w32 = got.float(), want.float()
+    diff = (g32 - w32).abs()
+    moved = int((_bits(got) != _bits(want)).sum())
+    print(f"stream-K vs one workgroup per tile: {moved} of {got.numel()} values moved, largest "
+          f"{float(diff.max()) / float(w32.abs().max()):.2e} of max |h|", flush=True)
+    assert bool((diff <= 2.0 ** -7 * w32.abs() + 1e-5 * w32.abs().max()).all())
+    # and against float64 with the same bf16 operands
+    import oracle
+    xr = xb.float().cpu().numpy().astype(np.float64)
+    wg, wu = (oracle.dequant_np(*synth.qlinear(940 + i + n_inter, n_inter, n_in, 64), 64) for i in (0, 1))
+    bf = lambda a: torch.from_numpy(a.astype(np.float32)).to(torch.bfloat16).float().numpy().astype(np.float64)
+    g64, u64 = xr @ bf(wg).T, xr @ bf(wu).T
+    ref = g64 / (1 + np.exp(-g64)) * u64
+    err = oracle.normwise_rel(got.float().cpu().numpy(), ref)
+    print(f"normwise error vs float64: {err:.2e}", flush=True)
+    assert err < 8e-3                             # bf16 output rounding, 2^-8 relative at most
 
 
 def test_gate_up_silu_argument_errors(torch, lib):
