@@ -60,6 +60,7 @@ struct ChainPhase {
     int ring;        // ring size: 1, 2, 4 or 5, dividing the unit's items
     int pair;        // gate/up: out[0] = SiLU(W0 x) * (W1 x)
     int n_total;     // rows of the phase: n_out[0] (pair) or the sum of n_out
+    int sep_stage;   // x staged for the group sums in LDS of its own (else over the planes)
 };
 
 // Barrier state, every word on its own 128-byte line.  Zero between launches:
@@ -205,9 +206,15 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     float* red = xsum_lds + Gr;                                   // [16]
     int* claim_ctr = reinterpret_cast<int*>(red + 16);
     uint4* xpl = reinterpret_cast<uint4*>(red + 16 + 4 + 16);     // [C*256] swizzled
-    float* xstage = reinterpret_cast<float*>(xpl);                // [G][stage_stride(0)]: the prologue only
     const int NU = PAIR ? 2 * UB : UB;
     float* Tw = reinterpret_cast<float*>(xpl + C * 256) + wave * (NU * kTermStride);   // [NU][kTermStride]
+    // x staged for the group sums ([G][stage_stride(0)], the prologue only):
+    // after every wave's term table when it fits (sep_stage), so the planes
+    // may be written while the sums still read it; else over the planes,
+    // which then wait for a barrier after the sums
+    const bool sep = ph->sep_stage;                               // uniform
+    float* xstage = sep ? reinterpret_cast<float*>(xpl + C * 256) + nwaves * NU * kTermStride
+                        : reinterpret_cast<float*>(xpl);
     const int n_total = ph->n_total;
     const int n_units = (n_total + UB - 1) / UB;
     const int items = NU * C;
@@ -233,6 +240,8 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     chain_event(stamps, st, 2);
 
     // ---- 3. x: device-scope loads, thread t owns words t, t + nt, t + 2nt
+    // (the unit counter is free again: every wave is past the phase before)
+    if (tid == 0) *claim_ctr = 0;
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(n_in) * 4u);
     float4 wv[kChainRounds][2];
 #pragma unroll
@@ -269,8 +278,7 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
         for (int g = tid; g < G; g += nt)
             xsum_lds[g] = chain_add<32>(chain_add<32>(0.0f, xstage + g * SS), xstage + g * SS + 32);
     }
-    if (tid == 0) *claim_ctr = 0;
-    __syncthreads();
+    if (!sep) __syncthreads();                                    // the staging is read: the planes may overwrite it
 
     auto claim = [&]() -> int {
         int v = 0;
@@ -547,7 +555,16 @@ int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) 
     if (!ring) return fail(Q4_EARG, "no ring size divides %d items", items);
     out.UB = UB;
     out.ring = ring;
-    const size_t need = kChainLdsHead + stream_lds_bytes(1, C, G, kChainWaves, mult * UB, kChainRounds, 0);
+    // the x staging in LDS of its own when it fits beside the planes and
+    // every wave's term table: one barrier fewer in the x prologue (the
+    // sweep 1.248 -> 1.227 ms, same box)
+    const size_t shared = kChainLdsHead + stream_lds_bytes(1, C, G, kChainWaves, mult * UB, kChainRounds, 0);
+    const size_t header = static_cast<size_t>((G + 3) & ~3) * 4 + 16 * 4 + 16 + 64;
+    const size_t separate = kChainLdsHead + header + static_cast<size_t>(C) * 256 * 16 +
+                            static_cast<size_t>(kChainWaves) * mult * UB * kTermStride * 4 +
+                            static_cast<size_t>(G) * stage_stride(0) * 4;
+    out.sep_stage = separate <= kStreamLdsMax ? 1 : 0;
+    const size_t need = out.sep_stage ? separate : shared;
     if (need > lds) lds = need;
     return 0;
 }
