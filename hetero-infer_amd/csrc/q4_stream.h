@@ -75,12 +75,15 @@ __host__ __device__ constexpr int stage_stride(int gsh) { return (64 << gsh) + 4
 // x planes and the per-wave term
 // tables -- where the prologue first stages one row of x in fp32.
 // rw: words of x per thread and row (the register rounds of the x prologue).
-inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU, int rw, int gsh = 0) {
+// sep: the staging after the term tables instead of over them (the planes
+// may then be written while the group sums still read the staging).
+inline size_t stream_lds_bytes(int mr, int n_chunks, int G, int nwaves, int NU, int rw, int gsh = 0, bool sep = false) {
     (void)rw;
     const size_t header = static_cast<size_t>(mr) * ((G + 3) & ~3) * 4 + static_cast<size_t>(mr) * 16 * 4 + 16 + 64;
     const size_t planes = static_cast<size_t>(mr) * n_chunks * 256 * 16;
     const size_t terms = static_cast<size_t>(nwaves) * mr * NU * kTermStride * 4;
     const size_t stage = static_cast<size_t>(G) * stage_stride(gsh) * 4;
+    if (sep) return header + planes + terms + stage;
     return header + (planes + terms > stage ? planes + terms : stage);
 }
 
@@ -330,7 +333,8 @@ __device__ __forceinline__ void greedy_tail(float bv, int bi, const GreedyArgs& 
 template <int MR, int RW, bool PAIR, int RING, bool NORM, int GSH>
 __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_kernel(MatList ml,
                                                                                      const float* __restrict__ x,
-                                                                                     int n_in, int UB, NormArgs na) {
+                                                                                     int n_in, int UB, int sep,
+                                                                                     NormArgs na) {
     static_assert(!NORM || (MR == 1 && RW == 1 && GSH == 0), "the norm prologue takes one row, one word per thread");
     static_assert(GSH == 0 || GSH == 1, "group size 64 or 128");
     extern __shared__ uint4 lds4[];
@@ -348,10 +352,15 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
     int* claim_ctr = reinterpret_cast<int*>(red + MR * 16);       // units handed out past the first
     float* stage = red + MR * 16 + 4;                              // NORM: the wave sums [16]
     uint4* xpl = reinterpret_cast<uint4*>(stage + 16);            // [MR][C*256] swizzled
-    float* xstage = reinterpret_cast<float*>(xpl);                // [G][stage_stride]: the prologue only
     const int NU = PAIR ? 2 * UB : UB;                            // rows per unit
     float* Tw = reinterpret_cast<float*>(xpl + MR * C * 256) + wave * (MR * NU * kTermStride);
                                                                   // this wave: [MR][NU][kTermStride]
+    // x staged for the group sums ([G][stage_stride], the prologue only):
+    // after every wave's term tables (sep), so the planes need not wait for
+    // the sums to have read it, or over the planes
+    float* xstage = sep ? reinterpret_cast<float*>(xpl + MR * C * 256) + nwaves * MR * NU * kTermStride
+                        : reinterpret_cast<float*>(xpl);
+    if (tid == 0) *claim_ctr = 0;                                 // published by the prologue's first barrier
 
     // ---- x loads: thread t owns words t, t + nt, ... of every row, 8 values
     //      each, through a resource over x (words at or past the row end read
@@ -498,8 +507,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
         load_item<PAIR, GSH>(ring[d], pf_rows, pf_unit, pf_c, pf_r, UB, wpr, G, vo_w, vo_g, has_work);
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
-    if (tid == 0) *claim_ctr = 0;
-    __syncthreads();
+    if (!sep) __syncthreads();                                    // the staging is read: the planes may overwrite it
 
     // the claim for the wave's second unit, in flight during the rest of the prologue
     auto claim = [&]() -> int {
@@ -704,7 +712,7 @@ __global__ __launch_bounds__(64 * stream_waves_per_cu<MR>()) void gemv_stream_ke
 // that every workgroup runs in the first round.
 template <int MR, int RW, bool PAIR, int RING, bool NORM, int GSH>
 int launch_stream_k(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
-                    size_t lds, int want, hipStream_t st) {
+                    size_t lds, int sep, int want, hipStream_t st) {
     auto kern = gemv_stream_kernel<MR, RW, PAIR, RING, NORM, GSH>;
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(kern), kStreamLdsMax, lds_raised)) return rc;
@@ -715,7 +723,7 @@ int launch_stream_k(const MatList& ml, const float* x, const NormArgs& na, int n
     const int grid = want < cap ? want : cap;
     if (na.greedy.part && (MR != 1 || PAIR || grid > kGreedyMaxParts))
         return fail(Q4_EARG, "greedy token: one matrix, one row and at most %d workgroups", kGreedyMaxParts);
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB, na);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nwaves), lds, st, ml, x, n_in, UB, sep, na);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "stream gemv launch: %s", hipGetErrorString(e));
     return 1;

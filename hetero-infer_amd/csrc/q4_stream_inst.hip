@@ -13,7 +13,7 @@ namespace q4k {
 
 #define Q4_STREAM_INST(RW, NORM)                                                                      \
     template int launch_stream_k<Q4_MR, RW, static_cast<bool>(Q4_PAIR), Q4_RING, NORM, Q4_GSH>(      \
-        const MatList&, const float*, const NormArgs&, int, int, int, size_t, int, hipStream_t);
+        const MatList&, const float*, const NormArgs&, int, int, int, size_t, int, int, hipStream_t);
 
 Q4_STREAM_INST(1, false)
 #if Q4_MR <= 4

@@ -77,7 +77,7 @@ int num_cus() {
 #define Q4_STREAM_EXTERN(MR, RW, PAIR, RING, NORM, GSH)                                            \
     extern template int launch_stream_k<MR, RW, PAIR, RING, NORM, GSH>(const MatList&, const float*,   \
                                                                        const NormArgs&, int, int, int, \
-                                                                       size_t, int, hipStream_t);
+                                                                       size_t, int, int, hipStream_t);
 #define Q4_STREAM_RINGS(MR, RW, PAIR, NORM, GSH)                                                    \
     Q4_STREAM_EXTERN(MR, RW, PAIR, 1, NORM, GSH) Q4_STREAM_EXTERN(MR, RW, PAIR, 2, NORM, GSH)
 #define Q4_STREAM_GS(GSH)                                                                           \
@@ -601,7 +601,7 @@ hipError_t launch_main(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 
 template <int MR, int RW, bool PAIR, bool NORM, int GSH>
 int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int n_in, int UB, int nwaves,
-                     size_t lds, int n_units, int items, hipStream_t st) {
+                     size_t lds, int sep, int n_units, int items, hipStream_t st) {
     // one unit per wave, capped by the launch at what is resident at once
     const int grid = (n_units + nwaves - 1) / nwaves;
     // ring: a divisor of the unit's items (units change only between rings),
@@ -610,11 +610,11 @@ int launch_stream_rw(const MatList& ml, const float* x, const NormArgs& na, int 
     // 15.6 us at 10, 12.5 us at 2, 14.7 us at 1; gate+up 17.3 us at 4,
     // 16.3 us at 2), the more loads a CU has queued the longer each waits.
     if (items % 2 == 0)
-        return launch_stream_k<MR, RW, PAIR, 2, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+        return launch_stream_k<MR, RW, PAIR, 2, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, sep, grid, st);
     if constexpr (MR == 1 && !PAIR)
         if (items % 5 == 0)
-            return launch_stream_k<MR, RW, PAIR, 5, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
-    return launch_stream_k<MR, RW, PAIR, 1, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, grid, st);
+            return launch_stream_k<MR, RW, PAIR, 5, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, sep, grid, st);
+    return launch_stream_k<MR, RW, PAIR, 1, NORM, GSH>(ml, x, na, n_in, UB, nwaves, lds, sep, grid, st);
 }
 
 // GSH: group size 64 << GSH.  NORM: the norm prologue (group size 64; one
@@ -649,27 +649,31 @@ int launch_stream(const MatList& ml, const float* x, int n_in, hipStream_t st, c
     if (nwaves < minw) nwaves = minw;
     if (nwaves > kWavesPerCu) nwaves = kWavesPerCu;
     const int rw = (C * kChunkWords + 64 * nwaves - 1) / (64 * nwaves);
-    const size_t lds = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB, rw, GSH);
+    // the x staging in LDS of its own while that keeps two workgroups per CU
+    // possible: one barrier fewer in the prologue
+    const size_t lds_sep = stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB, rw, GSH, true);
+    const int sep = lds_sep <= kStreamLdsMax / 2 ? 1 : 0;
+    const size_t lds = sep ? lds_sep : stream_lds_bytes(MR, C, G, nwaves, (PAIR ? 2 : 1) * UB, rw, GSH);
     if (lds > kStreamLdsMax) return 0;
     const int items = (PAIR ? 2 : 1) * UB * C;
     if constexpr (NORM)
         return rw == 1 && GSH == 0
-                   ? launch_stream_rw<MR, 1, PAIR, true, 0>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st)
+                   ? launch_stream_rw<MR, 1, PAIR, true, 0>(ml, x, na, n_in, UB, nwaves, lds, sep, n_units, items, st)
                    : 0;
     switch (rw) {
-        case 1: return launch_stream_rw<MR, 1, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+        case 1: return launch_stream_rw<MR, 1, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, sep, n_units, items, st);
         case 2:
             if constexpr (rmax >= 2)
-                return launch_stream_rw<MR, 2, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+                return launch_stream_rw<MR, 2, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, sep, n_units, items, st);
             return 0;
         // (3 and 4 words per thread: the single-matrix launches of one row)
         case 3:
             if constexpr (rmax >= 3 && !PAIR)
-                return launch_stream_rw<MR, 3, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+                return launch_stream_rw<MR, 3, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, sep, n_units, items, st);
             return 0;
         case 4:
             if constexpr (rmax >= 4 && !PAIR)
-                return launch_stream_rw<MR, 4, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, n_units, items, st);
+                return launch_stream_rw<MR, 4, PAIR, false, GSH>(ml, x, na, n_in, UB, nwaves, lds, sep, n_units, items, st);
             return 0;
         default: return 0;
     }
