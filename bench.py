@@ -808,7 +808,9 @@ def chain_stamp_table(torch, chain, n_phases, dev, stream, reps=3):
     microseconds, of each step of a phase -- the wait at the grid barrier
     before it, x loaded and staged, the int16 planes, wave 0's items, every
     wave's items and stores -- and the latency from the last workgroup's
-    arrival to the first one's release."""
+    arrival to the first one's release.  Where the phase before does not
+    write x, x is loaded and staged from the workgroup's arrival on, before
+    the release; the items start at the later of release and planes."""
     import numpy as np
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     buf = torch.zeros((n_phases + 1) * cus * 8, dtype=torch.int64, device=dev)
@@ -829,10 +831,12 @@ def chain_stamp_table(torch, chain, n_phases, dev, stream, reps=3):
                                                    "planes", "items_wave0", "items_and_stores", "phase")})
         r["barrier_wait"].append(np.median(released - arrived))
         r["release_after_last_arrival"].append(released.min() - arrived.max())
-        r["x_staged"].append(np.median(staged - released))
+        early = planes <= released
+        ready = np.maximum(planes, released)
+        r["x_staged"].append(np.median(staged - np.where(early, arrived, released)))
         r["planes"].append(np.median(planes - staged))
-        r["items_wave0"].append(np.median(wave0 - planes))
-        r["items_and_stores"].append(np.median(nxt - planes))
+        r["items_wave0"].append(np.median(wave0 - ready))
+        r["items_and_stores"].append(np.median(nxt - ready))
         r["phase"].append(np.median(nxt - arrived))
     return {k: {kk: round(float(np.median(vv)), 3) for kk, vv in v.items() if vv} for k, v in rows.items()}
 
@@ -1003,7 +1007,9 @@ def main():
 
     # the same sweep as one chained GEMV program (include/q4chain.h): one
     # launch, a grid barrier between phases, each phase's first weights
-    # requested before its barrier.  It is the headline unless a barrier
+    # requested before its barrier (and its x quantised there too, since
+    # every phase of the sweep reads an x from outside the program, as the
+    # reference's per-shape calls do).  It is the headline unless a barrier
     # wait timed out (then its outputs are not to be trusted and the grouped
     # launches give the figure).
     chained = None
@@ -1085,7 +1091,8 @@ def main():
                     "kernel": "gemv_chain_kernel: the whole sweep as one launch of 113 phases",
                     "avg_launch_us": round(chain_ev * 1e3, 3)}
         path = ("one chained GEMV program per step (include/q4chain.h): 113 phases in one persistent "
-                "launch, a grid barrier between phases")
+                "launch, a grid barrier between phases; each phase's first weights and its x (read from "
+                "outside the program) loaded before its barrier")
         launches = 1
     else:
         achieved = grouped_achieved

@@ -22,7 +22,10 @@
 // Memory: outputs are stored, and x is loaded, at device scope (cache policy
 // sc1): a phase's outputs are written on one XCD and read as x on all
 // eight, whose L2s are not coherent with each other.  Before a workgroup
-// signals the barrier, each of its waves has waited for its own stores.
+// signals a barrier after which a phase reads (or writes over) what an
+// earlier phase stored, each of its waves has waited for its own stores.
+// x that the phase just before does not write is loaded, and its prologue
+// run, before the barrier, as the weights are.
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -61,6 +64,8 @@ struct ChainPhase {
     int pair;        // gate/up: out[0] = SiLU(W0 x) * (W1 x)
     int n_total;     // rows of the phase: n_out[0] (pair) or the sum of n_out
     int sep_stage;   // x staged for the group sums in LDS of its own (else over the planes)
+    int x_early;     // the phase before does not write x: x and its prologue before the barrier
+    int ack_stores;  // every wave's stores complete before the arrival at the next barrier
 };
 
 // Barrier state, every word on its own 128-byte line.  Zero between launches:
@@ -222,7 +227,25 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     const int first_unit = blockIdx.x + wave * grid;
     const bool has_work = first_unit < n_units;                   // uniform
 
-    // ---- 1. the first ring of this phase: weights only, no dependency
+    // ---- 1. x, first when the phase before does not write it (x_early):
+    //         then x does not depend on that phase either, and its loads
+    //         and the whole prologue run before the barrier as the weights'
+    //         do.  Device-scope loads, thread t owns words t, t + nt, t + 2nt.
+    const bool early = ph->x_early;                               // uniform
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(n_in) * 4u);
+    float4 wv[kChainRounds][2];
+    auto load_x = [&]() {
+#pragma unroll
+        for (int r = 0; r < kChainRounds; r++) {
+            const int j = r * nt + tid;
+            const uint32_t off = j < wpr ? static_cast<uint32_t>(8 * j) * 4u : kOutOfRange;
+            wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kStoreDevice));
+            wv[r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, kStoreDevice));
+        }
+    };
+    if (early) load_x();
+
+    // ---- 2. the first ring of this phase: weights only, no dependency
     Item ring[RING];
     const uint32_t vo_w = static_cast<uint32_t>(lane) * 16u, vo_g = static_cast<uint32_t>(lane >> 1) * 2u;
     int pf_unit = first_unit, pf_c = 0, pf_r = 0;
@@ -234,23 +257,17 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
         if (++pf_r == NU) { pf_r = 0; ++pf_c; }
     }
 
-    // ---- 2. every workgroup is done with the phases before (x may be one
-    //         of their outputs)
-    if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
-    chain_event(stamps, st, 2);
-
-    // ---- 3. x: device-scope loads, thread t owns words t, t + nt, t + 2nt
-    // (the unit counter is free again: every wave is past the phase before)
-    if (tid == 0) *claim_ctr = 0;
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(n_in) * 4u);
-    float4 wv[kChainRounds][2];
-#pragma unroll
-    for (int r = 0; r < kChainRounds; r++) {
-        const int j = r * nt + tid;
-        const uint32_t off = j < wpr ? static_cast<uint32_t>(8 * j) * 4u : kOutOfRange;
-        wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kStoreDevice));
-        wv[r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, kStoreDevice));
+    // ---- 3. otherwise every workgroup must be done with the phase before
+    //         (x is one of its outputs) before x is loaded
+    if (!early) {
+        if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
+        chain_event(stamps, st, 2);
+        load_x();
     }
+
+    // ---- 4. the x prologue (the unit counter is free again: every wave of
+    //         the workgroup is past the phase before)
+    if (tid == 0) *claim_ctr = 0;
     // group sums in ascending order (kernel/q4gemv.c:244-248) and max |x|
     // (:258-259), as the streaming kernel computes them
     {
@@ -313,8 +330,12 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     }
     __syncthreads();
     chain_event(stamps, st, 4);
+    if (early) {
+        if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
+        chain_event(stamps, st, 2);
+    }
 
-    // ---- 4. the item stream (as gemv_stream_kernel)
+    // ---- 5. the item stream (as gemv_stream_kernel)
     constexpr int GPC = kChunkWords / WPG;                        // groups per chunk
     auto consume = [&](const Item& itm, int c, int u) {
         const int lim = wpr - c * kChunkWords;                    // uniform
@@ -438,9 +459,12 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
 
     chain_event(stamps, st, 5);
 
-    // ---- 5. this wave's stores are done; the workgroup arrives at the next
-    //         barrier (the LDS of this phase is free once every wave is past it)
-    wait_own_stores();
+    // ---- 6. the workgroup arrives at the next barrier (the LDS of this
+    //         phase is free once every wave is past it), each wave's stores
+    //         complete first where a later phase reads what was stored
+    //         before that barrier (ack_stores); else the stores only need to
+    //         be complete at the kernel's end, which they are
+    if (ph->ack_stores) wait_own_stores();
     if (arrive_after) {
         chain_arrive(sync, stamps, st, p);
     } else {
@@ -503,6 +527,17 @@ struct q4_chain_plan {
 
 namespace {
 
+// Whether phase `ph` writes any byte of [lo, hi) (every out[k] of its
+// matrices counts as written, out[1] of a gate/up pair too).
+bool phase_writes(const q4_chain_phase& ph, uintptr_t lo, uintptr_t hi) {
+    for (int k = 0; k < ph.count; k++) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(ph.out[k]);
+        const uintptr_t b = a + static_cast<uintptr_t>(ph.n_out[k]) * 4u;
+        if (a < hi && lo < b) return true;
+    }
+    return false;
+}
+
 // Rows per unit and ring size of a phase, as launch_stream picks them for
 // one row at 16 waves per CU.
 int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) {
@@ -530,6 +565,12 @@ int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) 
         rb += in.n_out[k];
     }
     if (in.pair && in.n_out[0] != in.n_out[1]) return fail(Q4_EARG, "pair: n_out %d != %d", in.n_out[0], in.n_out[1]);
+    {
+        // a workgroup may store its rows while another still loads x
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(in.x);
+        if (phase_writes(in, lo, lo + static_cast<uintptr_t>(in.n_in) * 4u))
+            return fail(Q4_EARG, "an output overlaps x");
+    }
     for (int k = count; k <= kMaxMats; k++) out.ml.row_begin[k] = rb;
     out.ml.count = count;
     out.ml.mrows = 1;
@@ -569,6 +610,35 @@ int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) 
     return 0;
 }
 
+// What each barrier must order, from the buffers the phases read and write:
+//  - x_early[j]: phase j-1 writes no byte of x_j, so x_j may be loaded (and
+//    its prologue run) before barrier j; every phase before j-1 is past
+//    barrier j-1 by then.
+//  - ack_stores[b-1]: the waves wait for their stores before arriving at
+//    barrier b when a read or a write after b must see them: x_j written by
+//    an earlier phase is read after barrier j (j-1 when early), and a phase
+//    writing what an earlier phase wrote stores after its own barrier.
+void plan_dependencies(const q4_chain_phase* in, std::vector<ChainPhase>& out) {
+    const int n = static_cast<int>(out.size());
+    for (int j = 0; j < n; j++) {
+        const uintptr_t lo = reinterpret_cast<uintptr_t>(in[j].x);
+        const uintptr_t hi = lo + static_cast<uintptr_t>(in[j].n_in) * 4u;
+        out[j].x_early = j == 0 || !phase_writes(in[j - 1], lo, hi);
+        bool read_dep = false, write_dep = false;
+        for (int i = 0; i < j; i++) {
+            read_dep = read_dep || phase_writes(in[i], lo, hi);
+            for (int k = 0; k < in[j].count && !write_dep; k++) {
+                const uintptr_t a = reinterpret_cast<uintptr_t>(in[j].out[k]);
+                write_dep = phase_writes(in[i], a, a + static_cast<uintptr_t>(in[j].n_out[k]) * 4u);
+            }
+        }
+        // a read before barrier j-1 needs phase j-2's stores at the latest,
+        // whose arrival is barrier j-1: the arrival after phase j-2
+        if (read_dep) out[out[j].x_early ? j - 2 : j - 1].ack_stores = 1;
+        if (write_dep) out[j - 1].ack_stores = 1;
+    }
+}
+
 }  // namespace
 
 #pragma GCC visibility push(default)
@@ -600,6 +670,7 @@ int q4_chain_create(const q4_chain_phase* phases, int n_phases, q4_chain_plan** 
         }
     }
     if (lds > kStreamLdsMax) return fail(Q4_EARG, "phases need %zu bytes of LDS", lds);
+    plan_dependencies(phases, host);
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(gemv_chain_kernel), kStreamLdsMax, lds_raised))
         return rc;

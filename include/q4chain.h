@@ -6,11 +6,15 @@
  * reference's caller makes one q4_gemv call per projection per token
  * (hetero/cpu_model.py:269-275, :291-292, :367), each one a full round trip.
  * A phase here computes exactly what one q4_gemv_multi_dev (or, with `pair`,
- * q4_gate_up_silu_dev) call of one row computes, bit for bit; phase p reads
- * its x only after every workgroup has finished phase p-1, so a phase may
- * read the outputs of the phases before it.  Within the launch each wave
- * issues the weight loads of the next phase before it waits for that
- * dependency, so the weight stream does not pause at each one.
+ * q4_gate_up_silu_dev) call of one row computes, bit for bit; phase p
+ * stores its outputs only after every workgroup has finished phase p-1, and
+ * reads an x that phase p-1 writes only then, so a phase may read the
+ * outputs of the phases before it.  Within the launch each wave issues the
+ * weight loads of the next phase before it waits for that dependency, so the
+ * weight stream does not pause at each one; an x that phase p-1 does not
+ * write (found from the pointers at q4_chain_create) is loaded and
+ * quantised before the wait too.  A phase's outputs must not overlap its
+ * own x (Q4_EARG).
  *
  * All pointers are device pointers on the device current at q4_chain_create.
  * A plan holds its phase table and barrier state in device memory; it runs
@@ -60,11 +64,12 @@ int q4_chain_run(q4_chain_plan *plan, void *stream);
  * (n_phases + 1) * workgroups * 8 words (workgroups = the device's CU count),
  * later runs record, for each phase p and workgroup b, the 100 MHz clock
  * (s_memrealtime) at stamps[(p * workgroups + b) * 8 + e] for the events
- * e = 1: the workgroup done with phase p - 1 (every wave's stores complete),
- * arriving at the grid barrier; 2: the barrier released; 3: p's x staged in
- * LDS; 4: p's int16 planes ready; 5: wave 0 done with its items of p (row
- * n_phases holds event 1 only: the end).  NULL stops recording.  Returns
- * Q4_EARG when `words` is too small. */
+ * e = 1: the workgroup done with phase p - 1, arriving at the grid barrier
+ * (every wave's stores complete when a later phase depends on them); 2: the
+ * barrier released; 3: p's x staged in LDS; 4: p's int16 planes ready (3 and
+ * 4 come before 2 when phase p - 1 does not write p's x); 5: wave 0 done with
+ * its items of p (row n_phases holds event 1 only: the end).  NULL stops
+ * recording.  Returns Q4_EARG when `words` is too small. */
 int q4_chain_stamps(q4_chain_plan *plan, unsigned long long *stamps, long words);
 
 /* Synchronise the device and return how many barrier waits ran out of time

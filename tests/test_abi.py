@@ -180,7 +180,8 @@ def test_chain_argument_errors(lib):
     def phase(**kw):
         ph = q4.ChainPhase()
         ph.count, ph.pair, ph.n_in, ph.gs, ph.x = 1, 0, 256, 64, fake
-        ph.w[0] = ph.scales[0] = ph.biases[0] = ph.out[0] = fake
+        ph.w[0] = ph.scales[0] = ph.biases[0] = fake
+        ph.out[0] = fake + (1 << 16)                     # apart from x
         ph.n_out[0] = 8
         for k, v in kw.items():
             setattr(ph, k, v)
@@ -205,6 +206,13 @@ def test_chain_argument_errors(lib):
     ph.n_out[1], ph.w[1] = 8, 0
     assert create(ph)[0] == q4.Q4_EARG
     assert create(phase(), phase(n_in=96))[0] == q4.Q4_EARG      # any bad phase
+    rc, plan = create(phase())                           # valid: fails later only without a device
+    assert rc != q4.Q4_EARG
+    if plan.value:
+        lib.q4_chain_destroy(plan)
+    ph = phase()
+    ph.out[0] = fake + 1020                              # the last value of x: the output overlaps it
+    assert create(ph)[0] == q4.Q4_EARG
     assert lib.q4_chain_create(None, 1, ctypes.byref(ctypes.c_void_p())) == q4.Q4_EARG
     assert lib.q4_chain_run(None, None) == q4.Q4_EARG
     assert lib.q4_chain_destroy(None) == 0

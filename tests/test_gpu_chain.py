@@ -121,6 +121,45 @@ def test_phase_shapes_vs_separate_launches(n_in, counts, pair):
     ch.close()
 
 
+def test_mixed_dependencies_vs_launches_in_order():
+    """A program whose barriers order different things: x from outside the
+    program (loaded before the barrier), x written by the phase just before
+    (after it), x written two phases back (before the barrier, so the
+    writer's stores complete one barrier earlier), and an output buffer
+    written again by a later phase.  Every buffer ends bit-identical to the
+    same phases run as separate launches in order, on two runs."""
+    import torch
+    from hetero import sweep
+    n = 1024
+    mats = [mat(1300 + i, n, n)[1] for i in range(7)]
+    x1, x2 = dev(synth.activations(1301, 1, n), synth.activations(1302, 1, n))
+
+    def program():
+        a, b, c, d, e, f = (torch.full((1, n), float("nan"), device="cuda") for _ in range(6))
+        ph = [([mats[0]], x1, [a], False),      # outside x
+              ([mats[1]], x2, [b], False),      # outside x, no dependency on the phase before
+              ([mats[2]], a, [c], False),       # x from two phases back
+              ([mats[3]], c, [d], False),       # x from the phase before
+              ([mats[4]], x1, [a], False),      # writes a again
+              ([mats[5]], a, [e], False),       # reads the new a
+              ([mats[6], mats[0]], d, [f, b], False)]   # x from three back; writes b again
+        return ph, (a, b, c, d, e, f)
+
+    ph, bufs = program()
+    ch = q4.Chain(ph)
+    ref_ph, ref = program()
+    sweep.run_launches(ref_ph, torch.cuda.current_stream())
+    for r in range(2):
+        for t in bufs:
+            t.fill_(float("nan"))
+        ch.run()
+        torch.cuda.synchronize()
+        assert ch.errors() == 0
+        for i, (got, want) in enumerate(zip(bufs, ref)):
+            assert np.array_equal(bits(got), bits(want)), f"run {r} buffer {'abcdef'[i]}"
+    ch.close()
+
+
 def test_graph_replays_and_barrier_reset():
     """A chain captured in a HIP graph: replays with eager work between them
     equal the eager run (the barrier state returns to zero after every
