@@ -21,7 +21,8 @@
 //
 // Memory: outputs are stored, and x is loaded, at device scope (cache policy
 // sc1): a phase's outputs are written on one XCD and read as x on all
-// eight, whose L2s are not coherent with each other.  Before a workgroup
+// eight, whose L2s are not coherent with each other (an x that no phase
+// writes is loaded through the L2, where it stays between phases).  Before a workgroup
 // signals a barrier after which a phase reads (or writes over) what an
 // earlier phase stored, each of its waves has waited for its own stores.
 // x that the phase just before does not write is loaded, and its prologue
@@ -64,7 +65,8 @@ struct ChainPhase {
     int pair;        // gate/up: out[0] = SiLU(W0 x) * (W1 x)
     int n_total;     // rows of the phase: n_out[0] (pair) or the sum of n_out
     int sep_stage;   // x staged for the group sums in LDS of its own (else over the planes)
-    int x_early;     // the phase before does not write x: x and its prologue before the barrier
+    int x_early;     // the phase before does not write x: x and its prologue before the barrier (ring 2)
+    int x_cached;    // no phase writes x: x loaded through the L2
     int ack_stores;  // every wave's stores complete before the arrival at the next barrier
 };
 
@@ -191,7 +193,7 @@ __device__ __forceinline__ void chain_wait(ChainSync* s, unsigned k, int* failed
 // stored at device scope, the rounds of x words are guarded at run time,
 // and the phase ends with the waves' stores complete and the workgroup's
 // arrival at the next barrier.
-template <int RING, bool PAIR>
+template <int RING, bool PAIR, bool EARLY>
 __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
                                             int* failed, uint4* lds4, bool arrive_after,
                                             unsigned long long* stamps, unsigned long long* st) {
@@ -227,23 +229,33 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     const int first_unit = blockIdx.x + wave * grid;
     const bool has_work = first_unit < n_units;                   // uniform
 
-    // ---- 1. x, first when the phase before does not write it (x_early):
+    // ---- 1. x, first when the phase before does not write it (EARLY):
     //         then x does not depend on that phase either, and its loads
     //         and the whole prologue run before the barrier as the weights'
-    //         do.  Device-scope loads, thread t owns words t, t + nt, t + 2nt.
-    const bool early = ph->x_early;                               // uniform
+    //         do.  x loads are the wave's oldest then, so the prologue waits
+    //         for them alone, not for the weights issued after them (a code
+    //         path of its own: one shared with the other order would wait
+    //         for both).  Thread t owns words t, t + nt, t + 2nt; device-scope
+    //         loads unless no phase of the program writes x (x_cached).
     const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(n_in) * 4u);
     float4 wv[kChainRounds][2];
     auto load_x = [&]() {
+        const bool cached = ph->x_cached;                         // uniform
 #pragma unroll
         for (int r = 0; r < kChainRounds; r++) {
             const int j = r * nt + tid;
             const uint32_t off = j < wpr ? static_cast<uint32_t>(8 * j) * 4u : kOutOfRange;
-            wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kStoreDevice));
-            wv[r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, kStoreDevice));
+            if (cached) {
+                wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+                wv[r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+            } else {
+                wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kStoreDevice));
+                wv[r][1] = __builtin_bit_cast(float4,
+                                              __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, kStoreDevice));
+            }
         }
     };
-    if (early) load_x();
+    if constexpr (EARLY) load_x();
 
     // ---- 2. the first ring of this phase: weights only, no dependency
     Item ring[RING];
@@ -259,7 +271,7 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
 
     // ---- 3. otherwise every workgroup must be done with the phase before
     //         (x is one of its outputs) before x is loaded
-    if (!early) {
+    if constexpr (!EARLY) {
         if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
         chain_event(stamps, st, 2);
         load_x();
@@ -330,7 +342,7 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     }
     __syncthreads();
     chain_event(stamps, st, 4);
-    if (early) {
+    if constexpr (EARLY) {
         if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
         chain_event(stamps, st, 2);
     }
@@ -484,19 +496,21 @@ __global__ __launch_bounds__(64 * kChainWaves) void gemv_chain_kernel(const Chai
     CPhase* table = (CPhase*)phases;
     for (int p = 0; p < n_phases; p++) {
         CPhase* ph = table + p;
-        const int pair = ph->pair, ring = ph->ring;               // uniform
+        const int pair = ph->pair, ring = ph->ring, early = ph->x_early;   // uniform
         const bool arrive = p + 1 < n_phases;
         if (pair) {
-            if (ring == 4) chain_phase<4, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
-            else chain_phase<2, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            if (ring == 4) chain_phase<4, true, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            else if (early) chain_phase<2, true, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            else chain_phase<2, true, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 1) {
-            chain_phase<1, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            chain_phase<1, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 2) {
-            chain_phase<2, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            if (early) chain_phase<2, false, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            else chain_phase<2, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 4) {
-            chain_phase<4, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            chain_phase<4, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         } else {
-            chain_phase<5, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            chain_phase<5, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
         }
     }
     // every workgroup is past its last barrier wait once it gets here; the
@@ -613,7 +627,10 @@ int plan_phase(const q4_chain_phase& in, ChainPhase& out, int cus, size_t& lds) 
 // What each barrier must order, from the buffers the phases read and write:
 //  - x_early[j]: phase j-1 writes no byte of x_j, so x_j may be loaded (and
 //    its prologue run) before barrier j; every phase before j-1 is past
-//    barrier j-1 by then.
+//    barrier j-1 by then.  Only the ring-2 phases have that code path; the
+//    others load x after the barrier, which orders at least as much.
+//  - x_cached[j]: no phase writes x_j, so the L2 of any XCD holds no stale
+//    copy of it (the launch starts with the L2s coherent).
 //  - ack_stores[b-1]: the waves wait for their stores before arriving at
 //    barrier b when a read or a write after b must see them: x_j written by
 //    an earlier phase is read after barrier j (j-1 when early), and a phase
@@ -623,8 +640,11 @@ void plan_dependencies(const q4_chain_phase* in, std::vector<ChainPhase>& out) {
     for (int j = 0; j < n; j++) {
         const uintptr_t lo = reinterpret_cast<uintptr_t>(in[j].x);
         const uintptr_t hi = lo + static_cast<uintptr_t>(in[j].n_in) * 4u;
-        out[j].x_early = j == 0 || !phase_writes(in[j - 1], lo, hi);
+        out[j].x_early = out[j].ring == 2 && (j == 0 || !phase_writes(in[j - 1], lo, hi));
         bool read_dep = false, write_dep = false;
+        out[j].x_cached = 1;
+        for (int i = 0; i < n && out[j].x_cached; i++)
+            if (phase_writes(in[i], lo, hi)) out[j].x_cached = 0;
         for (int i = 0; i < j; i++) {
             read_dep = read_dep || phase_writes(in[i], lo, hi);
             for (int k = 0; k < in[j].count && !write_dep; k++) {
