@@ -204,7 +204,11 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     const int wpr = n_in >> 3, G = n_in >> 6;
     const int C = (wpr + kChunkWords - 1) / kChunkWords;
     const int Gr = (G + 3) & ~3;
-    const int tid = threadIdx.x, nt = blockDim.x;
+    // the launch shape is fixed: blockDim.x would be a 16-bit load from the
+    // dispatch packet, a vector-memory round trip (and a wait for every
+    // store still in flight) at the start of every phase
+    constexpr int nt = 64 * kChainWaves;
+    const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nwaves = nt >> 6;
