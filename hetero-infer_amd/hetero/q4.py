@@ -185,6 +185,68 @@ def _ptr(t) -> int:
     return t.data_ptr()
 
 
+# The entry points take raw device pointers and sizes, so nothing below the
+# wrappers can tell a buffer of the wrong type or size: the wrappers check
+# every tensor they pass (a too-small buffer would be read or written past
+# its end by a kernel) and raise before any library call.
+
+def _need(t, name, dtypes, numel=None, shape=None):
+    import torch
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: a torch tensor, got {type(t).__name__}")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {' or '.join(str(d) for d in dtypes)}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name}: {t.numel()} elements, expected {numel}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: not contiguous")
+    return t
+
+
+def _gpu(*ts):
+    """Every tensor given (None skipped) on one GPU; after the type and size
+    checks, so that those report first."""
+    ts = [t for t in ts if t is not None]
+    for t in ts:
+        if t.device.type != "cuda":
+            raise ValueError(f"a tensor on {t.device}: the library takes GPU tensors")
+    if len({t.device for t in ts}) > 1:
+        raise ValueError("tensors on more than one GPU")
+
+
+def _f32():
+    import torch
+    return (torch.float32,)
+
+
+def _mat(mat, name="w"):
+    """(n_out, n_in, gs) of a (w, scales, biases) triple: int32 words
+    [n_out, n_in / 8], 16-bit scales and biases [n_out, n_in / gs]."""
+    import torch
+    w, sc, b = mat
+    if w.dim() != 2 or sc.dim() != 2:
+        raise ValueError(f"{name}: w and scales are 2-D")
+    n_out, n_in = w.shape[0], w.shape[1] * 8
+    if sc.shape[1] == 0 or n_in % sc.shape[1]:
+        raise ValueError(f"{name}: {sc.shape[1]} scale groups do not divide n_in {n_in}")
+    gs = n_in // sc.shape[1]
+    _need(w, name, (torch.int32, torch.uint32))
+    for t, k in ((sc, "scales"), (b, "biases")):
+        _need(t, f"{name} {k}", (torch.int16, torch.float16), shape=(n_out, n_in // gs))
+    return n_out, n_in, gs
+
+
+def _same_in(mats, name="mats"):
+    dims = [_mat(m, f"{name}[{i}]") for i, m in enumerate(mats)]
+    if not dims:
+        raise ValueError(f"{name}: no matrices")
+    if any(d[1:] != dims[0][1:] for d in dims):
+        raise ValueError(f"{name}: the matrices differ in n_in or group size")
+    return dims
+
+
 def _ptr_or_null(t):
     return None if t is None else _ptr(t)
 
@@ -198,13 +260,13 @@ def _stream(stream=None) -> int:
 def gemv_dev(w, scales, biases, x, out=None, stream=None, lib=None):
     """out[m, n_out] = x[m, n_in] @ W^T on the GPU (torch tensors on one device)."""
     import torch
-    lib = lib or load()
-    n_out, n_in = w.shape[0], w.shape[1] * 8
-    gs = n_in // scales.shape[1]
-    x2 = x.reshape(-1, n_in)
-    assert x2.dtype == torch.float32 and x2.is_contiguous()
+    n_out, n_in, gs = _mat((w, scales, biases))
+    x2 = _need(x, "x", _f32()).reshape(-1, n_in)
     if out is None:
         out = torch.empty((x2.shape[0], n_out), dtype=torch.float32, device=x.device)
+    _need(out, "out", _f32(), numel=x2.shape[0] * n_out)
+    _gpu(w, scales, biases, x2, out)
+    lib = lib or load()
     rc = lib.q4_gemv_dev(_ptr(w), _ptr(scales), _ptr(biases), _ptr(x2), _ptr(out),
                          x2.shape[0], n_out, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gemv_dev")
@@ -214,14 +276,17 @@ def gemv_dev(w, scales, biases, x, out=None, stream=None, lib=None):
 def gemv_multi_dev(mats, x, outs=None, stream=None, lib=None):
     """Several (w, scales, biases) sharing x in one launch; returns the outputs."""
     import torch
-    lib = lib or load()
-    n_in = mats[0][0].shape[1] * 8
-    gs = n_in // mats[0][1].shape[1]
-    x2 = x.reshape(-1, n_in)
+    dims = _same_in(mats)
+    n_in, gs = dims[0][1], dims[0][2]
+    x2 = _need(x, "x", _f32()).reshape(-1, n_in)
     m = x2.shape[0]
     if outs is None:
-        outs = [torch.empty((m, w.shape[0]), dtype=torch.float32, device=x.device) for w, _, _ in mats]
+        outs = [torch.empty((m, d[0]), dtype=torch.float32, device=x.device) for d in dims]
+    for i, (o, d) in enumerate(zip(outs, dims)):
+        _need(o, f"outs[{i}]", _f32(), numel=m * d[0])
     k = len(mats)
+    _gpu(x2, *outs, *(t for m in mats for t in m))
+    lib = lib or load()
     arr = lambda vals: (ctypes.c_void_p * k)(*vals)
     rc = lib.q4_gemv_multi_dev(k, arr([_ptr(a[0]) for a in mats]), arr([_ptr(a[1]) for a in mats]),
                                arr([_ptr(a[2]) for a in mats]), arr([_ptr(o) for o in outs]),
@@ -231,16 +296,30 @@ def gemv_multi_dev(mats, x, outs=None, stream=None, lib=None):
     return outs
 
 
+def _norm_args(n_in, x, delta, norm_w, x_out):
+    """One row of x, delta (optional), norm weights and x_out (optional), fp32."""
+    _need(x, "x", _f32(), numel=n_in)
+    _need(norm_w, "norm_w", _f32(), numel=n_in)
+    if delta is not None:
+        _need(delta, "delta", _f32(), numel=n_in)
+    if x_out is not None:
+        _need(x_out, "x_out", _f32(), numel=n_in)
+
+
 def norm_gemv_multi_dev(mats, x, delta, norm_w, eps, x_out=None, outs=None, stream=None, lib=None):
     """gemv_multi_dev of rmsnorm(x + delta) * norm_w (one row), the norm in
     the GEMV prologue; x_out (if given, with delta) receives x + delta."""
     import torch
-    lib = lib or load()
-    n_in = mats[0][0].shape[1] * 8
-    gs = n_in // mats[0][1].shape[1]
+    dims = _same_in(mats)
+    n_in, gs = dims[0][1], dims[0][2]
+    _norm_args(n_in, x, delta, norm_w, x_out)
     if outs is None:
-        outs = [torch.empty((1, w.shape[0]), dtype=torch.float32, device=x.device) for w, _, _ in mats]
+        outs = [torch.empty((1, d[0]), dtype=torch.float32, device=x.device) for d in dims]
+    for i, (o, d) in enumerate(zip(outs, dims)):
+        _need(o, f"outs[{i}]", _f32(), numel=d[0])
     k = len(mats)
+    _gpu(x, delta, norm_w, x_out, *outs, *(t for m in mats for t in m))
+    lib = lib or load()
     arr = lambda vals: (ctypes.c_void_p * k)(*vals)
     rc = lib.q4_norm_gemv_multi_dev(k, arr([_ptr(a[0]) for a in mats]), arr([_ptr(a[1]) for a in mats]),
                                     arr([_ptr(a[2]) for a in mats]), arr([_ptr(o) for o in outs]),
@@ -257,12 +336,18 @@ def norm_gemv_argmax_dev(mat, x, delta, norm_w, eps, tok, pos, hist=None, s0=0, 
     of the logits (NumPy's rule), hist[*pos - s0] = *tok when in range, *pos
     += 1 -- all in the GEMV's launch.  Returns the logits."""
     import torch
-    lib = lib or load()
     w, s, b = mat
-    n_out, n_in = w.shape[0], w.shape[1] * 8
-    gs = n_in // s.shape[1]
+    n_out, n_in, gs = _mat(mat)
+    _norm_args(n_in, x, delta, norm_w, x_out)
     if logits is None:
         logits = torch.empty((1, n_out), dtype=torch.float32, device=x.device)
+    _need(logits, "logits", _f32(), numel=n_out)
+    _need(tok, "tok", (torch.int64,), numel=1)
+    _need(pos, "pos", (torch.int64,), numel=1)
+    if hist is not None:
+        _need(hist, "hist", (torch.int64,))
+    _gpu(w, s, b, x, delta, norm_w, x_out, logits, tok, pos, hist)
+    lib = lib or load()
     rc = lib.q4_norm_gemv_argmax_dev(_ptr(w), _ptr(s), _ptr(b), _ptr(logits), n_out, _ptr(x), _ptr_or_null(delta),
                                      _ptr(norm_w), eps, _ptr_or_null(x_out), n_in, gs, _ptr(tok), _ptr_or_null(hist),
                                      _ptr(pos), s0, 0 if hist is None else hist.numel(), _stream(stream))
@@ -270,15 +355,25 @@ def norm_gemv_argmax_dev(mat, x, delta, norm_w, eps, tok, pos, hist=None, s0=0, 
     return logits
 
 
+def _pair(gate, up):
+    """(n_inter, n_in, gs) of a gate/up pair of equal shapes."""
+    d = _mat(gate, "gate")
+    if _mat(up, "up") != d:
+        raise ValueError("gate and up differ in shape or group size")
+    return d
+
+
 def norm_gate_up_silu_dev(gate, up, x, delta, norm_w, eps, x_out=None, h=None, stream=None, lib=None):
     """gate_up_silu_dev of rmsnorm(x + delta) * norm_w (one row), the norm in
     the GEMV prologue; x_out (if given, with delta) receives x + delta."""
     import torch
-    lib = lib or load()
-    n_inter, n_in = gate[0].shape[0], gate[0].shape[1] * 8
-    gs = n_in // gate[1].shape[1]
+    n_inter, n_in, gs = _pair(gate, up)
+    _norm_args(n_in, x, delta, norm_w, x_out)
     if h is None:
         h = torch.empty((1, n_inter), dtype=torch.float32, device=x.device)
+    _need(h, "h", _f32(), numel=n_inter)
+    _gpu(*gate, *up, x, delta, norm_w, x_out, h)
+    lib = lib or load()
     rc = lib.q4_norm_gate_up_silu_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), _ptr(x),
                                       _ptr_or_null(delta), _ptr(norm_w), eps, _ptr_or_null(x_out), _ptr(h),
                                       n_inter, n_in, gs, _stream(stream))
@@ -289,12 +384,13 @@ def norm_gate_up_silu_dev(gate, up, x, delta, norm_w, eps, x_out=None, h=None, s
 def gate_up_silu_dev(gate, up, x, h=None, stream=None, lib=None):
     """h[m, n_inter] = SiLU(x @ gate^T) * (x @ up^T); gate/up = (w, scales, biases)."""
     import torch
-    lib = lib or load()
-    n_inter, n_in = gate[0].shape[0], gate[0].shape[1] * 8
-    gs = n_in // gate[1].shape[1]
-    x2 = x.reshape(-1, n_in)
+    n_inter, n_in, gs = _pair(gate, up)
+    x2 = _need(x, "x", _f32()).reshape(-1, n_in)
     if h is None:
         h = torch.empty((x2.shape[0], n_inter), dtype=torch.float32, device=x.device)
+    _need(h, "h", _f32(), numel=x2.shape[0] * n_inter)
+    _gpu(*gate, *up, x2, h)
+    lib = lib or load()
     rc = lib.q4_gate_up_silu_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), _ptr(x2), _ptr(h),
                                  x2.shape[0], n_inter, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gate_up_silu_dev")
@@ -304,15 +400,19 @@ def gate_up_silu_dev(gate, up, x, h=None, stream=None, lib=None):
 def mlp_dev(gate, up, down, x, h=None, out=None, stream=None, lib=None):
     """down(SiLU(gate(x)) * up(x)) for 4-bit (w, scales, biases) triples."""
     import torch
-    lib = lib or load()
-    n_inter, n_hidden = gate[0].shape[0], gate[0].shape[1] * 8
-    gs = n_hidden // gate[1].shape[1]
-    x2 = x.reshape(-1, n_hidden)
+    n_inter, n_hidden, gs = _pair(gate, up)
+    if _mat(down, "down") != (n_hidden, n_inter, gs):
+        raise ValueError("down must map n_inter back to n_hidden with the same group size")
+    x2 = _need(x, "x", _f32()).reshape(-1, n_hidden)
     m = x2.shape[0]
     if h is None:
         h = torch.empty((m, n_inter), dtype=torch.float32, device=x.device)
     if out is None:
         out = torch.empty((m, n_hidden), dtype=torch.float32, device=x.device)
+    _need(h, "h", _f32(), numel=m * n_inter)
+    _need(out, "out", _f32(), numel=m * n_hidden)
+    _gpu(*gate, *up, *down, x2, h, out)
+    lib = lib or load()
     rc = lib.q4_mlp_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), *(_ptr(t) for t in down),
                         _ptr(x2), _ptr(h), _ptr(out), m, n_hidden, n_inter, gs, _stream(stream))
     check(lib, rc, "q4_mlp_dev")
@@ -322,12 +422,13 @@ def mlp_dev(gate, up, down, x, h=None, out=None, stream=None, lib=None):
 def gemm_bf16_dev(w, scales, biases, x, out=None, stream=None, lib=None):
     """Prefill: out[m, n_out] = bf16(x) @ bf16(dequant(W))^T with fp32 accumulation."""
     import torch
-    lib = lib or load()
-    n_out, n_in = w.shape[0], w.shape[1] * 8
-    gs = n_in // scales.shape[1]
-    x2 = x.reshape(-1, n_in)
+    n_out, n_in, gs = _mat((w, scales, biases))
+    x2 = _need(x, "x", _f32()).reshape(-1, n_in)             # rounded to bf16 by the call
     if out is None:
         out = torch.empty((x2.shape[0], n_out), dtype=torch.float32, device=x.device)
+    _need(out, "out", _f32(), numel=x2.shape[0] * n_out)
+    _gpu(w, scales, biases, x2, out)
+    lib = lib or load()
     rc = lib.q4_gemm_bf16_dev(_ptr(w), _ptr(scales), _ptr(biases), _ptr(x2), _ptr(out),
                               x2.shape[0], n_out, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gemm_bf16_dev")
@@ -338,14 +439,17 @@ def gemm_bf16_multi_dev(mats, x, outs=None, stream=None, lib=None):
     """Prefill for several (w, scales, biases) sharing x in one launch; returns
     the outputs.  x in fp32 (rounded to bf16 by the call) or already bf16."""
     import torch
-    lib = lib or load()
-    n_in = mats[0][0].shape[1] * 8
-    gs = n_in // mats[0][1].shape[1]
-    x2 = x.reshape(-1, n_in)
+    dims = _same_in(mats)
+    n_in, gs = dims[0][1], dims[0][2]
+    x2 = _need(x, "x", (torch.float32, torch.bfloat16)).reshape(-1, n_in)
     m = x2.shape[0]
     if outs is None:
-        outs = [torch.empty((m, w.shape[0]), dtype=torch.float32, device=x.device) for w, _, _ in mats]
+        outs = [torch.empty((m, d[0]), dtype=torch.float32, device=x.device) for d in dims]
+    for i, (o, d) in enumerate(zip(outs, dims)):
+        _need(o, f"outs[{i}]", _f32(), numel=m * d[0])
     k = len(mats)
+    _gpu(x2, *outs, *(t for m in mats for t in m))
+    lib = lib or load()
     arr = lambda vals: (ctypes.c_void_p * k)(*vals)
     fn = lib.q4_gemm_bf16in_multi_dev if x2.dtype == torch.bfloat16 else lib.q4_gemm_bf16_multi_dev
     rc = fn(k, arr([_ptr(a[0]) for a in mats]), arr([_ptr(a[1]) for a in mats]),
@@ -360,14 +464,13 @@ def gemm_bf16_gate_up_silu_dev(gate, up, xb, h=None, stream=None, lib=None):
     """Prefill MLP activations from bf16 x: h[m, n_inter] = bf16(SiLU(x @
     gate^T) * (x @ up^T)), the down projection's bf16 operand."""
     import torch
-    lib = lib or load()
-    n_inter, n_in = gate[0].shape[0], gate[0].shape[1] * 8
-    gs = n_in // gate[1].shape[1]
-    x2 = xb.reshape(-1, n_in)
-    if x2.dtype != torch.bfloat16:
-        raise TypeError("gemm_bf16_gate_up_silu_dev takes x in bf16")
+    n_inter, n_in, gs = _pair(gate, up)
+    x2 = _need(xb, "x", (torch.bfloat16,)).reshape(-1, n_in)
     if h is None:
         h = torch.empty((x2.shape[0], n_inter), dtype=torch.bfloat16, device=xb.device)
+    _need(h, "h", (torch.bfloat16,), numel=x2.shape[0] * n_inter)
+    _gpu(*gate, *up, x2, h)
+    lib = lib or load()
     rc = lib.q4_gemm_bf16in_gate_up_silu_dev(*(_ptr(t) for t in gate), *(_ptr(t) for t in up), _ptr(x2), _ptr(h),
                                              x2.shape[0], n_inter, n_in, gs, _stream(stream))
     check(lib, rc, "q4_gemm_bf16in_gate_up_silu_dev")
@@ -396,14 +499,15 @@ def prefill_errors(stream=None, lib=None) -> int:
 
 def dequant_dev(w, scales, biases, row0=0, row1=None, out=None, bf16=False, stream=None, lib=None):
     import torch
-    lib = lib or load()
-    n_in = w.shape[1] * 8
-    gs = n_in // scales.shape[1]
-    row1 = w.shape[0] if row1 is None else row1
+    n_out, n_in, gs = _mat((w, scales, biases))
+    row1 = n_out if row1 is None else row1
     rows = max(row1 - row0, 0)
+    odt = torch.bfloat16 if bf16 else torch.float32
     if out is None:
-        out = torch.empty((rows, n_in), dtype=torch.bfloat16 if bf16 else torch.float32,
-                          device=w.device)
+        out = torch.empty((rows, n_in), dtype=odt, device=w.device)
+    _need(out, "out", (odt,), numel=rows * n_in)
+    _gpu(w, scales, biases, out)
+    lib = lib or load()
     fn = lib.q4_dequant_bf16_dev if bf16 else lib.q4_dequant_dev
     rc = fn(_ptr(w), _ptr(scales), _ptr(biases), _ptr(out), row0, row1, n_in, gs, _stream(stream))
     check(lib, rc, "q4_dequant_dev")
@@ -423,9 +527,17 @@ class Chain:
         table = (ChainPhase * len(phases))()
         for i, (mats, x, outs, pair) in enumerate(phases):
             ph = table[i]
-            n_in = mats[0][0].shape[1] * 8
+            dims = _same_in(mats, f"phase {i}")
+            n_in = dims[0][1]
+            _need(x, f"phase {i} x", _f32(), numel=n_in)
+            n_outs = [dims[0][0]] if pair else [d[0] for d in dims]
+            if len(outs) < len(n_outs):
+                raise ValueError(f"phase {i}: {len(outs)} outputs for {len(n_outs)}")
+            for k, n in enumerate(n_outs):
+                _need(outs[k], f"phase {i} outs[{k}]", _f32(), numel=n)
+            _gpu(x, *outs[:len(n_outs)], *(t for m in mats for t in m))
             ph.count, ph.pair = len(mats), int(bool(pair))
-            ph.n_in, ph.gs = n_in, n_in // mats[0][1].shape[1]
+            ph.n_in, ph.gs = n_in, dims[0][2]
             ph.x = _ptr(x)
             for k, (w, sc, b) in enumerate(mats):
                 ph.w[k], ph.scales[k], ph.biases[k] = _ptr(w), _ptr(sc), _ptr(b)
@@ -468,8 +580,15 @@ class Chain:
 
 def gemv_host(lib, w: np.ndarray, scales: np.ndarray, biases: np.ndarray, x: np.ndarray,
               gs: int, nthreads: int = 0) -> np.ndarray:
+    if w.ndim != 2 or w.dtype not in (np.uint32, np.int32) or not w.flags.c_contiguous:
+        raise TypeError("w: C-contiguous [n_out, n_in / 8] uint32")
     n_out, n_in = w.shape[0], w.shape[1] * 8
+    for a, k in ((scales, "scales"), (biases, "biases")):
+        if a.dtype.itemsize != 2 or a.size != n_out * (n_in // gs) or not a.flags.c_contiguous:
+            raise TypeError(f"{k}: C-contiguous [n_out, n_in / gs] of 16-bit values")
     xc = np.ascontiguousarray(x, dtype=np.float32)
+    if xc.size != n_in:
+        raise ValueError(f"x: {xc.size} values, expected {n_in}")
     out = np.empty(n_out, dtype=np.float32)
     rc = lib.q4_gemv(w.ctypes.data, scales.ctypes.data, biases.ctypes.data, xc.ctypes.data,
                      out.ctypes.data, n_out, n_in, gs, nthreads)
