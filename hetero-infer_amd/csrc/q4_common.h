@@ -250,6 +250,13 @@ struct GreedyArgs {
 // host side, defined in q4gemv.hip
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int num_cus();
+// Arrays of the library in device memory that a launch uses as its own
+// (the greedy token's parts and counter, argmax's parts) come in
+// kStreamSlots sets per GPU, one per stream: the kStreamSlots streams that
+// used them most recently on a device each hold a set, so calls on
+// different streams never share one (calls on one stream are ordered by it).
+constexpr int kStreamSlots = 16;
+int stream_slot(hipStream_t st, int* slot);
 
 // The matrices of one prefill launch (q4_gemm.hip), up to 4 sharing x:
 // matrix k's 256-column blocks are blocks nb0[k] .. nb0[k+1] - 1 of the

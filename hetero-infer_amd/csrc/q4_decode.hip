@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float2* __restr
 }
 
 // The argmax partials: a fixed array in device memory, one per GPU.
-static __device__ __align__(256) float2 argmax_scratch[kArgmaxParts];
+static __device__ __align__(256) float2 argmax_scratch[kStreamSlots * kArgmaxParts];   // a set per stream slot
 
 // Threads of an add_rmsnorm_kernel workgroup: a word (8 values) each, whole
 // waves (the sum's order does not depend on the count: threads past the
@@ -532,6 +532,9 @@ int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64
         }
         sp = scr[dev];
     }
+    int slot = 0;
+    if (int rc = stream_slot(static_cast<hipStream_t>(stream), &slot)) return rc;
+    sp = static_cast<float2*>(sp) + static_cast<size_t>(slot) * kArgmaxParts;
     const int n4 = n >> 2;
     // at least 1024 float4s per workgroup, at most kArgmaxParts workgroups
     int parts = (n4 + 1023) / 1024;

@@ -71,6 +71,45 @@ int num_cus() {
     return cus[dev];
 }
 
+// The stream slots of each device: the stream holding each slot and when it
+// last used it; a stream new to the table takes a free slot, else the
+// least recently used one.
+struct SlotTable {
+    hipStream_t stream[kStreamSlots] = {};
+    uint64_t used[kStreamSlots] = {};
+    bool taken[kStreamSlots] = {};
+    uint64_t tick = 0;
+};
+std::mutex g_slot_mu;
+std::map<int, SlotTable> g_slots;
+
+int stream_slot(hipStream_t st, int* slot) {
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(Q4_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_slot_mu);
+    SlotTable& t = g_slots[dev];
+    int pick = -1;
+    for (int i = 0; i < kStreamSlots && pick < 0; i++)
+        if (t.taken[i] && t.stream[i] == st) pick = i;
+    if (pick < 0) {
+        int free_i = -1, lru = -1;
+        for (int i = 0; i < kStreamSlots; i++) {
+            if (!t.taken[i]) {
+                if (free_i < 0) free_i = i;
+            } else if (lru < 0 || t.used[i] < t.used[lru]) {
+                lru = i;
+            }
+        }
+        pick = free_i >= 0 ? free_i : lru;
+        t.taken[pick] = true;
+        t.stream[pick] = st;
+    }
+    t.used[pick] = ++t.tick;
+    *slot = pick;
+    return 0;
+}
+
 // The streaming kernel's instances are compiled in q4_stream_inst.hip
 // (a build with -DQ4_SINGLE_TU instantiates them here instead).
 #ifndef Q4_SINGLE_TU
@@ -924,6 +963,7 @@ int current_device(int* dev) {
     return 0;
 }
 
+
 int dev_state(DevState** out) {
     int dev;
     int rc = current_device(&dev);
@@ -1130,11 +1170,10 @@ std::mutex g_scr_mu;
 void* g_scr_ptr[64] = {};
 
 // q4_norm_gemv_argmax_dev's per-workgroup (value, index) parts and arrival
-// counter: fixed arrays in device memory, one per GPU (zero at load; the
-// last workgroup of each launch sets the counter back to zero), so calls
-// that overlap in time on one GPU race.
-static __device__ __align__(256) float2 greedy_part[kGreedyMaxParts];
-static __device__ __align__(256) unsigned greedy_count[64];   // one counter ([0]) on a 256-byte line of its own
+// counter: fixed arrays in device memory, kStreamSlots sets per GPU (zero at
+// load; the last workgroup of each launch sets its counter back to zero).
+static __device__ __align__(256) float2 greedy_part[kStreamSlots * kGreedyMaxParts];
+static __device__ __align__(256) unsigned greedy_count[kStreamSlots * 64];   // counter [64 s]: a 256-byte line each
 std::mutex g_greedy_mu;
 void* g_greedy_part[64] = {};
 void* g_greedy_count[64] = {};
@@ -1576,6 +1615,10 @@ int q4_norm_gemv_argmax_dev(const uint32_t* w, const uint16_t* scales, const uin
         part = g_greedy_part[dev];
         count = g_greedy_count[dev];
     }
+    int slot = 0;
+    if ((rc = stream_slot(static_cast<hipStream_t>(stream), &slot))) return rc;
+    part = static_cast<float2*>(part) + static_cast<size_t>(slot) * kGreedyMaxParts;
+    count = static_cast<unsigned*>(count) + static_cast<size_t>(slot) * 64;
     MatList ml{};
     for (int k = 0; k < kMaxMats; k++) {
         ml.w[k] = w; ml.s[k] = scales; ml.b[k] = biases; ml.out[k] = logits;

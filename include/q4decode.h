@@ -163,9 +163,12 @@ int q4_attention_rope_dev(const float* q, const float* k, const float* v, const 
  * *tok, hist and *pos exactly as q4_argmax_dev(logits, n_out, ...) sets them
  * (hetero/backends.py:106-109).  Each workgroup reduces the rows it stored
  * and the last one to finish reduces those parts, through fixed arrays of
- * the library in device memory (one per GPU): calls that overlap in time on
- * one GPU, with each other or with another launch of this entry point,
- * race.  The same arguments as q4_norm_gemv_multi_dev with count 1, plus
+ * the library in device memory: 16 sets per GPU, one for each of the 16
+ * streams that called it most recently on that GPU, so calls on different
+ * streams do not share them (a call captured in a graph keeps the set of
+ * the stream it was captured on; 17 or more streams calling it at once, or
+ * such a graph replayed beside the stream's own calls, share sets and
+ * race).  The same arguments as q4_norm_gemv_multi_dev with count 1, plus
  * q4_argmax_dev's. */
 int q4_norm_gemv_argmax_dev(const uint32_t* w, const uint16_t* scales, const uint16_t* biases, float* logits,
                             int n_out, const float* x, const float* delta, const float* norm_w, float eps,
@@ -177,8 +180,8 @@ int q4_norm_gemv_argmax_dev(const uint32_t* w, const uint16_t* scales, const uin
  * one, else the first index of the maximum) and the step's bookkeeping:
  * *tok = argmax, hist[*pos - s0] = *tok when that index is in [0, hist_len),
  * *pos += 1.  Two launches; the per-slice maxima go through a fixed array
- * of the library in device memory (one per GPU), so argmax calls that
- * overlap in time on one GPU race. */
+ * of the library in device memory, one set per stream as for
+ * q4_norm_gemv_argmax_dev. */
 int q4_argmax_dev(const float* logits, int n, int64_t* tok, int64_t* hist, int64_t* pos, int64_t s0,
                   int hist_len, void* stream);
 

@@ -166,3 +166,38 @@ def test_norm_gemv_argmax_matches_two_launches(n_in, n_out):
     tok, hist, pos = fused(mat, calls=3)[1:]
     torch.cuda.synchronize()
     assert int(pos.item()) == 14 and hist.cpu().tolist() == [-1, a, a, a]
+
+
+def test_greedy_and_argmax_on_two_streams():
+    """Calls on two streams at once use arrays of their own (a set per
+    stream): each stream's greedy token (q4_norm_gemv_argmax_dev, the Qwen
+    vocabulary) and argmax (q4_argmax_dev) equal the same call alone, over
+    rounds in which the two streams' launches overlap."""
+    import torch
+    lib = q4.load()
+    n_in, n_out = 3584, 152064
+    rng = np.random.default_rng(5)
+    _, mat = mats(901, n_out, n_in)
+    xs = [tensors(rng.normal(0, 1, n_in).astype(np.float32), rng.normal(1, 0.2, n_in).astype(np.float32))
+          for _ in range(2)]
+    logits = [torch.from_numpy(rng.normal(0, 1, 200003).astype(np.float32)).cuda() for _ in range(2)]
+    want_g = [int(torch.argmax(q4.norm_gemv_multi_dev([mat], x, None, nw, EPS, lib=lib)[0]).item()) for x, nw in xs]
+    want_a = [int(torch.argmax(lg).item()) for lg in logits]
+    assert want_g[0] != want_g[1] and want_a[0] != want_a[1]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for rnd in range(8):
+        toks = [torch.zeros(2, dtype=torch.int64, device="cuda") for _ in range(2)]
+        poss = [torch.zeros(2, dtype=torch.int64, device="cuda") for _ in range(2)]
+        torch.cuda.synchronize()                        # the fills above ran on the default stream
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                x, nw = xs[i]
+                q4.norm_gemv_argmax_dev(mat, x, None, nw, EPS, toks[i][:1], poss[i][:1], stream=streams[i], lib=lib)
+                rc = lib.q4_argmax_dev(logits[i].data_ptr(), logits[i].numel(), toks[i][1:].data_ptr(), None,
+                                       poss[i][1:].data_ptr(), 0, 0, streams[i].cuda_stream)
+                assert rc == 0, q4.last_error(lib)
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert toks[i].cpu().tolist() == [want_g[i], want_a[i]], (rnd, i)
+            assert poss[i].cpu().tolist() == [1, 1], (rnd, i)
