@@ -238,25 +238,56 @@ __device__ __forceinline__ void w4_segment(W4Acc<BM, NW>& acc, char* lds, const 
             sf[j] = h2f(static_cast<uint16_t>(Ss[row]));
             bf[j] = h2f(static_cast<uint16_t>(Ts[row]));
         }
+        // four K slices of 16; slice ks + 1's operands are read while slice
+        // ks multiplies, and its dequant is spread over the last of slice
+        // ks's MFMAs (fences pin the order), so the VALU work runs under the
+        // matrix core instead of before it
+        constexpr int NM = TM * TN, NPC = TN * 4;                  // MFMAs, dequant pieces per slice
+        auto a_frag = [&](int ks, int i) {
+            const int row = wm * RW + i * 32 + (lane & 31);
+            const int c = (2 * ks + hb) ^ (row & 7);
+            return *reinterpret_cast<const gemm_bf16x8*>(As + row * 64 + c * 8);
+        };
+        auto b_word = [&](int ks, int j) { return Bs[w4_brow<PAIR, WC>(wn, j, lane) * 8 + 2 * ks + hb]; };
+        gemm_bf16x8 av[2][TM], bv[2][TN];
+        uint32_t bw[TN], blo[TN], bhi[TN], pk[TN][4];
+#pragma unroll
+        for (int j = 0; j < TN; j++) bv[0][j] = w4_dequant8(b_word(0, j), sf[j], bf[j]);
+#pragma unroll
+        for (int i = 0; i < TM; i++) av[0][i] = a_frag(0, i);
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            gemm_bf16x8 av[TM], bv[TN];
+            const int cu = ks & 1, nx = cu ^ 1;
+            if (ks < 3) {
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int row = w4_brow<PAIR, WC>(wn, j, lane);
-                bv[j] = w4_dequant8(Bs[row * 8 + 2 * ks + hb], sf[j], bf[j]);
+                for (int j = 0; j < TN; j++) bw[j] = b_word(ks + 1, j);
+#pragma unroll
+                for (int i = 0; i < TM; i++) av[nx][i] = a_frag(ks + 1, i);
             }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int row = wm * RW + i * 32 + (lane & 31);
-                const int c = (2 * ks + hb) ^ (row & 7);
-                av[i] = *reinterpret_cast<const gemm_bf16x8*>(As + row * 64 + c * 8);
+            for (int m = 0; m < NM; m++) {
+                const int i = m / TN, j = m % TN;
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[cu][i], bv[cu][j], acc[i][j], 0, 0, 0);
+                if (ks < 3) {
+                    constexpr int M0 = NPC < NM ? NM - NPC : 0, NR = NM - M0;   // pieces in the last NR MFMAs
+#pragma unroll
+                    for (int pc = m < M0 ? 0 : (m - M0) * NPC / NR; pc < (m < M0 ? 0 : (m - M0 + 1) * NPC / NR); pc++) {
+                        const int jj = pc / 4, q = pc % 4;
+                        if (q == 0) {
+                            blo[jj] = bw[jj] & 0x0F0F0F0Fu;          // even / odd elements, a byte each
+                            bhi[jj] = (bw[jj] >> 4) & 0x0F0F0F0Fu;
+                        }
+                        pk[jj][q] = w4_pack_bf16(
+                            __builtin_fmaf(static_cast<float>((blo[jj] >> (8 * q)) & 0xFFu), sf[jj], bf[jj]),
+                            __builtin_fmaf(static_cast<float>((bhi[jj] >> (8 * q)) & 0xFFu), sf[jj], bf[jj]));
+                        if (q == 3)
+                            bv[nx][jj] = __builtin_bit_cast(gemm_bf16x8,
+                                                            make_uint4(pk[jj][0], pk[jj][1], pk[jj][2], pk[jj][3]));
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
         }
     }
     // the last copies issued (past the segment) read nothing; wait for them,
