@@ -810,7 +810,9 @@ def chain_stamp_table(torch, chain, n_phases, dev, stream, reps=3):
     wave's items and stores -- and the latency from the last workgroup's
     arrival to the first one's release.  Where the phase before does not
     write x, x is loaded and staged from the workgroup's arrival on, before
-    the release; the items start at the later of release and planes."""
+    the release; the items start at the later of release and planes.  An x
+    prepared at the program's start is staged when its planes, group sums
+    and scale are copied into LDS (planes then follow at once)."""
     import numpy as np
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     buf = torch.zeros((n_phases + 1) * cus * 8, dtype=torch.int64, device=dev)
@@ -1007,9 +1009,10 @@ def main():
 
     # the same sweep as one chained GEMV program (include/q4chain.h): one
     # launch, a grid barrier between phases, each phase's first weights
-    # requested before its barrier (and its x quantised there too, since
-    # every phase of the sweep reads an x from outside the program, as the
-    # reference's per-shape calls do).  It is the headline unless a barrier
+    # requested before its barrier.  Every phase of the sweep reads an x from
+    # outside the program, as the reference's per-shape calls do, so each
+    # phase's x is quantised once at the program's start (one workgroup per
+    # phase) and only copied into LDS before its barrier.  It is the headline unless a barrier
     # wait timed out (then its outputs are not to be trusted and the grouped
     # launches give the figure).
     chained = None
@@ -1091,8 +1094,9 @@ def main():
                     "kernel": "gemv_chain_kernel: the whole sweep as one launch of 113 phases",
                     "avg_launch_us": round(chain_ev * 1e3, 3)}
         path = ("one chained GEMV program per step (include/q4chain.h): 113 phases in one persistent "
-                "launch, a grid barrier between phases; each phase's first weights and its x (read from "
-                "outside the program) loaded before its barrier")
+                "launch, a grid barrier between phases; each phase's x (read from outside the program) "
+                "quantised once at the program's start; each phase's first weights and its prepared x "
+                "loaded before its barrier")
         launches = 1
     else:
         achieved = grouped_achieved

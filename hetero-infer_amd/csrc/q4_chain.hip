@@ -26,9 +26,15 @@
 // signals a barrier after which a phase reads (or writes over) what an
 // earlier phase stored, each of its waves has waited for its own stores.
 // x that the phase just before does not write is loaded, and its prologue
-// run, before the barrier, as the weights are.
+// run, before the barrier, as the weights are.  x that no phase writes is
+// prepared at the program's start: one workgroup per such phase runs the
+// phase's x prologue and stores the int16 planes, group sums and scale
+// (device scope); after one more grid barrier the phase only copies them
+// into LDS.  The last workgroup to reach a barrier then starts its stream
+// after a copy instead of a whole prologue.
 #include <hip/hip_runtime.h>
 
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -68,7 +74,22 @@ struct ChainPhase {
     int x_early;     // the phase before does not write x: x and its prologue before the barrier (ring 2)
     int x_cached;    // no phase writes x: x loaded through the L2
     int ack_stores;  // every wave's stores complete before the arrival at the next barrier
+    const uint4* prep;   // x prepared at the program's start (prep_bytes), or null
 };
+
+using v4u32 = unsigned int __attribute__((__vector_size__(16)));
+
+// How a phase gets its x planes: loaded and quantised after its barrier, or
+// before it (the phase before does not write x), or prepared once at the
+// program's start (no phase writes x) and only copied into LDS.
+constexpr int kXLate = 0, kXEarly = 1, kXPrep = 2;
+
+// A prepared x: the int16 planes in the LDS layout ([C][256] words of 16
+// bytes, swizzled as the prologue stores them), the group sums [Gr] and the
+// x scale, padded to 256 bytes.
+__host__ __device__ constexpr size_t prep_bytes(int C, int Gr) {
+    return (static_cast<size_t>(C) * 256 * 16 + static_cast<size_t>(Gr) * 4 + 16 + 255) & ~static_cast<size_t>(255);
+}
 
 // Barrier state, every word on its own 128-byte line.  Zero between launches:
 // the last workgroup to leave resets it.
@@ -187,14 +208,142 @@ __device__ __forceinline__ void chain_wait(ChainSync* s, unsigned k, int* failed
     lds_barrier();
 }
 
+// Thread t's words t, t + nt, t + 2nt of x (8 floats each), device-scope
+// loads unless no phase of the program writes x (cached).
+__device__ __forceinline__ void chain_load_x(float4 (&wv)[kChainRounds][2], const float* x, int n_in, bool cached) {
+    constexpr int nt = 64 * kChainWaves;
+    const int wpr = n_in >> 3;
+    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(n_in) * 4u);
+#pragma unroll
+    for (int r = 0; r < kChainRounds; r++) {
+        const int j = r * nt + threadIdx.x;
+        const uint32_t off = j < wpr ? static_cast<uint32_t>(8 * j) * 4u : kOutOfRange;
+        if (cached) {
+            wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            wv[r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
+        } else {
+            wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kStoreDevice));
+            wv[r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, kStoreDevice));
+        }
+    }
+}
+
+// The x prologue's first half, as the streaming kernel's: the unit counter
+// zeroed, x staged in LDS, max |x| per wave (kernel/q4gemv.c:258-259) and,
+// after a barrier, the group sums in ascending order (:244-248), one lane
+// per group.
+__device__ __forceinline__ void chain_sums(const float4 (&wv)[kChainRounds][2], int wpr, int G, float* xsum_lds,
+                                           float* red, float* xstage, int* claim_ctr, unsigned long long* stamps,
+                                           unsigned long long* st) {
+    constexpr int WPG = 8;                                        // packed words per group
+    constexpr int nt = 64 * kChainWaves;
+    constexpr int SS = stage_stride(0);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (tid == 0) *claim_ctr = 0;
+    float amax = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kChainRounds; r++) {
+        if (r * nt + wave * 64 < wpr) {                           // uniform: the wave has words this round
+            const float4 a = wv[r][0], b = wv[r][1];
+            amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                     fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+            const int j = r * nt + tid;
+            if (j < wpr) {
+                float4* dst = reinterpret_cast<float4*>(xstage + (j / WPG) * SS + (j % WPG) * 8);
+                dst[0] = a;
+                dst[1] = b;
+            }
+        }
+    }
+    amax = wave_max(amax);
+    if (lane == 0) red[wave] = amax;
+    __syncthreads();
+    chain_event(stamps, st, 3);
+    for (int g = tid; g < G; g += nt)
+        xsum_lds[g] = chain_add<32>(chain_add<32>(0.0f, xstage + g * SS), xstage + g * SS + 32);
+}
+
+// The second half: the x scale (kernel/q4gemv.c:260-261) and int16 x
+// (:262-270) as byte planes in LDS, word j of chunk c at
+// c*256 + (j%4)*64 + (j%256)/4.  Returns the x scale.
+__device__ __forceinline__ float chain_quant(const float4 (&wv)[kChainRounds][2], int wpr, int C, const float* red,
+                                             uint4* xpl) {
+    constexpr int nt = 64 * kChainWaves;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float a = 0.0f;
+    for (int i = 0; i < kChainWaves; i++) a = fmaxf(a, red[i]);
+    const float xsc = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;   // kernel/q4gemv.c:260
+    const float inv = __fdiv_rn(1.0f, xsc);                        // :261
+    const bool exact_clamp = __builtin_isinf(inv);
+#pragma unroll
+    for (int r = 0; r < kChainRounds; r++) {
+        const int j = r * nt + tid;
+        if (r * nt + wave * 64 < C * kChunkWords) {               // uniform
+            uint4 pl = make_uint4(0, 0, 0, 0);
+            if (r * nt + wave * 64 < wpr) {                       // uniform
+                const float vv[8] = {wv[r][0].x, wv[r][0].y, wv[r][0].z, wv[r][0].w,
+                                     wv[r][1].x, wv[r][1].y, wv[r][1].z, wv[r][1].w};
+                pl = exact_clamp ? quant_word(vv, inv, true) : quant_word(vv, inv, false);
+                if (j >= wpr) pl = make_uint4(0, 0, 0, 0);
+            }
+            const int cc = j >> 8, jj = j & 255;
+            xpl[cc * 256 + (jj & 3) * 64 + (jj >> 2)] = pl;
+        }
+    }
+    return xsc;
+}
+
+// The program's first stage: phase ph's x through the whole prologue (as
+// the phase itself would run it), then its planes, group sums and scale
+// stored to ph->prep at device scope.  Every phase that reads it copies them
+// after the barrier that ends this stage.
+__device__ __forceinline__ void chain_prepare(CPhase* ph, uint4* lds4) {
+    constexpr int nt = 64 * kChainWaves;
+    const int n_in = ph->n_in;
+    const int wpr = n_in >> 3, G = n_in >> 6;
+    const int C = (wpr + kChunkWords - 1) / kChunkWords;
+    const int Gr = (G + 3) & ~3;
+    const int NU = ph->pair ? 2 * ph->UB : ph->UB;
+    float* xsum_lds = reinterpret_cast<float*>(lds4);
+    float* red = xsum_lds + Gr;
+    int* claim_ctr = reinterpret_cast<int*>(red + 16);
+    uint4* xpl = reinterpret_cast<uint4*>(red + 16 + 4 + 16);
+    const bool sep = ph->sep_stage;
+    float* xstage = sep ? reinterpret_cast<float*>(xpl + C * 256) + kChainWaves * NU * kTermStride
+                        : reinterpret_cast<float*>(xpl);
+    float4 wv[kChainRounds][2];
+    chain_load_x(wv, ph->x, n_in, ph->x_cached);
+    chain_sums(wv, wpr, G, xsum_lds, red, xstage, claim_ctr, nullptr, nullptr);
+    if (!sep) __syncthreads();
+    const float xsc = chain_quant(wv, wpr, C, red, xpl);
+    __syncthreads();
+    const int tid = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t sr = buf_rsrc(ph->prep, static_cast<uint32_t>(prep_bytes(C, Gr)));
+    for (int i = tid; i < C * 256; i += nt)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4u32, xpl[i]), sr, static_cast<uint32_t>(i) * 16u,
+                                               0, kStoreDevice);
+    if (tid < Gr / 4)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(v4u32, reinterpret_cast<const float4*>(xsum_lds)[tid]), sr,
+            static_cast<uint32_t>(C * 256 * 16 + tid * 16), 0, kStoreDevice);
+    if (tid == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, xsc), sr,
+                                              static_cast<uint32_t>(C * 256 * 16 + Gr * 4), 0, kStoreDevice);
+    __syncthreads();                                              // the LDS is read: the next user may write it
+}
+
 // One phase.  The body follows gemv_stream_kernel<1, RW, PAIR, RING, false, 0>
 // (q4_stream.h) step for step; the differences: the whole first ring is
 // issued before the barrier and the x loads, x is loaded and the outputs
 // stored at device scope, the rounds of x words are guarded at run time,
 // and the phase ends with the waves' stores complete and the workgroup's
-// arrival at the next barrier.
-template <int RING, bool PAIR, bool EARLY>
-__device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
+// arrival at the next barrier.  Barrier k is the k-th arrival of every
+// workgroup: base (1 when the program starts with a preparation stage, else
+// 0) plus the phases before.
+template <int RING, bool PAIR, int XM>
+__device__ __forceinline__ void chain_phase(CPhase* ph, int p, int base, ChainSync* sync,
                                             int* failed, uint4* lds4, bool arrive_after,
                                             unsigned long long* stamps, unsigned long long* st) {
     constexpr int lpg = 2;                                        // lanes per group in an item
@@ -233,33 +382,38 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
     const int first_unit = blockIdx.x + wave * grid;
     const bool has_work = first_unit < n_units;                   // uniform
 
-    // ---- 1. x, first when the phase before does not write it (EARLY):
+    // ---- 1. x, first when the phase before does not write it (kXEarly):
     //         then x does not depend on that phase either, and its loads
     //         and the whole prologue run before the barrier as the weights'
     //         do.  x loads are the wave's oldest then, so the prologue waits
     //         for them alone, not for the weights issued after them (a code
     //         path of its own: one shared with the other order would wait
-    //         for both).  Thread t owns words t, t + nt, t + 2nt; device-scope
-    //         loads unless no phase of the program writes x (x_cached).
-    const __amdgpu_buffer_rsrc_t xr = buf_rsrc(x, static_cast<uint32_t>(n_in) * 4u);
+    //         for both).  A prepared x (kXPrep) is loaded the same way, as
+    //         its planes, group sums and scale; phase 0 first waits for the
+    //         stage that prepared it.
     float4 wv[kChainRounds][2];
-    auto load_x = [&]() {
-        const bool cached = ph->x_cached;                         // uniform
+    uint4 pv[kChainRounds];
+    float4 gv;
+    float xsc_v;
+    if constexpr (XM == kXEarly) chain_load_x(wv, x, n_in, ph->x_cached);
+    if constexpr (XM == kXPrep) {
+        if (p == 0) {
+            chain_wait(sync, static_cast<unsigned>(base), failed);
+            chain_event(stamps, st, 2);
+        }
+        const int n_pl = C * 256;
+        const __amdgpu_buffer_rsrc_t sr = buf_rsrc(ph->prep, static_cast<uint32_t>(prep_bytes(C, Gr)));
 #pragma unroll
         for (int r = 0; r < kChainRounds; r++) {
             const int j = r * nt + tid;
-            const uint32_t off = j < wpr ? static_cast<uint32_t>(8 * j) * 4u : kOutOfRange;
-            if (cached) {
-                wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
-                wv[r][1] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0));
-            } else {
-                wv[r][0] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, kStoreDevice));
-                wv[r][1] = __builtin_bit_cast(float4,
-                                              __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, kStoreDevice));
-            }
+            const uint32_t off = j < n_pl ? static_cast<uint32_t>(j) * 16u : kOutOfRange;
+            pv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, kStoreDevice));
         }
-    };
-    if constexpr (EARLY) load_x();
+        const uint32_t goff = tid < Gr / 4 ? static_cast<uint32_t>(n_pl * 16 + tid * 16) : kOutOfRange;
+        gv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(sr, goff, 0, kStoreDevice));
+        xsc_v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              sr, static_cast<uint32_t>(n_pl * 16 + Gr * 4), 0, kStoreDevice));
+    }
 
     // ---- 2. the first ring of this phase: weights only, no dependency
     Item ring[RING];
@@ -275,80 +429,42 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
 
     // ---- 3. otherwise every workgroup must be done with the phase before
     //         (x is one of its outputs) before x is loaded
-    if constexpr (!EARLY) {
-        if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
+    if constexpr (XM == kXLate) {
+        if (p > 0) chain_wait(sync, static_cast<unsigned>(p + base), failed);
         chain_event(stamps, st, 2);
-        load_x();
+        chain_load_x(wv, x, n_in, ph->x_cached);
     }
 
     // ---- 4. the x prologue (the unit counter is free again: every wave of
     //         the workgroup is past the phase before)
-    if (tid == 0) *claim_ctr = 0;
-    // group sums in ascending order (kernel/q4gemv.c:244-248) and max |x|
-    // (:258-259), as the streaming kernel computes them
-    {
-        constexpr int SS = stage_stride(0);
-        float amax = 0.0f;
-#pragma unroll
-        for (int r = 0; r < kChainRounds; r++) {
-            if (r * nt + wave * 64 < wpr) {                       // uniform: the wave has words this round
-                const float4 a = wv[r][0], b = wv[r][1];
-                amax = fmaxf(amax, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
-                                         fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
-                const int j = r * nt + tid;
-                if (j < wpr) {
-                    float4* dst = reinterpret_cast<float4*>(xstage + (j / WPG) * SS + (j % WPG) * 8);
-                    dst[0] = a;
-                    dst[1] = b;
-                }
-            }
-        }
-        amax = wave_max(amax);
-        if (lane == 0) red[wave] = amax;
-        __syncthreads();
-        chain_event(stamps, st, 3);
-        // one lane per group adds its 64 values in ascending order
-        for (int g = tid; g < G; g += nt)
-            xsum_lds[g] = chain_add<32>(chain_add<32>(0.0f, xstage + g * SS), xstage + g * SS + 32);
-    }
-    if (!sep) __syncthreads();                                    // the staging is read: the planes may overwrite it
-
     auto claim = [&]() -> int {
         int v = 0;
         if (lane == 0) v = __hip_atomic_fetch_add(claim_ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         return v + nwaves;                                        // lane 0's value counts
     };
-    int claimed = claim();
-
-    // int16 x (kernel/q4gemv.c:260-270) as byte planes in LDS
+    int claimed;
     float xsc;
-    {
-        float a = 0.0f;
-        for (int i = 0; i < nwaves; i++) a = fmaxf(a, red[i]);
-        xsc = a > 0.0f ? __fdiv_rn(a, 32767.0f) : 1.0f;           // kernel/q4gemv.c:260
-        const float inv = __fdiv_rn(1.0f, xsc);                    // :261
-        const bool exact_clamp = __builtin_isinf(inv);
+    if constexpr (XM == kXPrep) {
+        if (tid == 0) *claim_ctr = 0;
 #pragma unroll
-        for (int r = 0; r < kChainRounds; r++) {
-            const int j = r * nt + tid;
-            if (r * nt + wave * 64 < C * kChunkWords) {           // uniform
-                uint4 pl = make_uint4(0, 0, 0, 0);
-                if (r * nt + wave * 64 < wpr) {                   // uniform
-                    const float vv[8] = {wv[r][0].x, wv[r][0].y, wv[r][0].z, wv[r][0].w,
-                                         wv[r][1].x, wv[r][1].y, wv[r][1].z, wv[r][1].w};
-                    pl = exact_clamp ? quant_word(vv, inv, true) : quant_word(vv, inv, false);
-                    if (j >= wpr) pl = make_uint4(0, 0, 0, 0);
-                }
-                const int cc = j >> 8, jj = j & 255;
-                xpl[cc * 256 + (jj & 3) * 64 + (jj >> 2)] = pl;
-            }
-        }
+        for (int r = 0; r < kChainRounds; r++)
+            if (r * nt + wave * 64 < C * 256) xpl[r * nt + tid] = pv[r];   // uniform: 256 words per chunk
+        if (tid < Gr / 4) reinterpret_cast<float4*>(xsum_lds)[tid] = gv;
+        xsc = xsc_v;
+        __syncthreads();
+        chain_event(stamps, st, 3);
+        claimed = claim();
+    } else {
+        chain_sums(wv, wpr, G, xsum_lds, red, xstage, claim_ctr, stamps, st);
+        if (!sep) __syncthreads();                                // the staging is read: the planes may overwrite it
+        claimed = claim();
+        xsc = chain_quant(wv, wpr, C, red, xpl);
+        __syncthreads();
     }
-    __syncthreads();
     chain_event(stamps, st, 4);
-    if constexpr (EARLY) {
-        if (p > 0) chain_wait(sync, static_cast<unsigned>(p), failed);
-        chain_event(stamps, st, 2);
+    if constexpr (XM != kXLate) {
+        if (p > 0) chain_wait(sync, static_cast<unsigned>(p + base), failed);
+        if (XM == kXEarly || p > 0) chain_event(stamps, st, 2);
     }
 
     // ---- 5. the item stream (as gemv_stream_kernel)
@@ -490,7 +606,8 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, ChainSync* sync,
 }
 
 __global__ __launch_bounds__(64 * kChainWaves) void gemv_chain_kernel(const ChainPhase* __restrict__ phases,
-                                                                      int n_phases, ChainSync* __restrict__ sync,
+                                                                      int n_phases, int prepare,
+                                                                      ChainSync* __restrict__ sync,
                                                                       unsigned long long* __restrict__ stamps) {
     extern __shared__ uint4 lds_all[];
     int* failed = reinterpret_cast<int*>(lds_all);               // read and written by thread 0 only
@@ -498,23 +615,39 @@ __global__ __launch_bounds__(64 * kChainWaves) void gemv_chain_kernel(const Chai
     uint4* lds4 = lds_all + kChainLdsHead / 16;
     if (threadIdx.x == 0) *failed = 0;
     CPhase* table = (CPhase*)phases;
+    // the preparation stage: workgroup b prepares the x of phases b, b + grid,
+    // ... that take a prepared x, then arrives at barrier 1
+    int base = 0;
+    if (prepare) {
+        for (int q = blockIdx.x; q < n_phases; q += gridDim.x)
+            if (table[q].prep) chain_prepare(table + q, lds4);
+        wait_own_stores();
+        lds_barrier();
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(&sync->group[blockIdx.x / kChainGroup][0], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        base = 1;
+    }
     for (int p = 0; p < n_phases; p++) {
         CPhase* ph = table + p;
-        const int pair = ph->pair, ring = ph->ring, early = ph->x_early;   // uniform
+        const int pair = ph->pair, ring = ph->ring;                  // uniform
+        const int xm = ph->prep ? kXPrep : ph->x_early ? kXEarly : kXLate;
         const bool arrive = p + 1 < n_phases;
         if (pair) {
-            if (ring == 4) chain_phase<4, true, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
-            else if (early) chain_phase<2, true, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
-            else chain_phase<2, true, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            if (ring == 4) chain_phase<4, true, kXLate>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
+            else if (xm == kXPrep) chain_phase<2, true, kXPrep>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
+            else if (xm == kXEarly) chain_phase<2, true, kXEarly>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
+            else chain_phase<2, true, kXLate>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 1) {
-            chain_phase<1, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            chain_phase<1, false, kXLate>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 2) {
-            if (early) chain_phase<2, false, true>(ph, p, sync, failed, lds4, arrive, stamps, st);
-            else chain_phase<2, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            if (xm == kXPrep) chain_phase<2, false, kXPrep>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
+            else if (xm == kXEarly) chain_phase<2, false, kXEarly>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
+            else chain_phase<2, false, kXLate>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
         } else if (ring == 4) {
-            chain_phase<4, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            chain_phase<4, false, kXLate>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
         } else {
-            chain_phase<5, false, false>(ph, p, sync, failed, lds4, arrive, stamps, st);
+            chain_phase<5, false, kXLate>(ph, p, base, sync, failed, lds4, arrive, stamps, st);
         }
     }
     // every workgroup is past its last barrier wait once it gets here; the
@@ -538,9 +671,11 @@ struct q4_chain_plan {
     int n_phases = 0;
     int grid = 0;
     size_t lds = 0;
+    int prepare = 0;             // phases with a prepared x: the program starts with their preparation
     unsigned long long* stamps = nullptr;
     ChainPhase* d_phases = nullptr;
     ChainSync* d_sync = nullptr;
+    void* d_prep = nullptr;      // the prepared x of those phases
 };
 
 namespace {
@@ -695,6 +830,16 @@ int q4_chain_create(const q4_chain_phase* phases, int n_phases, q4_chain_plan** 
     }
     if (lds > kStreamLdsMax) return fail(Q4_EARG, "phases need %zu bytes of LDS", lds);
     plan_dependencies(phases, host);
+    // an x that no phase writes is prepared once, at the program's start, by
+    // one workgroup per phase (ring-2 phases: the code path exists for those)
+    std::vector<size_t> prep_off(n_phases, SIZE_MAX);
+    size_t prep_total = 0;
+    for (int p = 0; p < n_phases; p++) {
+        if (!host[p].x_cached || host[p].ring != 2) continue;
+        const int wpr = host[p].n_in / 8, G = host[p].n_in / 64;
+        prep_off[p] = prep_total;
+        prep_total += prep_bytes((wpr + kChunkWords - 1) / kChunkWords, (G + 3) & ~3);
+    }
     static std::atomic<uint64_t> lds_raised{0};
     if (int rc = raise_lds_limit(reinterpret_cast<const void*>(gemv_chain_kernel), kStreamLdsMax, lds_raised))
         return rc;
@@ -709,12 +854,20 @@ int q4_chain_create(const q4_chain_phase* phases, int n_phases, q4_chain_plan** 
     pl->lds = lds;
     e = hipMalloc(&pl->d_phases, sizeof(ChainPhase) * n_phases);
     if (e == hipSuccess) e = hipMalloc(&pl->d_sync, sizeof(ChainSync));
+    if (e == hipSuccess && prep_total) e = hipMalloc(&pl->d_prep, prep_total);
+    if (e == hipSuccess && prep_total) {
+        pl->prepare = 1;
+        for (int p = 0; p < n_phases; p++)
+            if (prep_off[p] != SIZE_MAX)
+                host[p].prep = reinterpret_cast<const uint4*>(static_cast<char*>(pl->d_prep) + prep_off[p]);
+    }
     if (e == hipSuccess) e = hipMemcpy(pl->d_phases, host.data(), sizeof(ChainPhase) * n_phases, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemset(pl->d_sync, 0, sizeof(ChainSync));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         hipFree(pl->d_phases);
         hipFree(pl->d_sync);
+        hipFree(pl->d_prep);
         delete pl;
         return fail(e == hipErrorOutOfMemory ? Q4_ENOMEM : Q4_EHIP, "chain plan: %s", hipGetErrorString(e));
     }
@@ -728,7 +881,8 @@ int q4_chain_run(q4_chain_plan* plan, void* stream) {
     hipGetDevice(&dev);
     if (dev != plan->device) return fail(Q4_EARG, "plan made on device %d, current device %d", plan->device, dev);
     hipLaunchKernelGGL(gemv_chain_kernel, dim3(plan->grid), dim3(64 * kChainWaves), plan->lds,
-                       static_cast<hipStream_t>(stream), plan->d_phases, plan->n_phases, plan->d_sync, plan->stamps);
+                       static_cast<hipStream_t>(stream), plan->d_phases, plan->n_phases, plan->prepare, plan->d_sync,
+                       plan->stamps);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(Q4_EHIP, "chain launch: %s", hipGetErrorString(e));
     return 0;
@@ -759,6 +913,7 @@ int q4_chain_destroy(q4_chain_plan* plan) {
     hipDeviceSynchronize();
     hipFree(plan->d_phases);
     hipFree(plan->d_sync);
+    hipFree(plan->d_prep);
     delete plan;
     return 0;
 }

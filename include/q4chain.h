@@ -13,11 +13,17 @@
  * weight loads of the next phase before it waits for that dependency, so the
  * weight stream does not pause at each one; an x that phase p-1 does not
  * write (found from the pointers at q4_chain_create) is loaded and
- * quantised before the wait too.  A phase's outputs must not overlap its
- * own x (Q4_EARG).
+ * quantised before the wait too.  An x that no phase writes is quantised
+ * once per phase at the program's start (its int16 planes, group sums and
+ * scale, computed as the phase's own prologue computes them, into memory
+ * the plan holds), and the phase only copies them, before its wait.  So x
+ * must not change while the program runs, which no phase can do.  A
+ * phase's outputs must not overlap its own x (Q4_EARG).
  *
  * All pointers are device pointers on the device current at q4_chain_create.
- * A plan holds its phase table and barrier state in device memory; it runs
+ * A plan holds its phase table, barrier state and the prepared x in device
+ * memory (2 bytes per x element of each such phase, n_in rounded up to a
+ * multiple of 2048, plus 4 per group); it runs
  * asynchronously on `stream` (a hipStream_t, NULL = the null stream), makes
  * no allocation or memset when it runs, and can be captured in a HIP graph.
  * One plan must not run on two streams at once (its barrier state is shared).
@@ -66,8 +72,9 @@ int q4_chain_run(q4_chain_plan *plan, void *stream);
  * (s_memrealtime) at stamps[(p * workgroups + b) * 8 + e] for the events
  * e = 1: the workgroup done with phase p - 1, arriving at the grid barrier
  * (every wave's stores complete when a later phase depends on them); 2: the
- * barrier released; 3: p's x staged in LDS; 4: p's int16 planes ready (3 and
- * 4 come before 2 when phase p - 1 does not write p's x); 5: wave 0 done with
+ * barrier released; 3: p's x staged in LDS (a prepared x: its planes, group
+ * sums and scale copied into LDS); 4: p's int16 planes ready (3 and 4 come
+ * before 2 when phase p - 1 does not write p's x); 5: wave 0 done with
  * its items of p (row n_phases holds event 1 only: the end).  NULL stops
  * recording.  Returns Q4_EARG when `words` is too small. */
 int q4_chain_stamps(q4_chain_plan *plan, unsigned long long *stamps, long words);
