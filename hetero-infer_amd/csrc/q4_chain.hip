@@ -401,18 +401,23 @@ __device__ __forceinline__ void chain_phase(CPhase* ph, int p, int base, ChainSy
             chain_wait(sync, static_cast<unsigned>(base), failed);
             chain_event(stamps, st, 2);
         }
+        // through the L2: the stage before the barrier wrote the prepared x
+        // at device scope, and no L2 holds a line of it from before (none is
+        // read before that barrier, and the launch starts with the L2s
+        // coherent), so the first workgroup of an XCD fetches it and the
+        // others hit
         const int n_pl = C * 256;
         const __amdgpu_buffer_rsrc_t sr = buf_rsrc(ph->prep, static_cast<uint32_t>(prep_bytes(C, Gr)));
 #pragma unroll
         for (int r = 0; r < kChainRounds; r++) {
             const int j = r * nt + tid;
             const uint32_t off = j < n_pl ? static_cast<uint32_t>(j) * 16u : kOutOfRange;
-            pv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, kStoreDevice));
+            pv[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, 0));
         }
         const uint32_t goff = tid < Gr / 4 ? static_cast<uint32_t>(n_pl * 16 + tid * 16) : kOutOfRange;
-        gv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(sr, goff, 0, kStoreDevice));
+        gv = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(sr, goff, 0, 0));
         xsc_v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                              sr, static_cast<uint32_t>(n_pl * 16 + Gr * 4), 0, kStoreDevice));
+                                              sr, static_cast<uint32_t>(n_pl * 16 + Gr * 4), 0, 0));
     }
 
     // ---- 2. the first ring of this phase: weights only, no dependency
