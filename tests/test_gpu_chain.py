@@ -301,3 +301,29 @@ def test_inputs_change_between_runs():
         torch.cuda.synchronize()
         check(f"replay {r}")
     ch.close()
+
+
+@pytest.mark.parametrize("n_in,n_out,phases", [(64, 300, 1), (24576, 700, 1), (24576, 700, 2), (64, 40, 3)])
+def test_prepared_x_edges(n_in, n_out, phases):
+    """Programs of one to three phases whose x is prepared at the program's
+    start, at the smallest and largest n_in (one group; 12 chunks of planes,
+    the most a prepared x holds): with one phase the preparation stage's
+    barrier is the program's only one.  Every phase bit-exact against the
+    oracle and bit-identical to its own launch, on two runs."""
+    import torch
+    o = oracle.Oracle()
+    mats = [mat(1500 + n_in % 97 + p, n_out, n_in) for p in range(phases)]
+    x = synth.activations(1501 + n_in % 89, 1, n_in)
+    tx = dev(x)[0]
+    outs = [torch.full((1, n_out), float("nan"), device="cuda") for _ in range(phases)]
+    ch = q4.Chain([([m[1]], tx, [outs[p]], False) for p, m in enumerate(mats)])
+    for r in range(2):
+        for t in outs:
+            t.fill_(float("nan"))
+        ch.run()
+        torch.cuda.synchronize()
+        assert ch.errors() == 0
+        for p, (m, got) in enumerate(zip(mats, outs)):
+            assert np.array_equal(bits(got)[0], o.gemv(*m[0], x[0], 64).view(np.uint32)), f"run {r} phase {p}"
+            assert np.array_equal(bits(got), bits(q4.gemv_dev(*m[1], tx))), f"run {r} phase {p} vs launch"
+    ch.close()
