@@ -852,8 +852,11 @@ int q4_chain_create(const q4_chain_phase* phases, int n_phases, q4_chain_plan** 
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_chain_kernel, 64 * kChainWaves, lds);
     if (e != hipSuccess || per_cu < 1)
         return fail(Q4_EHIP, "the chained kernel does not fit a CU (%s)", hipGetErrorString(e));
+    int device = 0;
+    e = hipGetDevice(&device);
+    if (e != hipSuccess) return fail(Q4_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
     auto* pl = new q4_chain_plan;
-    hipGetDevice(&pl->device);
+    pl->device = device;
     pl->n_phases = n_phases;
     pl->grid = cus;
     pl->lds = lds;
@@ -870,9 +873,9 @@ int q4_chain_create(const q4_chain_phase* phases, int n_phases, q4_chain_plan** 
     if (e == hipSuccess) e = hipMemset(pl->d_sync, 0, sizeof(ChainSync));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
-        hipFree(pl->d_phases);
-        hipFree(pl->d_sync);
-        hipFree(pl->d_prep);
+        (void)hipFree(pl->d_phases);
+        (void)hipFree(pl->d_sync);
+        (void)hipFree(pl->d_prep);
         delete pl;
         return fail(e == hipErrorOutOfMemory ? Q4_ENOMEM : Q4_EHIP, "chain plan: %s", hipGetErrorString(e));
     }
@@ -883,7 +886,7 @@ int q4_chain_create(const q4_chain_phase* phases, int n_phases, q4_chain_plan** 
 int q4_chain_run(q4_chain_plan* plan, void* stream) {
     if (!plan) return fail(Q4_EARG, "null plan");
     int dev = 0;
-    hipGetDevice(&dev);
+    if (hipGetDevice(&dev) != hipSuccess) return fail(Q4_EHIP, "hipGetDevice failed");
     if (dev != plan->device) return fail(Q4_EARG, "plan made on device %d, current device %d", plan->device, dev);
     hipLaunchKernelGGL(gemv_chain_kernel, dim3(plan->grid), dim3(64 * kChainWaves), plan->lds,
                        static_cast<hipStream_t>(stream), plan->d_phases, plan->n_phases, plan->prepare, plan->d_sync,
@@ -915,11 +918,14 @@ int q4_chain_errors(q4_chain_plan* plan) {
 
 int q4_chain_destroy(q4_chain_plan* plan) {
     if (!plan) return 0;
-    hipDeviceSynchronize();
-    hipFree(plan->d_phases);
-    hipFree(plan->d_sync);
-    hipFree(plan->d_prep);
+    // free everything whatever fails; report the first failure
+    hipError_t e = hipDeviceSynchronize();
+    for (void* ptr : {static_cast<void*>(plan->d_phases), static_cast<void*>(plan->d_sync), plan->d_prep}) {
+        const hipError_t f = hipFree(ptr);
+        if (e == hipSuccess) e = f;
+    }
     delete plan;
+    if (e != hipSuccess) return fail(Q4_EHIP, "chain destroy: %s", hipGetErrorString(e));
     return 0;
 }
 
