@@ -565,8 +565,9 @@ class Chain:
 
     def close(self):
         if self._plan:
-            self.lib.q4_chain_destroy(self._plan)
-            self._plan = _VP()
+            plan, self._plan = self._plan, _VP()
+            self._keep = []
+            check(self.lib, self.lib.q4_chain_destroy(plan), "q4_chain_destroy")
         self._keep = []
 
     def __del__(self):
