@@ -327,3 +327,37 @@ def test_prepared_x_edges(n_in, n_out, phases):
             assert np.array_equal(bits(got)[0], o.gemv(*m[0], x[0], 64).view(np.uint32)), f"run {r} phase {p}"
             assert np.array_equal(bits(got), bits(q4.gemv_dev(*m[1], tx))), f"run {r} phase {p} vs launch"
     ch.close()
+
+
+def test_stamps_leave_outputs_unchanged():
+    """Event stamps on (q4_chain_stamps) in a program with prepared x, an x
+    from the phase before and an x from two phases back: outputs
+    bit-identical to the run without stamps, and every workgroup's events
+    of a phase in order (arrival before release, x staged before planes
+    ready, planes before wave 0 is done)."""
+    import torch
+    n = 3584
+    mats = [mat(1600 + i, n, n)[1] for i in range(4)]
+    x = dev(synth.activations(1601, 1, n))[0]
+    a, b, c, d = (torch.empty((1, n), device="cuda") for _ in range(4))
+    ch = q4.Chain([([mats[0]], x, [a], False), ([mats[1]], a, [b], False),
+                   ([mats[2]], x, [c], False), ([mats[3]], b, [d], False)])
+    ch.run()
+    torch.cuda.synchronize()
+    want = [bits(t) for t in (a, b, c, d)]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    buf = torch.zeros(5 * cus * 8, dtype=torch.int64, device="cuda")
+    ch.stamps(buf)
+    for t in (a, b, c, d):
+        t.fill_(float("nan"))
+    ch.run()
+    torch.cuda.synchronize()
+    ch.stamps(None)
+    assert ch.errors() == 0
+    assert all(np.array_equal(bits(t), w) for t, w in zip((a, b, c, d), want))
+    ev = buf.cpu().numpy().reshape(5, cus, 8)
+    for p in range(1, 4):
+        arrived, released, staged, planes, done = (ev[p, :, e] for e in range(1, 6))
+        assert (released.min() >= arrived.max() - 1), f"phase {p}: released before the last arrival"
+        assert (staged <= planes).all() and (planes <= done).all(), f"phase {p}: events out of order"
+    ch.close()
